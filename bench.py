@@ -1,0 +1,315 @@
+"""Benchmark of the CSR SpMV / SpMM hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu]
+
+A step is one pass of the hot path over one synthetic input: one SpMV
+y = A x (or one SpMM C = A B) through the public operator API with the
+matrix prepared once (analysis / transpose outside the timed region, as
+the reference's prepare_* APIs do).  Inputs are generated on the GPU from
+a fixed seed and resident in HBM before timing starts.
+
+Default workload: BASELINE config 2 (27-point stencil SpMV, 128^3 grid,
+fp64 / int32).  The line reports effective algorithmic HBM GB/s (bytes =
+values + col indices + row pointer + x (or B) once + y (or C) once) and
+its fraction of the 8 TB/s HBM3E peak, GFLOP/s, the dominant kernel's
+roofline entry timed with HIP events on the launch stream, and the
+reference CPU path (scipy CSR product, 1 thread) on the same matrix.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "effective HBM GB/s (% of peak) + GFLOP/s for CSR SpMV/SpMM, 1 MI355X"
+
+CONFIGS = {
+    "c2_spmv_stencil128_f64_i32": dict(op_kind="spmv", gen="stencil", dtype="f64", index="i32", op="non"),
+    "c1_spmv_uniform4096_f32_i32": dict(op_kind="spmv", gen="uniform4096", dtype="f32", index="i32", op="non"),
+    "c3_spmv_powerlaw4M_f32_i32": dict(op_kind="spmv", gen="powerlaw", dtype="f32", index="i32", op="non"),
+    "c3_spmv_powerlaw4M_f32_i64": dict(op_kind="spmv", gen="powerlaw", dtype="f32", index="i64", op="non"),
+    "c4_spmm_uniform1M_f32_i32_n64_non": dict(op_kind="spmm", gen="uniform1M", dtype="f32", index="i32", op="non", n=64),
+    "c4_spmm_uniform1M_f32_i32_n64_trans": dict(op_kind="spmm", gen="uniform1M", dtype="f32", index="i32", op="trans",
+                                                n=64),
+    "c5_spmm_rmat21_f32_i64_n256_non": dict(op_kind="spmm", gen="rmat", dtype="f32", index="i64", op="non", n=256),
+    "c5_spmm_rmat21_c64_i64_n32_conj": dict(op_kind="spmm", gen="rmat", dtype="c64", index="i64", op="conj", n=32),
+}
+DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
+
+
+def _dtypes(torch):
+    return (
+        {"f32": torch.float32, "f64": torch.float64, "c64": torch.complex64, "c128": torch.complex128},
+        {"i32": torch.int32, "i64": torch.int64},
+    )
+
+
+def generate(cfg, device):
+    import torch
+
+    from flagsparse_amd import synthetic as S
+
+    vt, it = _dtypes(torch)
+    dtype, idx = vt[cfg["dtype"]], it[cfg["index"]]
+    g = cfg["gen"]
+    if g == "stencil":
+        return S.stencil27(128, dtype, idx, device, seed=2)
+    if g == "uniform4096":
+        return S.uniform_rows(4096, 4096, 16, dtype, idx, device, seed=1)
+    if g == "powerlaw":
+        return S.powerlaw(4194304, dtype, idx, device, seed=3)
+    if g == "uniform1M":
+        return S.uniform_rows(1 << 20, 1 << 20, 32, dtype, idx, device, seed=5)
+    if g == "rmat":
+        return S.rmat(21, dtype=dtype, index_dtype=idx, device=device, seed=7)
+    raise ValueError(g)
+
+
+def elem_bytes(t):
+    return t.element_size()
+
+
+def time_loop(fn, steps, stream):
+    """Average ms per call with HIP events recorded on `stream`."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz):
+    """Reference CPU path (scipy CSR product, 1 thread) on a bounded sample."""
+    import numpy as np
+
+    from oracle import cpu_baseline as CB
+
+    d = data.cpu().numpy()
+    i = indices.cpu().numpy()
+    p = indptr.cpu().numpy().astype(np.int64)
+    R = rhs.cpu().numpy()
+    n_rows = shape[0]
+    op = cfg["op"]
+    if cfg["op_kind"] == "spmm" and op != "non":
+        # A^T / A^H once (not timed), then rows of it: same sample policy as op=non.
+        import scipy.sparse as sp
+
+        A = sp.csr_matrix((d, i, p), shape=shape)
+        A = (A.conj() if op == "conj" else A).T.tocsr()
+        d, i, p, shape = A.data, A.indices, A.indptr.astype(np.int64), A.shape
+        n_rows = shape[0]
+        op = "non"
+    budget = 3e8 if cfg["op_kind"] == "spmv" else 2e8 / max(1, R.shape[1] if R.ndim == 2 else 1)
+    rows = n_rows
+    if p[-1] > budget:
+        rows = int(np.searchsorted(p, budget))
+        rows = max(1, min(rows, n_rows))
+    nnz_s = int(p[rows])
+    secs, reps = CB.time_scipy(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R, op=op, min_seconds=10.0)
+    frac = nnz_s / max(1, full_nnz)
+    value = full_bytes * frac / secs / 1e9
+    info = CB.host_info()
+    return {
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (
+            f"scipy.sparse csr_matrix @ {'x' if R.ndim == 1 else 'B'} (the reference's CPU path), native dtype, "
+            f"rows [0,{rows}) of the same matrix ({nnz_s} of {full_nnz} nnz), median of {reps} runs "
+            f"({secs * 1e3:.2f} ms each); value = full algorithmic bytes x sampled nnz fraction / time; "
+            f"host {info['model']}, {info['affinity']} cores visible"
+        ),
+    }
+
+
+def run(args):
+    import torch
+
+    import flagsparse_amd as fs
+    from flagsparse_amd import _lib
+    from flagsparse_amd import synthetic as S
+
+    cfg = CONFIGS[args.config]
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    stream = torch.cuda.current_stream(device)
+    t0 = time.perf_counter()
+    data, indices, indptr, shape = generate(cfg, device)
+    torch.cuda.synchronize()
+    gen_s = time.perf_counter() - t0
+    nnz = data.numel()
+    vb, ib, pb = elem_bytes(data), elem_bytes(indices), elem_bytes(indptr)
+    complex_values = data.dtype.is_complex
+    op = cfg["op"]
+    extra = {}
+
+    if cfg["op_kind"] == "spmv":
+        t1 = time.perf_counter()
+        prep = fs.prepare_spmv_csr(data, indices, indptr, shape, op=op)
+        torch.cuda.synchronize()
+        analysis_ms = (time.perf_counter() - t1) * 1e3
+        x = S.vector(prep.n_cols, data.dtype, device, seed=11)
+        rhs = x
+        step = lambda: fs.flagsparse_spmv_csr(x=x, prepared=prep)  # noqa: E731
+        plan = prep.hip_plan()
+        y = torch.empty(prep.n_rows, dtype=data.dtype, device=device)
+        carry = prep._carry
+        lib = _lib.lib()
+        args_abi = (
+            plan.plan, _lib.ptr(prep.data), _lib.ptr(prep.kernel_indices), _lib.ptr(prep.kernel_indptr),
+            _lib.ptr(x), _lib.ptr(y), _lib.ptr(prep._part), _lib.ptr(carry), 0 if carry is None else carry.numel(),
+            _lib.stream_handle(device),
+        )
+        kernel_call = lambda: lib.fs_spmv_csr(*args_abi)  # noqa: E731
+        bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
+        flops = S.flops_spmv(nnz, complex_values)
+        kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel"}[plan.kernel_name]
+        extra.update(kernel_variant=plan.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
+        m, k, n_dense = prep.n_rows, prep.n_cols, 1
+    else:
+        n_dense = cfg["n"]
+        t1 = time.perf_counter()
+        if op != "non":
+            from flagsparse_amd import _csr
+
+            d_op, i_op, p_op, sh_op = _csr.transpose_csr(data, indices, indptr, shape, conj=(op == "conj"))
+        else:
+            d_op, i_op, p_op, sh_op = data, indices, indptr, shape
+        route = fs.prepare_spmm_csr_route(d_op, i_op, p_op, sh_op, op="non")
+        torch.cuda.synchronize()
+        analysis_ms = (time.perf_counter() - t1) * 1e3
+        m, k = sh_op
+        B = S.dense(k, n_dense, data.dtype, device, seed=13, dist="normal" if cfg["gen"] == "rmat" else "uniform")
+        rhs = B
+        step = lambda: fs.flagsparse_spmm_csr_run(route, B)  # noqa: E731
+        plan = route.hip_plan()
+        C = torch.empty((m, n_dense), dtype=data.dtype, device=device)
+        lib = _lib.lib()
+        ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(data.dtype), plan.n_tiles, n_dense), device)
+        args_abi = (
+            plan.csr.plan, _lib.ptr(route.data), _lib.ptr(route.kernel_indices), _lib.ptr(route.kernel_indptr),
+            _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.ptr(plan.part), plan.tile_items, plan.n_tiles,
+            _lib.ptr(ws), ws.numel(), _lib.stream_handle(device),
+        )
+        kernel_call = lambda: lib.fs_spmm_csr(*args_abi)  # noqa: E731
+        bytes_alg = S.bytes_spmm(nnz, m, k, n_dense, vb, ib, pb)
+        flops = S.flops_spmm(nnz, n_dense, complex_values)
+        kernel_name = "spmm_merge_kernel"
+        extra.update(max_row_nnz=plan.csr.max_row_nnz, analysis_ms=round(analysis_ms, 3), n_dense=n_dense)
+        if op != "non":
+            # Public call including the per-call transpose (reference semantics).
+            full = lambda: fs.flagsparse_spmm_csr(data, indices, indptr, B, shape, op=op)  # noqa: E731
+            full()
+            extra["ms_with_transpose"] = round(time_loop(full, max(2, args.steps // 10), stream), 4)
+
+    # warm-up, then the timed steps
+    for _ in range(args.warmup):
+        step()
+    ms_per_step = time_loop(step, args.steps, stream)
+    rc = kernel_call()
+    if rc != 0:
+        raise RuntimeError(lib.fs_last_error().decode())
+    kernel_ms = time_loop(kernel_call, args.steps, stream)
+
+    value = bytes_alg / (ms_per_step * 1e-3) / 1e9
+    achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
+    dtype_name = {"f32": "f32 (fp64 accumulate)", "f64": "f64", "c64": "c64 (fp64 accumulate)"}[cfg["dtype"]]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype_name,
+        "data": "synthetic (seeded on-device generator, flagsparse_amd/synthetic.py)",
+        "config": {
+            "workload": args.config,
+            "op": op,
+            "n_rows": int(m),
+            "n_cols": int(k),
+            "nnz": int(nnz),
+            "n_dense": int(n_dense),
+            "index_dtype": cfg["index"],
+            "value_dtype": cfg["dtype"],
+            "algorithmic_bytes": int(bytes_alg),
+        },
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "gflops": round(flops / (ms_per_step * 1e-3) / 1e9, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kernel_name,
+            "kernel_ms": round(kernel_ms, 5),
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": args.traffic_bytes,
+        },
+        "extra": dict(extra, generate_s=round(gen_s, 2)),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(cfg, data, indices, indptr, shape, rhs, bytes_alg, nnz)
+    return line
+
+
+def copy_calibration(args):
+    """A plain device copy of known size (for scaling FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+
+    n = 1 << 28  # 1 GiB of fp32
+    a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(max(1, args.steps)):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "launches": max(1, args.steps)}))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default=DEFAULT_CONFIG, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic-bytes", type=float, default=None,
+                    help="HBM bytes per launch measured with rocprofv3 FETCH_SIZE+WRITE_SIZE (scaled)")
+    ap.add_argument("--copy-calibration", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            json.dumps({"error": "this build runs on one GPU only; the path's multi-GPU sharding is described "
+                                 "in DESIGN.md and not implemented", "n_gpus": args.gpus}),
+            flush=True,
+        )
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "multi-process runs are not supported"}), flush=True)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args)
+        return
+    line = run(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,47 @@
+"""flagsparse_amd — FlagSparse's CSR SpMV / SpMM path on MI355X (gfx950).
+
+Drop-in for the reference's CSR SpMV/SpMM operators
+(src/flagsparse/__init__.py:124-254, sparse_operations/__init__.py): same
+function names, signatures, return shapes and error messages; the device
+work runs in hand-written HIP kernels (libflagsparse_hip.so, C ABI in
+include/flagsparse_hip.h).
+
+    import flagsparse_amd as flagsparse
+    y = flagsparse.flagsparse_spmv_csr(data, indices, indptr, x, shape)
+"""
+
+from ._common import (
+    SUPPORTED_INDEX_DTYPES,
+    SUPPORTED_VALUE_DTYPES,
+    _INDEX_LIMIT_INT32,
+    _tolerance_for_dtype,
+)
+from .spmm_csr import (
+    SPMM_CSR_ALGORITHMS,
+    PreparedCsrSpmmRoute,
+    SpmmCsrAlgorithm,
+    SpmmCsrAlgorithmUnavailable,
+    flagsparse_spmm_csr,
+    flagsparse_spmm_csr_run,
+    list_spmm_csr_algorithms,
+    prepare_spmm_csr_route,
+    resolve_spmm_csr_algorithm,
+)
+from .spmv_csr import PreparedCsrSpmv, flagsparse_spmv_csr, prepare_spmv_csr
+
+__all__ = [
+    "SUPPORTED_VALUE_DTYPES",
+    "SUPPORTED_INDEX_DTYPES",
+    "flagsparse_spmv_csr",
+    "prepare_spmv_csr",
+    "PreparedCsrSpmv",
+    "flagsparse_spmm_csr",
+    "flagsparse_spmm_csr_run",
+    "prepare_spmm_csr_route",
+    "list_spmm_csr_algorithms",
+    "resolve_spmm_csr_algorithm",
+    "SPMM_CSR_ALGORITHMS",
+    "SpmmCsrAlgorithm",
+    "SpmmCsrAlgorithmUnavailable",
+    "PreparedCsrSpmmRoute",
+]

@@ -1,0 +1,166 @@
+"""ctypes binding of libflagsparse_hip.so (C ABI in include/flagsparse_hip.h).
+
+torch is imported before the library is opened so that its bundled HIP
+runtime (same soname, libamdhip64.so.7) is the one our library binds to;
+torch streams and our launches then live in one runtime.
+
+There is no CPU fallback: every compute entry point raises if the library
+is missing or a call fails.
+"""
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libflagsparse_hip.so")
+
+FS_F32, FS_F64, FS_C64, FS_C128 = 0, 1, 2, 3
+FS_I32, FS_I64 = 0, 1
+FS_KERNEL_VECTOR, FS_KERNEL_MERGE = 0, 1
+FS_HIST_BINS = 24
+
+VALUE_TYPE_CODES = {
+    torch.float32: FS_F32,
+    torch.float64: FS_F64,
+    torch.complex64: FS_C64,
+    torch.complex128: FS_C128,
+}
+INDEX_TYPE_CODES = {torch.int32: FS_I32, torch.int64: FS_I64}
+KERNEL_NAMES = {FS_KERNEL_VECTOR: "vector", FS_KERNEL_MERGE: "merge"}
+
+# Every symbol the header declares (checked by the CPU test suite).
+EXPORTED_SYMBOLS = (
+    "fs_last_error",
+    "fs_version",
+    "fs_csr_stats_bytes",
+    "fs_csr_analyze",
+    "fs_csr_partition",
+    "fs_spmv_csr",
+    "fs_spmm_workspace_bytes",
+    "fs_spmm_tile_items",
+    "fs_spmm_csr",
+    "fs_csr_transpose_workspace_bytes",
+    "fs_csr_transpose",
+)
+
+
+class FsCsrPlan(ctypes.Structure):
+    """Mirror of struct fs_csr_plan."""
+
+    _fields_ = [
+        ("n_rows", ctypes.c_int64),
+        ("n_cols", ctypes.c_int64),
+        ("nnz", ctypes.c_int64),
+        ("val_t", ctypes.c_int32),
+        ("idx_t", ctypes.c_int32),
+        ("ptr_t", ctypes.c_int32),
+        ("kernel", ctypes.c_int32),
+        ("vec_width", ctypes.c_int32),
+        ("tile_items", ctypes.c_int32),
+        ("n_tiles", ctypes.c_int64),
+        ("max_row", ctypes.c_int64),
+        ("min_row", ctypes.c_int64),
+        ("hist", ctypes.c_int64 * FS_HIST_BINS),
+        ("part_bytes", ctypes.c_size_t),
+        ("carry_bytes", ctypes.c_size_t),
+    ]
+
+
+class HipLibraryError(RuntimeError):
+    """A call into libflagsparse_hip failed (message from fs_last_error)."""
+
+
+_lib = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_sz = ctypes.c_size_t
+
+
+def _declare(lib):
+    lib.fs_last_error.restype = ctypes.c_char_p
+    lib.fs_last_error.argtypes = []
+    lib.fs_version.restype = ctypes.c_char_p
+    lib.fs_version.argtypes = []
+    lib.fs_csr_stats_bytes.restype = _sz
+    lib.fs_csr_stats_bytes.argtypes = []
+    lib.fs_csr_analyze.restype = _i32
+    lib.fs_csr_analyze.argtypes = [_vp, _i32, _i32, _i32, _i64, _i64, _i64, _i32, _vp,
+                                   ctypes.POINTER(FsCsrPlan), _vp]
+    lib.fs_csr_partition.restype = _i32
+    lib.fs_csr_partition.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _i32, _i64, _vp]
+    lib.fs_spmv_csr.restype = _i32
+    lib.fs_spmv_csr.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.fs_spmm_workspace_bytes.restype = _sz
+    lib.fs_spmm_workspace_bytes.argtypes = [_i32, _i64, _i64]
+    lib.fs_spmm_tile_items.restype = _i32
+    lib.fs_spmm_tile_items.argtypes = [_i32, _i64]
+    lib.fs_spmm_csr.restype = _i32
+    lib.fs_spmm_csr.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
+                                _vp, _i32, _i64, _vp, _sz, _vp]
+    lib.fs_csr_transpose_workspace_bytes.restype = _sz
+    lib.fs_csr_transpose_workspace_bytes.argtypes = [_i64, _i64, _i64]
+    lib.fs_csr_transpose.restype = _i32
+    lib.fs_csr_transpose.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32,
+                                     _vp, _vp, _vp, _vp, _sz, _vp]
+
+
+def load_library(path=None):
+    """Open the HIP library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise HipLibraryError(
+            f"libflagsparse_hip.so not found at {p}; build it with "
+            "`python -m flagsparse_amd.csrc.build` (there is no CPU fallback)"
+        )
+    lib = ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL)
+    _declare(lib)
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def lib():
+    return load_library()
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = lib().fs_last_error().decode("utf-8", "replace")
+        raise HipLibraryError(f"{what} failed (status {rc}): {msg}")
+
+
+def ptr(t):
+    """Raw device pointer of a tensor (None for empty tensors)."""
+    if t is None or t.numel() == 0:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def value_code(dtype):
+    try:
+        return VALUE_TYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported value dtype for the HIP kernels: {dtype}") from None
+
+
+def index_code(dtype):
+    try:
+        return INDEX_TYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported index dtype for the HIP kernels: {dtype}") from None
+
+
+def workspace(nbytes, device):
+    """Caller-owned scratch (the C ABI never allocates)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

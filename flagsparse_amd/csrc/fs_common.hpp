@@ -1,0 +1,187 @@
+// fs_common.hpp — shared device/host helpers for the gfx950 CSR kernels.
+//
+// Value types and their accumulators.  The reference computes fp32 CSR
+// products in fp64 and rounds once at the end (spmv_csr.py:124-130,
+// spmm_csr.py:2720-2759); every kernel here does the same for fp32 and also
+// accumulates complex64 in fp64 components.  fp64 / complex128 accumulate
+// natively.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/flagsparse_hip.h"
+
+namespace fs {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+struct alignas(8) c32 {
+  float re, im;
+};
+struct alignas(16) c64 {
+  double re, im;
+};
+
+// ---------------------------------------------------------------------------
+// Value traits: load type V, accumulator A.
+// ---------------------------------------------------------------------------
+template <class V>
+struct VT;
+
+template <>
+struct VT<float> {
+  using acc = double;
+  static constexpr bool complex = false;
+  __device__ static acc zero() { return 0.0; }
+  __device__ static acc mul(float a, float x) { return (double)a * (double)x; }
+  __device__ static acc fma(float a, float x, acc s) {
+    return __builtin_fma((double)a, (double)x, s);
+  }
+  __device__ static float out(acc s) { return (float)s; }
+  __device__ static float conj(float v) { return v; }
+};
+
+template <>
+struct VT<double> {
+  using acc = double;
+  static constexpr bool complex = false;
+  __device__ static acc zero() { return 0.0; }
+  __device__ static acc mul(double a, double x) { return a * x; }
+  __device__ static acc fma(double a, double x, acc s) {
+    return __builtin_fma(a, x, s);
+  }
+  __device__ static double out(acc s) { return s; }
+  __device__ static double conj(double v) { return v; }
+};
+
+template <>
+struct VT<c32> {
+  using acc = c64;
+  static constexpr bool complex = true;
+  __device__ static acc zero() { return c64{0.0, 0.0}; }
+  __device__ static acc mul(c32 a, c32 x) {
+    double ar = a.re, ai = a.im, xr = x.re, xi = x.im;
+    return c64{__builtin_fma(ar, xr, -ai * xi), __builtin_fma(ar, xi, ai * xr)};
+  }
+  __device__ static acc fma(c32 a, c32 x, acc s) {
+    double ar = a.re, ai = a.im, xr = x.re, xi = x.im;
+    s.re = __builtin_fma(ar, xr, s.re);
+    s.re = __builtin_fma(-ai, xi, s.re);
+    s.im = __builtin_fma(ar, xi, s.im);
+    s.im = __builtin_fma(ai, xr, s.im);
+    return s;
+  }
+  __device__ static c32 out(acc s) { return c32{(float)s.re, (float)s.im}; }
+  __device__ static c32 conj(c32 v) { return c32{v.re, -v.im}; }
+};
+
+template <>
+struct VT<c64> {
+  using acc = c64;
+  static constexpr bool complex = true;
+  __device__ static acc zero() { return c64{0.0, 0.0}; }
+  __device__ static acc mul(c64 a, c64 x) {
+    return c64{__builtin_fma(a.re, x.re, -a.im * x.im),
+               __builtin_fma(a.re, x.im, a.im * x.re)};
+  }
+  __device__ static acc fma(c64 a, c64 x, acc s) {
+    s.re = __builtin_fma(a.re, x.re, s.re);
+    s.re = __builtin_fma(-a.im, x.im, s.re);
+    s.im = __builtin_fma(a.re, x.im, s.im);
+    s.im = __builtin_fma(a.im, x.re, s.im);
+    return s;
+  }
+  __device__ static c64 out(acc s) { return s; }
+  __device__ static c64 conj(c64 v) { return c64{v.re, -v.im}; }
+};
+
+__device__ inline double add(double a, double b) { return a + b; }
+__device__ inline c64 add(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
+
+// ---------------------------------------------------------------------------
+// Cross-lane moves.  DPP for distances inside a 16-lane row, ds_swizzle for
+// the 16-lane xor inside each 32-lane half, readlane across halves.
+// ---------------------------------------------------------------------------
+// DPP control words (GCN3+ encoding).
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // reverse within 8 lanes
+constexpr int kDppRowMirror = 0x140;     // reverse within 16 lanes
+// ds_swizzle bit mode: and=0x1f, or=0, xor=0x10 -> lane ^ 16 within 32.
+constexpr int kSwzXor16 = (0x10 << 10) | 0x1F;
+
+template <int CTRL>
+__device__ inline double dpp_f64(double v) {
+  int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false);
+  int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
+__device__ inline double swz_xor16_f64(double v) {
+  int lo = __builtin_amdgcn_ds_swizzle(__double2loint(v), kSwzXor16);
+  int hi = __builtin_amdgcn_ds_swizzle(__double2hiint(v), kSwzXor16);
+  return __hiloint2double(hi, lo);
+}
+
+// Butterfly all-reduce over aligned groups of W lanes (W power of two, <=32).
+// Each step's partner set is closed under the group, so every lane of a
+// group ends with the group total.  Mirror permutations act as xor-4 /
+// xor-8 because the values are already uniform within quads / octets.
+template <int W>
+__device__ inline double group_sum(double v) {
+  if constexpr (W >= 2) v += dpp_f64<kDppQuadXor1>(v);
+  if constexpr (W >= 4) v += dpp_f64<kDppQuadXor2>(v);
+  if constexpr (W >= 8) v += dpp_f64<kDppRowHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_f64<kDppRowMirror>(v);
+  if constexpr (W >= 32) v += swz_xor16_f64(v);
+  return v;
+}
+
+template <int W>
+__device__ inline c64 group_sum(c64 v) {
+  return c64{group_sum<W>(v.re), group_sum<W>(v.im)};
+}
+
+__device__ inline double readlane_f64(double v, int lane) {
+  int lo = __builtin_amdgcn_readlane(__double2loint(v), lane);
+  int hi = __builtin_amdgcn_readlane(__double2hiint(v), lane);
+  return __hiloint2double(hi, lo);
+}
+
+// Generic shuffle (ds_bpermute) of 64-bit values, used for scans.
+__device__ inline double shfl_f64(double v, int src_lane) {
+  int lo = __builtin_amdgcn_ds_bpermute(src_lane << 2, __double2loint(v));
+  int hi = __builtin_amdgcn_ds_bpermute(src_lane << 2, __double2hiint(v));
+  return __hiloint2double(hi, lo);
+}
+__device__ inline c64 shfl(c64 v, int src) { return c64{shfl_f64(v.re, src), shfl_f64(v.im, src)}; }
+__device__ inline double shfl(double v, int src) { return shfl_f64(v, src); }
+__device__ inline int shfl(int v, int src) { return __builtin_amdgcn_ds_bpermute(src << 2, v); }
+
+// ---------------------------------------------------------------------------
+// Error reporting (thread-local message, see fs_last_error()).
+// ---------------------------------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_hip(hipError_t e, const char* what);
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Type-code validation shared by every entry point.
+bool valid_types(int val_t, int idx_t, int ptr_t);
+
+}  // namespace fs
+
+#define FS_CHECK_HIP(expr)                                  \
+  do {                                                      \
+    int _rc = ::fs::check_hip((expr), #expr);               \
+    if (_rc != FS_OK) return _rc;                           \
+  } while (0)
+
+#define FS_CHECK_LAUNCH(name)                               \
+  do {                                                      \
+    int _rc = ::fs::check_hip(hipGetLastError(), name);     \
+    if (_rc != FS_OK) return _rc;                           \
+  } while (0)

@@ -1,0 +1,514 @@
+// spmv.hip — CSR SpMV for gfx950: analysis, merge-path partition, and the
+// two SpMV kernel families.
+//
+// Reference behaviour being replaced (NCIC-AlphaSparse/FlagSparse):
+//   _spmv_csr_real_kernel / _spmv_csr_complex_kernel   spmv_csr.py:166-227
+//   opt CSR-Vector buckets                             spmv_csr.py:233-461
+//   prepare_spmv_csr block/segment sizing              spmv_csr.py:591-664
+// The reference walks every row for ceil(max_row/BLOCK) segments; here the
+// work is either one short vector per row (regular matrices) or an
+// nnz+row balanced merge path (any matrix), so a 50,000-nnz row costs the
+// same per item as a 10-nnz row.
+#include "fs_common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+namespace fs {
+
+// ---------------------------------------------------------------------------
+// Row-length statistics (input to the host-side kernel choice).
+// stats layout (uint64): [0..FS_HIST_BINS) histogram, [FS_HIST_BINS] max,
+// [FS_HIST_BINS+1] min.
+// ---------------------------------------------------------------------------
+constexpr int kStatsWords = FS_HIST_BINS + 2;
+
+__global__ void stats_init_kernel(unsigned long long* stats) {
+  int k = threadIdx.x;
+  if (k < kStatsWords) stats[k] = (k == FS_HIST_BINS + 1) ? ~0ull : 0ull;
+}
+
+template <class P>
+__global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr,
+                                                    int64_t n_rows,
+                                                    unsigned long long* stats) {
+  __shared__ unsigned int s_hist[FS_HIST_BINS];
+  if (threadIdx.x < FS_HIST_BINS) s_hist[threadIdx.x] = 0;
+  __syncthreads();
+  unsigned long long vmax = 0, vmin = ~0ull;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n_rows;
+       r += (int64_t)gridDim.x * blockDim.x) {
+    unsigned long long len = (unsigned long long)(rowptr[r + 1] - rowptr[r]);
+    int bin = len == 0 ? 0 : (64 - __clzll(len));
+    bin = bin < FS_HIST_BINS ? bin : FS_HIST_BINS - 1;
+    atomicAdd(&s_hist[bin], 1u);
+    vmax = len > vmax ? len : vmax;
+    vmin = len < vmin ? len : vmin;
+  }
+  // Integer max/min/count reductions are order independent.
+  atomicMax(&stats[FS_HIST_BINS], vmax);
+  atomicMin(&stats[FS_HIST_BINS + 1], vmin);
+  __syncthreads();
+  if (threadIdx.x < FS_HIST_BINS && s_hist[threadIdx.x])
+    atomicAdd(&stats[threadIdx.x], (unsigned long long)s_hist[threadIdx.x]);
+}
+
+// ---------------------------------------------------------------------------
+// Merge-path partition.  The merge path interleaves the row-end offsets
+// (rowptr[1..n_rows]) with the nnz indices 0..nnz-1; a row end is consumed
+// before nnz j when rowptr[i+1] <= j.  Tile t starts at diagonal t*T; part[t]
+// is the number of row ends consumed before that diagonal.
+// ---------------------------------------------------------------------------
+template <class P>
+__global__ __launch_bounds__(256) void partition_kernel(const P* __restrict__ rowptr,
+                                                        int64_t n_rows, int64_t nnz,
+                                                        int64_t tile_items, int64_t n_tiles,
+                                                        int64_t* __restrict__ part) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t > n_tiles) return;
+  int64_t diag = t * tile_items;
+  int64_t total = n_rows + nnz;
+  diag = diag < total ? diag : total;
+  int64_t lo = diag - nnz > 0 ? diag - nnz : 0;
+  int64_t hi = diag < n_rows ? diag : n_rows;
+  while (lo < hi) {
+    int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)rowptr[mid + 1] <= diag - mid - 1)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  part[t] = lo;
+}
+
+// ---------------------------------------------------------------------------
+// K1: vector-per-row.  VW lanes share a row; products accumulate in the
+// accumulator type and are combined with a DPP / ds_swizzle butterfly.
+// ---------------------------------------------------------------------------
+template <int VW, class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_vector_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / VW;
+  const int sub = threadIdx.x & (VW - 1);
+  if (row >= n_rows) return;  // whole VW-group leaves together
+  const int64_t s = (int64_t)rowptr[row];
+  const int64_t e = (int64_t)rowptr[row + 1];
+  A a0 = T::zero(), a1 = T::zero();
+  int64_t j = s + sub;
+  for (; j + VW < e; j += 2 * VW) {
+    V v0 = vals[j], v1 = vals[j + VW];
+    I c0 = cols[j], c1 = cols[j + VW];
+    a0 = T::fma(v0, x[c0], a0);
+    a1 = T::fma(v1, x[c1], a1);
+  }
+  if (j < e) a0 = T::fma(vals[j], x[cols[j]], a0);
+  A acc = add(a0, a1);
+  if constexpr (VW <= 32) {
+    acc = group_sum<VW>(acc);
+  } else {
+    acc = group_sum<32>(acc);
+    acc = add(acc, shfl(acc, (threadIdx.x & 63) ^ 32));
+  }
+  if (sub == 0) y[row] = T::out(acc);
+}
+
+// ---------------------------------------------------------------------------
+// K2: merge-path SpMV, one wave per tile of kSlabs*64 merge items.
+//
+// Item d of the tile is either a row end or one nnz.  For every 64-item
+// slab the wave
+//   1. marks which items are row ends (row-end positions are scattered into
+//      a 64-entry LDS table and read back, then ballot -> 64-bit mask held in
+//      scalar registers);
+//   2. loads the nnz of the slab (contiguous, coalesced) and gathers x;
+//   3. runs a segmented inclusive scan across the wave with DPP row shifts
+//      and row broadcasts; the lane holding a row end then owns that row's
+//      sum.
+// A running carry links slabs.  Rows that start in an earlier tile write
+// their in-tile part to head[t]; the part of the last open row goes to
+// tail[t]; merge_fixup_kernel adds them in tile order, so results are
+// deterministic and no floating-point atomics are used.
+// ---------------------------------------------------------------------------
+constexpr int kSlabs = 8;
+constexpr int kMergeTile = kSlabs * 64;
+constexpr int kMergeWaves = 4;
+
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ inline int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+__device__ inline int count_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((unsigned)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((unsigned)mask, 0u));
+}
+
+// DPP-shifted copy of a 32-bit value; lanes whose source is outside the
+// enabled rows / row bounds receive 0.
+template <int CTRL, int ROWMASK>
+__device__ inline int dpp_shift(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWMASK, 0xF, false);
+}
+
+template <int CTRL, int ROWMASK>
+__device__ inline double dpp_shift(double v) {
+  int lo = dpp_shift<CTRL, ROWMASK>(__double2loint(v));
+  int hi = dpp_shift<CTRL, ROWMASK>(__double2hiint(v));
+  return __hiloint2double(hi, lo);
+}
+
+template <int CTRL, int ROWMASK>
+__device__ inline c64 dpp_shift(c64 v) {
+  return c64{dpp_shift<CTRL, ROWMASK>(v.re), dpp_shift<CTRL, ROWMASK>(v.im)};
+}
+
+// One step of the segmented scan: lanes that have not yet reached their
+// segment head absorb the shifted partial and its head flag.
+template <int CTRL, int ROWMASK, class A>
+__device__ inline void seg_step(A& v, int& f) {
+  A pv = dpp_shift<CTRL, ROWMASK>(v);
+  int pf = dpp_shift<CTRL, ROWMASK>(f);
+  if (!f) {
+    v = add(v, pv);
+    f = pf;
+  }
+}
+
+// Segmented inclusive scan over the wave; f = 1 marks a segment head.
+// row_shr 1,2,4,8 scan each 16-lane row; row_bcast15 / row_bcast31 carry
+// across rows (the standard CDNA wave-scan sequence).
+template <class A>
+__device__ inline A seg_scan(A v, int f) {
+  seg_step<0x111, 0xF>(v, f);  // row_shr:1
+  seg_step<0x112, 0xF>(v, f);  // row_shr:2
+  seg_step<0x114, 0xF>(v, f);  // row_shr:4
+  seg_step<0x118, 0xF>(v, f);  // row_shr:8
+  seg_step<0x142, 0xA>(v, f);  // row_bcast:15 -> rows 1,3
+  seg_step<0x143, 0xC>(v, f);  // row_bcast:31 -> rows 2,3
+  return v;
+}
+
+template <class A>
+__device__ inline A readlane_acc(A v, int lane);
+template <>
+__device__ inline double readlane_acc<double>(double v, int lane) { return readlane_f64(v, lane); }
+template <>
+__device__ inline c64 readlane_acc<c64>(c64 v, int lane) {
+  return c64{readlane_f64(v.re, lane), readlane_f64(v.im, lane)};
+}
+
+template <class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_merge_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, const int64_t* __restrict__ part,
+    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail,
+    int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  __shared__ P s_end[kMergeWaves][kMergeTile];
+  __shared__ int s_tab[kMergeWaves][64];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kMergeWaves + w;
+  if (t >= n_tiles) return;  // per-wave work only; no block barriers below
+
+  const int64_t r0 = part[t];
+  const int64_t r1 = part[t + 1];
+  const int64_t d0 = t * kMergeTile;
+  const int64_t total = n_rows + nnz;
+  const int64_t dend = d0 + kMergeTile < total ? d0 + kMergeTile : total;
+  const int64_t n0 = d0 - r0;
+  const int64_t n1 = dend - r1;  // exclusive nnz end of the tile
+  const int R = (int)(r1 - r0);
+  P* end = s_end[w];
+  int* tab = s_tab[w];
+
+  for (int k = lane; k < R; k += 64) end[k] = rowptr[r0 + 1 + k];
+  const bool head_partial = R > 0 && (int64_t)rowptr[r0] < n0;
+  wave_sync();
+
+  // Pass 1: classify items of every slab (row end or nnz).
+  uint64_t masks[kSlabs];
+  int is_[kSlabs];
+  int js_[kSlabs];
+  int i_s = 0, j_s = 0;
+#pragma unroll
+  for (int s = 0; s < kSlabs; ++s) {
+    tab[lane] = 0;
+    wave_sync();
+    const int k = i_s + lane;
+    if (k < R) {
+      int64_t q = (r0 + k) + (int64_t)end[k] - (d0 + 64 * s);
+      if (q < 64) tab[(int)q] = 1;
+    }
+    wave_sync();
+    const bool e = tab[lane] != 0;
+    const uint64_t m = __ballot(e);
+    masks[s] = m;
+    is_[s] = i_s;
+    js_[s] = j_s;
+    const int cnt = __popcll(m);
+    i_s += cnt;
+    j_s += 64 - cnt;
+    wave_sync();
+  }
+
+  // Pass 2: issue every slab's loads before any arithmetic.
+  V av[kSlabs];
+  I cv[kSlabs];
+  bool ok[kSlabs];
+#pragma unroll
+  for (int s = 0; s < kSlabs; ++s) {
+    const uint64_t m = masks[s];
+    const bool is_end = (m >> lane) & 1ull;
+    const int64_t j = n0 + js_[s] + lane - count_below(m);
+    ok[s] = !is_end && j < n1;
+    if (ok[s]) {
+      av[s] = vals[j];
+      cv[s] = cols[j];
+    } else {
+      cv[s] = 0;
+    }
+  }
+  V xv[kSlabs];
+#pragma unroll
+  for (int s = 0; s < kSlabs; ++s) {
+    if (ok[s]) xv[s] = x[cv[s]];
+  }
+
+  // Pass 3: segmented scan per slab.
+  A carry = T::zero();
+#pragma unroll
+  for (int s = 0; s < kSlabs; ++s) {
+    const uint64_t m = masks[s];
+    const bool is_end = (m >> lane) & 1ull;
+    const int before = count_below(m);
+    A v = ok[s] ? T::mul(av[s], xv[s]) : T::zero();
+    const int f = (lane == 0) || ((m >> (lane - 1)) & 1ull) ? 1 : 0;
+    v = seg_scan(v, f);
+    if (is_end) {
+      A sum = v;
+      if (before == 0) sum = add(sum, carry);
+      const int64_t row = r0 + is_[s] + before;
+      if (row == r0 && head_partial)
+        head[t] = sum;
+      else
+        y[row] = T::out(sum);
+    }
+    const A last = readlane_acc(v, 63);
+    if ((m >> 63) & 1ull)
+      carry = T::zero();
+    else if (m == 0)
+      carry = add(carry, last);
+    else
+      carry = last;
+  }
+  if (lane == 0 && r1 < n_rows) tail[t] = carry;
+}
+
+// Rows that span tiles: y[row] = tail[f] + ... + tail[t-1] + head[t], where
+// tiles f..t-1 all end inside `row` and tile t holds its row end.
+template <class V, class P>
+__global__ __launch_bounds__(256) void merge_fixup_kernel(
+    const P* __restrict__ rowptr, const int64_t* __restrict__ part,
+    const typename VT<V>::acc* __restrict__ head, const typename VT<V>::acc* __restrict__ tail,
+    V* __restrict__ y, int64_t n_tiles, int64_t tile_items) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_tiles) return;
+  const int64_t r0 = part[t];
+  if (part[t + 1] == r0) return;  // tile holds no row end
+  const int64_t n0 = t * tile_items - r0;
+  if ((int64_t)rowptr[r0] >= n0) return;  // row r0 starts inside tile t
+  int64_t f = t - 1;
+  while (f > 0 && part[f] == r0) --f;
+  A sum = tail[f];
+  for (int64_t k = f + 1; k < t; ++k) sum = add(sum, tail[k]);
+  sum = add(sum, head[t]);
+  y[r0] = T::out(sum);
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+// ---------------------------------------------------------------------------
+template <class V, class I, class P>
+int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
+                const void* x, void* y, const void* part, void* carry, size_t carry_bytes,
+                hipStream_t stream) {
+  using A = typename VT<V>::acc;
+  const int64_t n_rows = plan->n_rows;
+  if (n_rows == 0) return FS_OK;
+  const V* v = static_cast<const V*>(vals);
+  const I* c = static_cast<const I*>(cols);
+  const P* p = static_cast<const P*>(indptr);
+  const V* xv = static_cast<const V*>(x);
+  V* yv = static_cast<V*>(y);
+  if (plan->kernel == FS_KERNEL_VECTOR) {
+    const int vw = plan->vec_width;
+    const int64_t threads = n_rows * vw;
+    const int64_t blocks = ceil_div(threads, 256);
+    if (blocks > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr: grid too large for vector kernel");
+    dim3 g((unsigned)blocks);
+    switch (vw) {
+      case 2: hipLaunchKernelGGL((spmv_vector_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      case 4: hipLaunchKernelGGL((spmv_vector_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      case 8: hipLaunchKernelGGL((spmv_vector_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      case 16: hipLaunchKernelGGL((spmv_vector_kernel<16, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      case 32: hipLaunchKernelGGL((spmv_vector_kernel<32, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      case 64: hipLaunchKernelGGL((spmv_vector_kernel<64, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      default: return fail(FS_E_INVALID, "fs_spmv_csr: vec_width must be a power of two in [2, 64]");
+    }
+    FS_CHECK_LAUNCH("spmv_vector_kernel");
+    return FS_OK;
+  }
+  if (plan->kernel != FS_KERNEL_MERGE) return fail(FS_E_INVALID, "fs_spmv_csr: unknown kernel");
+  if (plan->tile_items != kMergeTile)
+    return fail(FS_E_INVALID, "fs_spmv_csr: plan tile_items does not match the merge kernel");
+  const int64_t n_tiles = plan->n_tiles;
+  if (part == nullptr) return fail(FS_E_INVALID, "fs_spmv_csr: merge kernel needs the partition");
+  const size_t need = (size_t)n_tiles * 2 * sizeof(A);
+  if (carry == nullptr || carry_bytes < need)
+    return fail(FS_E_WORKSPACE, "fs_spmv_csr: carry workspace too small");
+  A* head = static_cast<A*>(carry);
+  A* tail = head + n_tiles;
+  const int64_t blocks = ceil_div(n_tiles, kMergeWaves);
+  hipLaunchKernelGGL((spmv_merge_kernel<V, I, P>), dim3((unsigned)blocks), dim3(256), 0, stream, v, c, p,
+                     xv, yv, static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
+  FS_CHECK_LAUNCH("spmv_merge_kernel");
+  hipLaunchKernelGGL((merge_fixup_kernel<V, P>), dim3((unsigned)ceil_div(n_tiles, 256)), dim3(256), 0,
+                     stream, p, static_cast<const int64_t*>(part), head, tail, yv, n_tiles,
+                     (int64_t)kMergeTile);
+  FS_CHECK_LAUNCH("merge_fixup_kernel");
+  return FS_OK;
+}
+
+template <class V, class I>
+int dispatch_ptr(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
+                 const void* x, void* y, const void* part, void* carry, size_t cb, hipStream_t s) {
+  if (plan->ptr_t == FS_I32) return launch_spmv<V, I, int32_t>(plan, vals, cols, indptr, x, y, part, carry, cb, s);
+  return launch_spmv<V, I, int64_t>(plan, vals, cols, indptr, x, y, part, carry, cb, s);
+}
+
+template <class V>
+int dispatch_idx(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
+                 const void* x, void* y, const void* part, void* carry, size_t cb, hipStream_t s) {
+  if (plan->idx_t == FS_I32) return dispatch_ptr<V, int32_t>(plan, vals, cols, indptr, x, y, part, carry, cb, s);
+  return dispatch_ptr<V, int64_t>(plan, vals, cols, indptr, x, y, part, carry, cb, s);
+}
+
+size_t acc_bytes(int val_t) {
+  return (val_t == FS_C64 || val_t == FS_C128) ? sizeof(c64) : sizeof(double);
+}
+
+
+// Kernel choice from the row-length histogram.
+void choose_spmv_kernel(fs_csr_plan* plan, int force_kernel) {
+  const int64_t n_rows = plan->n_rows;
+  const double mean = n_rows > 0 ? (double)plan->nnz / (double)n_rows : 0.0;
+  int kernel = FS_KERNEL_MERGE;
+  // Vector-per-row wins only when every row fits one short vector pass and
+  // rows are close to uniform; any long or skewed row goes to the merge
+  // path, which balances rows + nnz exactly.
+  if (n_rows > 0 && plan->max_row <= 64 && (double)plan->max_row <= 2.0 * mean + 4.0) kernel = FS_KERNEL_VECTOR;
+  const char* env = std::getenv("FLAGSPARSE_SPMV_KERNEL");
+  if (env && std::strcmp(env, "vector") == 0) kernel = FS_KERNEL_VECTOR;
+  if (env && std::strcmp(env, "merge") == 0) kernel = FS_KERNEL_MERGE;
+  if (force_kernel == FS_KERNEL_VECTOR || force_kernel == FS_KERNEL_MERGE) kernel = force_kernel;
+  plan->kernel = kernel;
+  int vw = 2;
+  while (vw < 64 && (double)vw < mean) vw <<= 1;
+  plan->vec_width = vw;
+  plan->tile_items = kMergeTile;
+  plan->n_tiles = ceil_div(n_rows + plan->nnz, kMergeTile);
+  plan->part_bytes = (size_t)(plan->n_tiles + 1) * sizeof(int64_t);
+  plan->carry_bytes = (size_t)plan->n_tiles * 2 * acc_bytes(plan->val_t);
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" size_t fs_csr_stats_bytes(void) { return kStatsWords * sizeof(unsigned long long); }
+
+extern "C" int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t, int64_t n_rows,
+                              int64_t n_cols, int64_t nnz, int force_kernel, void* stats_dev,
+                              fs_csr_plan* plan, hipStream_t stream) {
+  if (!plan) return fail(FS_E_INVALID, "fs_csr_analyze: plan is null");
+  if (!valid_types(val_t, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_csr_analyze: bad type code");
+  if (n_rows < 0 || n_cols < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_csr_analyze: negative size");
+  std::memset(plan, 0, sizeof(*plan));
+  plan->n_rows = n_rows;
+  plan->n_cols = n_cols;
+  plan->nnz = nnz;
+  plan->val_t = val_t;
+  plan->idx_t = idx_t;
+  plan->ptr_t = ptr_t;
+  if (n_rows > 0) {
+    if (!indptr || !stats_dev) return fail(FS_E_INVALID, "fs_csr_analyze: null pointer");
+    unsigned long long* st = static_cast<unsigned long long*>(stats_dev);
+    hipLaunchKernelGGL(stats_init_kernel, dim3(1), dim3(64), 0, stream, st);
+    FS_CHECK_LAUNCH("stats_init_kernel");
+    int64_t blocks = std::min<int64_t>(ceil_div(n_rows, 256), 2048);
+    if (ptr_t == FS_I32)
+      hipLaunchKernelGGL((stats_kernel<int32_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const int32_t*>(indptr), n_rows, st);
+    else
+      hipLaunchKernelGGL((stats_kernel<int64_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const int64_t*>(indptr), n_rows, st);
+    FS_CHECK_LAUNCH("stats_kernel");
+    unsigned long long host[kStatsWords];
+    FS_CHECK_HIP(hipMemcpyAsync(host, st, sizeof(host), hipMemcpyDeviceToHost, stream));
+    FS_CHECK_HIP(hipStreamSynchronize(stream));
+    for (int b = 0; b < FS_HIST_BINS; ++b) plan->hist[b] = (int64_t)host[b];
+    plan->max_row = (int64_t)host[FS_HIST_BINS];
+    plan->min_row = (int64_t)host[FS_HIST_BINS + 1];
+  }
+  choose_spmv_kernel(plan, force_kernel);
+  return FS_OK;
+}
+
+extern "C" int fs_csr_partition(const fs_csr_plan* plan, const void* indptr, void* part_dev,
+                                int tile_items, int64_t n_tiles, hipStream_t stream) {
+  if (!plan || !part_dev) return fail(FS_E_INVALID, "fs_csr_partition: null pointer");
+  if (tile_items <= 0) return fail(FS_E_INVALID, "fs_csr_partition: tile_items must be positive");
+  if (n_tiles != ceil_div(plan->n_rows + plan->nnz, tile_items))
+    return fail(FS_E_INVALID, "fs_csr_partition: n_tiles does not match tile_items");
+  if (plan->n_rows > 0 && !indptr) return fail(FS_E_INVALID, "fs_csr_partition: indptr is null");
+  const int64_t blocks = ceil_div(n_tiles + 1, 256);
+  if (plan->ptr_t == FS_I32)
+    hipLaunchKernelGGL((partition_kernel<int32_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const int32_t*>(indptr), plan->n_rows, plan->nnz, (int64_t)tile_items,
+                       n_tiles, static_cast<int64_t*>(part_dev));
+  else
+    hipLaunchKernelGGL((partition_kernel<int64_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const int64_t*>(indptr), plan->n_rows, plan->nnz, (int64_t)tile_items,
+                       n_tiles, static_cast<int64_t*>(part_dev));
+  FS_CHECK_LAUNCH("partition_kernel");
+  return FS_OK;
+}
+
+extern "C" int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
+                           const void* x, void* y, const void* part_dev, void* carry_dev,
+                           size_t carry_bytes, hipStream_t stream) {
+  if (!plan) return fail(FS_E_INVALID, "fs_spmv_csr: plan is null");
+  if (!valid_types(plan->val_t, plan->idx_t, plan->ptr_t)) return fail(FS_E_INVALID, "fs_spmv_csr: bad type code");
+  if (plan->n_rows == 0) return FS_OK;
+  if (!indptr || !y || (plan->nnz > 0 && (!vals || !cols || !x)))
+    return fail(FS_E_INVALID, "fs_spmv_csr: null pointer");
+  switch (plan->val_t) {
+    case FS_F32: return dispatch_idx<float>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
+    case FS_F64: return dispatch_idx<double>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
+    case FS_C64: return dispatch_idx<c32>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
+    default: return dispatch_idx<c64>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
+  }
+}

@@ -1,0 +1,466 @@
+// transpose.hip — CSR -> CSR of A^T (or A^H) on gfx950, bit-exact with a
+// stable sort of the entries by column.
+//
+// Reference: _transpose_csr_for_spmv (spmv_csr.py:477-515) and
+// _transpose_csr_for_spmm (spmm_csr.py:300-338) expand row ids
+// (repeat_interleave), stable-argsort the column indices, gather data and
+// row ids, and build the new indptr with bincount + cumsum; conj is applied
+// to the data first (spmv_csr.py:615-618, spmm_csr.py:341-349).
+//
+// Here: an LSD radix sort over the column index, 8 bits per pass.  Each
+// wave owns a contiguous sub-tile of kSub entries and walks it in 64-entry
+// chunks.  Lanes holding equal digits find each other with eight ballots
+// ("peer masks"), so the per-digit counts and the stable rank of every
+// entry come from popcounts: no atomics, and equal keys keep their input
+// order, which is what makes the result identical to the reference's
+// stable argsort.  Per pass: count -> exclusive scan over
+// [digit][sub-tile] -> stable scatter.  The new indptr is read off the
+// sorted keys (colptr[c] = first position whose key >= c).
+#include "fs_common.hpp"
+
+#include <cstring>
+
+namespace fs {
+
+constexpr int kRadixBits = 8;
+constexpr int kDigits = 1 << kRadixBits;
+constexpr int kChunks = 64;                 // 64-entry chunks per wave sub-tile
+constexpr int64_t kSub = 64 * kChunks;      // entries per wave sub-tile
+constexpr int kWavesPerBlock = 4;
+constexpr int kScanItems = 16;              // per-thread items in the scan kernels
+constexpr int64_t kScanTile = 256 * kScanItems;
+
+__device__ inline int lane_id_t() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+__device__ inline int count_below_t(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((unsigned)(mask >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)mask, 0u));
+}
+__device__ inline void wave_sync_t() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Lanes (among `active`) whose digit equals this lane's digit.
+__device__ inline uint64_t peer_mask(unsigned digit, uint64_t active) {
+  uint64_t peers = active;
+#pragma unroll
+  for (int b = 0; b < kRadixBits; ++b) {
+    const bool bit = (digit >> b) & 1u;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
+}
+
+// Key source: pass 0 reads the CSR column indices directly.
+template <class K>
+__device__ inline K load_key(const void* src, int kind, int64_t e) {
+  if (kind == 0) return (K)(uint32_t) static_cast<const int32_t*>(src)[e];
+  if (kind == 1) return (K)(uint64_t) static_cast<const int64_t*>(src)[e];
+  return static_cast<const K*>(src)[e];
+}
+
+template <class K>
+__global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict__ keys, int kind, int64_t n,
+                                                          int shift, int64_t n_sub,
+                                                          int64_t* __restrict__ counts) {
+  __shared__ unsigned s_hist[kWavesPerBlock][kDigits];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t sub = (int64_t)blockIdx.x * kWavesPerBlock + w;
+  if (sub >= n_sub) return;  // wave-local work only
+  unsigned* hist = s_hist[w];
+  for (int d = lane; d < kDigits; d += 64) hist[d] = 0;
+  wave_sync_t();
+  const int64_t base = sub * kSub;
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int64_t e = base + (int64_t)ch * 64 + lane;
+    const bool valid = e < n;
+    const uint64_t active = __ballot(valid);
+    if (active == 0) break;
+    const K key = valid ? load_key<K>(keys, kind, e) : (K)0;
+    const unsigned digit = (unsigned)(key >> shift) & (kDigits - 1);
+    const uint64_t peers = peer_mask(digit, active);
+    if (valid && count_below_t(peers) == 0) hist[digit] += (unsigned)__popcll(peers);
+    wave_sync_t();
+  }
+  for (int d = lane; d < kDigits; d += 64) counts[(int64_t)d * n_sub + sub] = hist[d];
+}
+
+template <class K, class Pos>
+__global__ __launch_bounds__(256) void radix_scatter_kernel(const void* __restrict__ keys_in, int kind,
+                                                            const Pos* __restrict__ pos_in, int64_t n, int shift,
+                                                            int64_t n_sub, const int64_t* __restrict__ offsets,
+                                                            K* __restrict__ keys_out, Pos* __restrict__ pos_out) {
+  __shared__ int64_t s_off[kWavesPerBlock][kDigits];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t sub = (int64_t)blockIdx.x * kWavesPerBlock + w;
+  if (sub >= n_sub) return;
+  int64_t* off = s_off[w];
+  for (int d = lane; d < kDigits; d += 64) off[d] = offsets[(int64_t)d * n_sub + sub];
+  wave_sync_t();
+  const int64_t base = sub * kSub;
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int64_t e = base + (int64_t)ch * 64 + lane;
+    const bool valid = e < n;
+    const uint64_t active = __ballot(valid);
+    if (active == 0) break;
+    const K key = valid ? load_key<K>(keys_in, kind, e) : (K)0;
+    const Pos p = valid ? (pos_in ? pos_in[e] : (Pos)e) : (Pos)0;
+    const unsigned digit = (unsigned)(key >> shift) & (kDigits - 1);
+    const uint64_t peers = peer_mask(digit, active);
+    const int rank = count_below_t(peers);
+    int64_t dst = 0;
+    if (valid) dst = off[digit] + rank;
+    wave_sync_t();
+    if (valid) {
+      keys_out[dst] = key;
+      pos_out[dst] = p;
+      if (rank == 0) off[digit] = dst + __popcll(peers);
+    }
+    wave_sync_t();
+  }
+}
+
+// ---- exclusive scan over int64 (reduce -> scan partials -> downsweep) ----
+__device__ inline int64_t block_exclusive_scan(int64_t v, int64_t* s_wave, int64_t& total) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  int64_t x = v;
+  for (int off = 1; off < 64; off <<= 1) {
+    int lo = __builtin_amdgcn_ds_bpermute((lane - off) << 2, (int)(x & 0xffffffff));
+    int hi = __builtin_amdgcn_ds_bpermute((lane - off) << 2, (int)(x >> 32));
+    int64_t y = ((int64_t)hi << 32) | (uint32_t)lo;
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_wave[w] = x;
+  __syncthreads();
+  int64_t wave_base = 0;
+  total = 0;
+  for (int k = 0; k < (int)(blockDim.x >> 6); ++k) {
+    if (k < w) wave_base += s_wave[k];
+    total += s_wave[k];
+  }
+  __syncthreads();
+  return wave_base + x - v;
+}
+
+__global__ __launch_bounds__(256) void scan_reduce_kernel(const int64_t* __restrict__ in, int64_t n,
+                                                          int64_t* __restrict__ partial) {
+  __shared__ int64_t s_wave[4];
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  int64_t s = 0;
+  for (int k = 0; k < kScanItems; ++k)
+    if (base + k < n) s += in[base + k];
+  int64_t total;
+  block_exclusive_scan(s, s_wave, total);
+  if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(256) void scan_partials_kernel(int64_t* __restrict__ partial, int64_t n) {
+  __shared__ int64_t s_wave[4];
+  int64_t carry = 0;
+  for (int64_t b = 0; b < n; b += 256) {
+    const int64_t i = b + threadIdx.x;
+    const int64_t v = i < n ? partial[i] : 0;
+    int64_t total;
+    const int64_t ex = block_exclusive_scan(v, s_wave, total);
+    if (i < n) partial[i] = carry + ex;
+    carry += total;
+  }
+}
+
+__global__ __launch_bounds__(256) void scan_downsweep_kernel(int64_t* __restrict__ data, int64_t n,
+                                                             const int64_t* __restrict__ partial) {
+  __shared__ int64_t s_wave[4];
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  int64_t v[kScanItems];
+  int64_t s = 0;
+  for (int k = 0; k < kScanItems; ++k) {
+    v[k] = base + k < n ? data[base + k] : 0;
+    s += v[k];
+  }
+  int64_t total;
+  int64_t run = partial[blockIdx.x] + block_exclusive_scan(s, s_wave, total);
+  for (int k = 0; k < kScanItems; ++k) {
+    if (base + k < n) data[base + k] = run;
+    run += v[k];
+  }
+}
+
+// ---- row ids, gather, column pointer ----
+constexpr int kExpandItems = 16;
+
+template <class P, class OI>
+__global__ __launch_bounds__(256) void expand_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz,
+                                                          OI* __restrict__ rowid) {
+  const int64_t e0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kExpandItems;
+  if (e0 >= nnz) return;
+  // first row whose end exceeds e0
+  int64_t lo = 0, hi = n_rows - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)rowptr[mid + 1] <= e0)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  int64_t row = lo;
+  int64_t rend = (int64_t)rowptr[row + 1];
+  for (int k = 0; k < kExpandItems; ++k) {
+    const int64_t e = e0 + k;
+    if (e >= nnz) break;
+    while (rend <= e) {
+      ++row;
+      rend = (int64_t)rowptr[row + 1];
+    }
+    rowid[e] = (OI)row;
+  }
+}
+
+template <class V, class OI, class Pos>
+__global__ __launch_bounds__(256) void transpose_gather_kernel(const V* __restrict__ vals, const OI* __restrict__ rowid,
+                                                               const Pos* __restrict__ perm, int64_t nnz, int conj,
+                                                               V* __restrict__ t_vals, OI* __restrict__ t_cols) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= nnz) return;
+  const int64_t p = (int64_t)perm[k];
+  V v = vals[p];
+  if (conj) v = VT<V>::conj(v);
+  t_vals[k] = v;
+  t_cols[k] = rowid[p];
+}
+
+template <class K, class OP>
+__global__ __launch_bounds__(256) void colptr_kernel(const K* __restrict__ keys, int64_t nnz, int64_t n_cols,
+                                                     OP* __restrict__ colptr) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k > nnz) return;
+  const int64_t prev = k > 0 ? (int64_t)keys[k - 1] : -1;
+  const int64_t cur = k < nnz ? (int64_t)keys[k] : n_cols;
+  for (int64_t c = prev + 1; c <= cur; ++c) colptr[c] = (OP)k;
+}
+
+template <class OP>
+__global__ __launch_bounds__(256) void fill_kernel(OP* __restrict__ p, int64_t n, OP v) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < n) p[k] = v;
+}
+
+template <class K>
+__global__ __launch_bounds__(256) void identity_kernel(const void* __restrict__ cols, int kind, int64_t n,
+                                                       K* __restrict__ keys) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < n) keys[k] = load_key<K>(cols, kind, k);
+}
+
+// ---- host side ----
+struct Layout {
+  size_t key_bytes, pos_bytes, rowid_bytes;
+  int64_t n_sub, n_counts, n_partials;
+  size_t off_keys_a, off_keys_b, off_pos_a, off_pos_b, off_rowid, off_counts, off_partials, total;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz) {
+  Layout L{};
+  L.key_bytes = (n_cols > (int64_t)0xffffffffLL) ? 8 : 4;
+  L.pos_bytes = (nnz > (int64_t)0xffffffffLL) ? 8 : 4;
+  L.rowid_bytes = 8;  // sized for the widest output index type
+  L.n_sub = ceil_div(nnz, kSub);
+  L.n_counts = (int64_t)kDigits * L.n_sub;
+  L.n_partials = ceil_div(L.n_counts, kScanTile);
+  size_t o = 0;
+  L.off_keys_a = o; o = align256(o + L.key_bytes * nnz);
+  L.off_keys_b = o; o = align256(o + L.key_bytes * nnz);
+  L.off_pos_a = o; o = align256(o + L.pos_bytes * nnz);
+  L.off_pos_b = o; o = align256(o + L.pos_bytes * nnz);
+  L.off_rowid = o; o = align256(o + L.rowid_bytes * nnz);
+  L.off_counts = o; o = align256(o + sizeof(int64_t) * L.n_counts);
+  L.off_partials = o; o = align256(o + sizeof(int64_t) * (L.n_partials + 1));
+  L.total = o;
+  (void)n_rows;
+  return L;
+}
+
+int device_exclusive_scan(int64_t* data, int64_t n, int64_t* partial, hipStream_t s) {
+  if (n == 0) return FS_OK;
+  const int64_t blocks = ceil_div(n, kScanTile);
+  hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, data, n, partial);
+  FS_CHECK_LAUNCH("scan_reduce_kernel");
+  hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(256), 0, s, partial, blocks);
+  FS_CHECK_LAUNCH("scan_partials_kernel");
+  hipLaunchKernelGGL(scan_downsweep_kernel, dim3((unsigned)blocks), dim3(256), 0, s, data, n, partial);
+  FS_CHECK_LAUNCH("scan_downsweep_kernel");
+  return FS_OK;
+}
+
+int key_bits(int64_t n_cols) {
+  int b = 0;
+  while (b < 64 && ((n_cols - 1) >> b) > 0) ++b;  // bits needed for n_cols-1
+  return b;
+}
+
+template <class K, class Pos>
+int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, int64_t nnz, int64_t n_cols,
+                    const K** sorted_keys, const Pos** perm, hipStream_t s) {
+  K* ka = reinterpret_cast<K*>(ws + L.off_keys_a);
+  K* kb = reinterpret_cast<K*>(ws + L.off_keys_b);
+  Pos* pa = reinterpret_cast<Pos*>(ws + L.off_pos_a);
+  Pos* pb = reinterpret_cast<Pos*>(ws + L.off_pos_b);
+  int64_t* counts = reinterpret_cast<int64_t*>(ws + L.off_counts);
+  int64_t* partial = reinterpret_cast<int64_t*>(ws + L.off_partials);
+  const int passes = (key_bits(n_cols) + kRadixBits - 1) / kRadixBits;
+  const unsigned blocks = (unsigned)ceil_div(L.n_sub, kWavesPerBlock);
+  const void* kin = cols;
+  int kind = col_kind;
+  const Pos* pin = nullptr;  // identity on the first pass
+  K* kout = ka;
+  Pos* pout = pa;
+  if (passes == 0) {
+    hipLaunchKernelGGL((identity_kernel<K>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s, cols, col_kind,
+                       nnz, ka);
+    FS_CHECK_LAUNCH("identity_kernel");
+    *sorted_keys = ka;
+    *perm = nullptr;
+    return FS_OK;
+  }
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * kRadixBits;
+    hipLaunchKernelGGL((radix_count_kernel<K>), dim3(blocks), dim3(256), 0, s, kin, kind, nnz, shift, L.n_sub,
+                       counts);
+    FS_CHECK_LAUNCH("radix_count_kernel");
+    int rc = device_exclusive_scan(counts, L.n_counts, partial, s);
+    if (rc != FS_OK) return rc;
+    hipLaunchKernelGGL((radix_scatter_kernel<K, Pos>), dim3(blocks), dim3(256), 0, s, kin, kind, pin, nnz, shift,
+                       L.n_sub, counts, kout, pout);
+    FS_CHECK_LAUNCH("radix_scatter_kernel");
+    kin = kout;
+    kind = 2;
+    pin = pout;
+    kout = (kout == ka) ? kb : ka;
+    pout = (pout == pa) ? pb : pa;
+  }
+  *sorted_keys = static_cast<const K*>(kin);
+  *perm = pin;
+  return FS_OK;
+}
+
+template <class Pos>
+__global__ __launch_bounds__(256) void iota_kernel(Pos* __restrict__ p, int64_t n) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < n) p[k] = (Pos)k;
+}
+
+template <class V, class P, class OI, class OP, class K, class Pos>
+int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                    const void* vals, const void* cols, const void* indptr, int conj, void* t_vals, void* t_cols,
+                    void* t_indptr, hipStream_t s) {
+  const K* keys = nullptr;
+  const Pos* perm = nullptr;
+  int rc = radix_sort_cols<K, Pos>(L, ws, cols, idx_t == FS_I32 ? 0 : 1, nnz, n_cols, &keys, &perm, s);
+  if (rc != FS_OK) return rc;
+  if (perm == nullptr) {  // single column: order unchanged
+    Pos* pa = reinterpret_cast<Pos*>(ws + L.off_pos_a);
+    hipLaunchKernelGGL((iota_kernel<Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s, pa, nnz);
+    FS_CHECK_LAUNCH("iota_kernel");
+    perm = pa;
+  }
+  OI* rowid = reinterpret_cast<OI*>(ws + L.off_rowid);
+  hipLaunchKernelGGL((expand_rows_kernel<P, OI>), dim3((unsigned)ceil_div(ceil_div(nnz, kExpandItems), 256)),
+                     dim3(256), 0, s, static_cast<const P*>(indptr), n_rows, nnz, rowid);
+  FS_CHECK_LAUNCH("expand_rows_kernel");
+  hipLaunchKernelGGL((transpose_gather_kernel<V, OI, Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s,
+                     static_cast<const V*>(vals), rowid, perm, nnz, conj, static_cast<V*>(t_vals),
+                     static_cast<OI*>(t_cols));
+  FS_CHECK_LAUNCH("transpose_gather_kernel");
+  hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
+                     n_cols, static_cast<OP*>(t_indptr));
+  FS_CHECK_LAUNCH("colptr_kernel");
+  return FS_OK;
+}
+
+template <class V, class P, class OI, class OP>
+int transpose_keys(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                   const void* vals, const void* cols, const void* indptr, int conj, void* tv, void* tc, void* tp,
+                   hipStream_t s) {
+  if (L.key_bytes == 4 && L.pos_bytes == 4)
+    return transpose_typed<V, P, OI, OP, uint32_t, uint32_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr,
+                                                             conj, tv, tc, tp, s);
+  if (L.key_bytes == 4)
+    return transpose_typed<V, P, OI, OP, uint32_t, uint64_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr,
+                                                             conj, tv, tc, tp, s);
+  if (L.pos_bytes == 4)
+    return transpose_typed<V, P, OI, OP, uint64_t, uint32_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr,
+                                                             conj, tv, tc, tp, s);
+  return transpose_typed<V, P, OI, OP, uint64_t, uint64_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr,
+                                                           conj, tv, tc, tp, s);
+}
+
+template <class V, class P>
+int transpose_out(const Layout& L, char* ws, int idx_t, int oi, int op, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                  const void* vals, const void* cols, const void* indptr, int conj, void* tv, void* tc, void* tp,
+                  hipStream_t s) {
+  if (oi == FS_I32 && op == FS_I32)
+    return transpose_keys<V, P, int32_t, int32_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
+  if (oi == FS_I32)
+    return transpose_keys<V, P, int32_t, int64_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
+  if (op == FS_I32)
+    return transpose_keys<V, P, int64_t, int32_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
+  return transpose_keys<V, P, int64_t, int64_t>(L, ws, idx_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
+}
+
+template <class V>
+int transpose_ptr(const Layout& L, char* ws, int idx_t, int ptr_t, int oi, int op, int64_t n_rows, int64_t n_cols,
+                  int64_t nnz, const void* vals, const void* cols, const void* indptr, int conj, void* tv, void* tc,
+                  void* tp, hipStream_t s) {
+  if (ptr_t == FS_I32)
+    return transpose_out<V, int32_t>(L, ws, idx_t, oi, op, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
+  return transpose_out<V, int64_t>(L, ws, idx_t, oi, op, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t nnz) {
+  if (nnz <= 0) return 0;
+  return make_layout(n_rows, n_cols, nnz).total;
+}
+
+extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, int out_ptr_t, int64_t n_rows,
+                                int64_t n_cols, int64_t nnz, const void* vals, const void* cols, const void* indptr,
+                                int conj, void* t_vals, void* t_cols, void* t_indptr, void* ws, size_t ws_bytes,
+                                hipStream_t stream) {
+  if (!valid_types(val_t, idx_t, ptr_t) || !(out_idx_t == FS_I32 || out_idx_t == FS_I64) ||
+      !(out_ptr_t == FS_I32 || out_ptr_t == FS_I64))
+    return fail(FS_E_INVALID, "fs_csr_transpose: bad type code");
+  if (n_rows < 0 || n_cols < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_csr_transpose: negative size");
+  if (!t_indptr) return fail(FS_E_INVALID, "fs_csr_transpose: t_indptr is null");
+  if (nnz == 0) {
+    const int64_t n = n_cols + 1;
+    if (out_ptr_t == FS_I32)
+      hipLaunchKernelGGL((fill_kernel<int32_t>), dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream,
+                         static_cast<int32_t*>(t_indptr), n, 0);
+    else
+      hipLaunchKernelGGL((fill_kernel<int64_t>), dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream,
+                         static_cast<int64_t*>(t_indptr), n, (int64_t)0);
+    FS_CHECK_LAUNCH("fill_kernel");
+    return FS_OK;
+  }
+  if (!vals || !cols || !indptr || !t_vals || !t_cols) return fail(FS_E_INVALID, "fs_csr_transpose: null pointer");
+  if (n_rows == 0 || n_cols == 0) return fail(FS_E_INVALID, "fs_csr_transpose: nnz > 0 with an empty dimension");
+  const Layout L = make_layout(n_rows, n_cols, nnz);
+  if (!ws || ws_bytes < L.total) return fail(FS_E_WORKSPACE, "fs_csr_transpose: workspace too small");
+  char* w = static_cast<char*>(ws);
+  switch (val_t) {
+    case FS_F32: return transpose_ptr<float>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
+    case FS_F64: return transpose_ptr<double>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
+    case FS_C64: return transpose_ptr<c32>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
+    default: return transpose_ptr<c64>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
+  }
+}

@@ -1,0 +1,537 @@
+"""CSR SpMV operators: the reference's public API on gfx950 HIP kernels.
+
+Public surface and behaviour follow src/flagsparse/sparse_operations/
+spmv_csr.py of the reference:
+  flagsparse_spmv_csr            spmv_csr.py:813-913
+  prepare_spmv_csr               spmv_csr.py:591-664
+  PreparedCsrSpmv                spmv_csr.py:55-130
+  op normalisation               spmv_csr.py:29-52
+  validation                     spmv_csr.py:518-588
+  int64 -> int32 index fallback  spmv_csr.py:464-468, 726-810
+  COO -> CSR convenience         spmv_csr.py:916-1057
+Error types and messages are the reference's, so its contract tests apply
+unchanged.  The device work (transpose, analysis, SpMV) is one call each
+into libflagsparse_hip; there is no CPU path.
+"""
+
+import time
+
+import torch
+
+from . import _lib
+from ._common import (
+    _INDEX_LIMIT_INT32,
+    SUPPORTED_INDEX_DTYPES,
+    _compute_dtype,
+    _is_complex_dtype,
+)
+from ._csr import analyze_csr, transpose_csr
+
+SUPPORTED_SPMV_VALUE_DTYPES = (
+    torch.float16,
+    torch.bfloat16,
+    torch.float32,
+    torch.float64,
+    torch.complex64,
+    torch.complex128,
+)
+
+SPMV_OP_NON = 0
+SPMV_OP_TRANS = 1
+SPMV_OP_CONJ_TRANS = 2
+SPMV_OP_NAMES = {
+    SPMV_OP_NON: "non",
+    SPMV_OP_TRANS: "trans",
+    SPMV_OP_CONJ_TRANS: "conj",
+}
+_SPMV_OP_NAME_TO_CODE = {name: code for code, name in SPMV_OP_NAMES.items()}
+_OP_ERROR = "op must be one of: 0=non, 1=trans, 2=conj"
+
+
+def _normalize_spmv_op(op=None, transpose=False):
+    """None -> trans if transpose else non; 'non'|'trans'|'conj' or 0|1|2."""
+    if op is None:
+        return SPMV_OP_TRANS if bool(transpose) else SPMV_OP_NON
+    if isinstance(op, str):
+        code = _SPMV_OP_NAME_TO_CODE.get(op.strip().lower())
+        if code is None:
+            raise ValueError(_OP_ERROR)
+        return code
+    try:
+        code = int(op)
+    except (TypeError, ValueError) as exc:
+        raise ValueError(_OP_ERROR) from exc
+    if code not in SPMV_OP_NAMES:
+        raise ValueError(_OP_ERROR)
+    return code
+
+
+def _spmv_op_to_name(op):
+    return SPMV_OP_NAMES[_normalize_spmv_op(op)]
+
+
+def _spmv_op_transposes(op):
+    return _normalize_spmv_op(op) in (SPMV_OP_TRANS, SPMV_OP_CONJ_TRANS)
+
+
+class PreparedCsrSpmv:
+    """Cached CSR metadata for repeated SpMV calls on the same sparse matrix.
+
+    Holds the (possibly transposed) matrix, the row-length analysis and the
+    merge-path partition / carry workspace the HIP kernel needs.
+    """
+
+    __slots__ = (
+        "data",
+        "kernel_indices",
+        "kernel_indptr",
+        "shape",
+        "n_rows",
+        "n_cols",
+        "block_nnz",
+        "max_segments",
+        "opt_max_segments",
+        "row_lengths",
+        "max_row_nnz",
+        "opt_buckets",
+        "supports_opt",
+        "transpose",
+        "op",
+        "index_fallback_policy",
+        "index_fallback_applied",
+        "index_fallback_reason",
+        "_compute_data",
+        "_plan",
+        "_part",
+        "_carry",
+    )
+
+    def __init__(
+        self,
+        data,
+        kernel_indices,
+        kernel_indptr,
+        shape,
+        n_rows,
+        n_cols,
+        block_nnz,
+        max_segments,
+        max_row_nnz,
+        opt_buckets=None,
+        opt_max_segments=None,
+        row_lengths=None,
+        transpose=False,
+        op=None,
+        index_fallback_policy="auto",
+        index_fallback_applied=False,
+        index_fallback_reason=None,
+    ):
+        self.data = data
+        self.kernel_indices = kernel_indices
+        self.kernel_indptr = kernel_indptr
+        self.shape = (int(shape[0]), int(shape[1]))
+        self.n_rows = n_rows
+        self.n_cols = n_cols
+        self.block_nnz = block_nnz
+        self.max_segments = max_segments
+        self.opt_max_segments = opt_max_segments
+        if row_lengths is None:
+            row_lengths = kernel_indptr[1:] - kernel_indptr[:-1]
+        self.row_lengths = row_lengths
+        self.max_row_nnz = max_row_nnz
+        self.opt_buckets = [] if opt_buckets is None else opt_buckets
+        self.supports_opt = (
+            data.dtype in (torch.float32, torch.float64) and kernel_indices.dtype == torch.int32
+        )
+        self.op = _normalize_spmv_op(op, transpose=transpose)
+        self.transpose = _spmv_op_transposes(self.op)
+        self.index_fallback_policy = str(index_fallback_policy).lower()
+        self.index_fallback_applied = bool(index_fallback_applied)
+        self.index_fallback_reason = index_fallback_reason
+        self._compute_data = None
+        self._plan = None
+        self._part = None
+        self._carry = None
+
+    # -- HIP plan (built lazily on first run, then cached) ------------------
+    def hip_plan(self):
+        if self._plan is None:
+            data = self.compute_data()
+            self._plan = analyze_csr(
+                data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols
+            )
+            p = self._plan.plan
+            if p.kernel == _lib.FS_KERNEL_MERGE:
+                self._part = self._plan.partition(self.kernel_indptr, int(p.tile_items))
+                self._carry = _lib.workspace(p.carry_bytes, data.device)
+        return self._plan
+
+    def compute_data(self):
+        """Values in the dtype the kernel runs in (f16/bf16 -> f32, cached)."""
+        cdt = _compute_dtype(self.data.dtype)
+        if cdt == self.data.dtype:
+            return self.data
+        if self._compute_data is None or self._compute_data.dtype != cdt:
+            self._compute_data = self.data.to(cdt)
+        return self._compute_data
+
+    @property
+    def kernel_name(self):
+        return self.hip_plan().kernel_name
+
+
+def _normalize_spmv_index_fallback_policy(index_fallback_policy):
+    policy = str(index_fallback_policy).lower()
+    if policy not in ("auto", "strict"):
+        raise ValueError("index_fallback_policy must be 'auto' or 'strict'")
+    return policy
+
+
+def _spmv_dtype_error_message():
+    return "data dtype must be one of: " + ", ".join(
+        str(dtype).replace("torch.", "") for dtype in SUPPORTED_SPMV_VALUE_DTYPES
+    )
+
+
+def _transpose_csr_for_spmv(data, indices, indptr, shape):
+    """CSR of A^T, stable by column (reference: spmv_csr.py:477-515)."""
+    return transpose_csr(data, indices, indptr, shape, conj=False)
+
+
+def _check_structure(data, indices, indptr, n_cols, messages):
+    """indptr / index checks with one device->host transfer.
+
+    The reference checks indptr[0], indptr[-1], monotonicity and the column
+    range with separate .item() syncs (spmv_csr.py:546-558); the checks and
+    the order in which their errors are raised are kept, the syncs merged.
+    """
+    nnz = data.numel()
+    if indptr.numel() == 0:
+        return
+    probes = [indptr[:1].to(torch.int64), indptr[-1:].to(torch.int64)]
+    if indptr.numel() > 1:
+        probes.append(torch.any(indptr[1:] < indptr[:-1]).reshape(1).to(torch.int64))
+    else:
+        probes.append(torch.zeros(1, dtype=torch.int64, device=indptr.device))
+    if nnz > 0:
+        probes.append(indices.min().reshape(1).to(torch.int64))
+        probes.append(indices.max().reshape(1).to(torch.int64))
+    vals = torch.cat(probes).cpu().tolist()
+    if int(vals[0]) != 0:
+        raise ValueError(messages["start"])
+    if int(vals[1]) != nnz:
+        raise ValueError(messages["last"](int(vals[1])))
+    if int(vals[2]) != 0:
+        raise ValueError(messages["monotone"])
+    if nnz > 0:
+        if int(vals[3]) < 0 or int(vals[4]) >= n_cols:
+            raise IndexError("indices out of range for n_cols")
+        return int(vals[3]), int(vals[4])
+    return None
+
+
+_SPMV_STRUCT_MESSAGES = {
+    "start": "indptr must start at zero",
+    "last": lambda got: "indptr[-1] must equal nnz",
+    "monotone": "indptr must be non-decreasing",
+}
+
+
+def _prepare_spmv_csr_matrix(data, indices, indptr, shape, index_fallback_policy="auto"):
+    """Validation of spmv_csr.py:518-572 (same order, types and messages)."""
+    _normalize_spmv_index_fallback_policy(index_fallback_policy)
+    if not all(torch.is_tensor(t) for t in (data, indices, indptr)):
+        raise TypeError("data, indices, indptr must all be torch.Tensor")
+    if data.ndim != 1 or indices.ndim != 1 or indptr.ndim != 1:
+        raise ValueError("data, indices, indptr must be 1D tensors")
+    n_rows, n_cols = int(shape[0]), int(shape[1])
+    if indptr.numel() != n_rows + 1:
+        raise ValueError(f"indptr length must be n_rows+1={n_rows + 1}, got {indptr.numel()}")
+    if data.numel() != indices.numel():
+        raise ValueError("data and indices must have the same length (nnz)")
+    if not all(t.is_cuda for t in (data, indices, indptr)):
+        raise ValueError("data, indices, indptr must be CUDA tensors")
+    if not all(t.device == data.device for t in (indices, indptr)):
+        raise ValueError("data, indices, indptr must be on the same CUDA device")
+    if data.dtype not in SUPPORTED_SPMV_VALUE_DTYPES:
+        raise TypeError(_spmv_dtype_error_message())
+    if indices.dtype not in SUPPORTED_INDEX_DTYPES:
+        raise TypeError("indices dtype must be torch.int32 or torch.int64")
+    if indptr.dtype not in SUPPORTED_INDEX_DTYPES:
+        raise TypeError("indptr dtype must be torch.int32 or torch.int64")
+
+    data = data.contiguous()
+    indices = indices.contiguous()
+    indptr = indptr.contiguous()
+    _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
+    row_lengths = indptr[1:] - indptr[:-1]
+    return data, indices, indptr, n_rows, n_cols, row_lengths
+
+
+def _validate_spmv_x(x, prepared):
+    """spmv_csr.py:575-588."""
+    if x is None or not torch.is_tensor(x):
+        raise TypeError("x must be a torch.Tensor")
+    if x.ndim != 1:
+        raise ValueError("x must be a 1D tensor")
+    if not x.is_cuda:
+        raise ValueError("x must be a CUDA tensor")
+    if x.dtype != prepared.data.dtype:
+        raise TypeError("x dtype must match sparse matrix dtype")
+    if x.numel() != prepared.n_cols:
+        raise ValueError(f"x length must be n_cols={prepared.n_cols}, got {x.numel()}")
+    if x.device != prepared.data.device:
+        raise ValueError("x must be on the same device as sparse matrix data")
+    return x.contiguous()
+
+
+def prepare_spmv_csr(
+    data,
+    indices,
+    indptr,
+    shape,
+    block_nnz=256,
+    max_segments=None,
+    transpose=False,
+    op=None,
+    index_fallback_policy="auto",
+):
+    """Validate, transpose for op=trans/conj, analyse and cache (spmv_csr.py:591-664).
+
+    block_nnz / max_segments keep the reference's meaning for callers that
+    read them back; the HIP kernels do not iterate fixed segments, so they
+    do not limit which rows can be processed.
+    """
+    index_fallback_policy = _normalize_spmv_index_fallback_policy(index_fallback_policy)
+    op_code = _normalize_spmv_op(op, transpose=transpose)
+    if op is not None and bool(transpose) and op_code == SPMV_OP_NON:
+        raise ValueError("transpose=True conflicts with op=non")
+    transposes = _spmv_op_transposes(op_code)
+    if transposes:
+        data, indices, indptr, *_ = _prepare_spmv_csr_matrix(
+            data, indices, indptr, shape, index_fallback_policy=index_fallback_policy
+        )
+        data, indices, indptr, shape = transpose_csr(
+            data, indices, indptr, shape, conj=(op_code == SPMV_OP_CONJ_TRANS)
+        )
+    data, indices, indptr, n_rows, n_cols, row_lengths = _prepare_spmv_csr_matrix(
+        data, indices, indptr, shape, index_fallback_policy=index_fallback_policy
+    )
+    prepared = PreparedCsrSpmv(
+        data=data,
+        kernel_indices=indices,
+        kernel_indptr=indptr,
+        shape=shape,
+        n_rows=n_rows,
+        n_cols=n_cols,
+        block_nnz=block_nnz,
+        max_segments=1,
+        opt_max_segments=max_segments,
+        row_lengths=row_lengths,
+        max_row_nnz=0,
+        opt_buckets=None,
+        transpose=transposes,
+        op=op_code,
+        index_fallback_policy=index_fallback_policy,
+    )
+    if n_rows > 0:
+        plan = prepared.hip_plan()
+        max_row = plan.max_row_nnz
+    else:
+        max_row = 0
+    prepared.max_row_nnz = max_row
+    # Segment sizing as the reference reports it (spmv_csr.py:637-647).
+    block_nnz_use = block_nnz
+    if max_segments is None:
+        segs = max((max_row + block_nnz_use - 1) // block_nnz_use, 1)
+        while segs > 2048 and block_nnz_use < 65536:
+            block_nnz_use *= 2
+            segs = max((max_row + block_nnz_use - 1) // block_nnz_use, 1)
+    else:
+        segs = max_segments
+    prepared.block_nnz = block_nnz_use
+    prepared.max_segments = segs
+    return prepared
+
+
+def _hip_spmv_csr_impl_prepared(prepared, x):
+    """One SpMV launch (replaces _triton_spmv_csr_impl_prepared, spmv_csr.py:679-723)."""
+    device = prepared.data.device
+    dtype = prepared.data.dtype
+    y = torch.empty(prepared.n_rows, dtype=dtype, device=device)
+    if prepared.n_rows == 0:
+        return y
+    data = prepared.compute_data()
+    cdt = data.dtype
+    x_in = x if x.dtype == cdt else x.to(cdt)
+    y_out = y if cdt == dtype else torch.empty(prepared.n_rows, dtype=cdt, device=device)
+    plan = prepared.hip_plan()
+    carry = prepared._carry
+    _lib.check(
+        _lib.lib().fs_spmv_csr(
+            plan.plan,
+            _lib.ptr(data),
+            _lib.ptr(prepared.kernel_indices),
+            _lib.ptr(prepared.kernel_indptr),
+            _lib.ptr(x_in),
+            _lib.ptr(y_out),
+            _lib.ptr(prepared._part),
+            _lib.ptr(carry),
+            0 if carry is None else carry.numel(),
+            _lib.stream_handle(device),
+        ),
+        "fs_spmv_csr",
+    )
+    if y_out is not y:
+        y.copy_(y_out)
+    return y
+
+
+def _spmv_uses_int64_indices(prepared):
+    return prepared.kernel_indices.dtype == torch.int64 or prepared.kernel_indptr.dtype == torch.int64
+
+
+def _spmv_int32_fallback_blocker(prepared):
+    """Reason the int32 re-run would be unsafe, or None (spmv_csr.py:733-754)."""
+    if prepared.kernel_indices.dtype == torch.int64 and prepared.kernel_indices.numel() > 0:
+        lo_hi = torch.stack([prepared.kernel_indices.min(), prepared.kernel_indices.max()]).cpu().tolist()
+        min_index, max_index = int(lo_hi[0]), int(lo_hi[1])
+        if min_index < 0 or max_index > _INDEX_LIMIT_INT32:
+            return f"column index range [{min_index}, {max_index}] cannot fit int32 for shape={prepared.shape}"
+    if prepared.kernel_indptr.dtype == torch.int64 and prepared.kernel_indptr.numel() > 0:
+        max_offset = int(prepared.kernel_indptr[-1].item())
+        if max_offset > _INDEX_LIMIT_INT32:
+            return f"CSR nnz offset {max_offset} cannot fit int32 for shape={prepared.shape}"
+    if prepared.n_rows > _INDEX_LIMIT_INT32:
+        return f"row count {prepared.n_rows} cannot fit int32 row metadata"
+    return None
+
+
+def _spmv_prepared_with_int32_indices(prepared, reason):
+    blocker = _spmv_int32_fallback_blocker(prepared)
+    if blocker is not None:
+        raise RuntimeError(f"native int64 CSR SpMV failed and int32 fallback is unsafe: {blocker}")
+    kernel_indices = prepared.kernel_indices.to(torch.int32)
+    kernel_indptr = prepared.kernel_indptr.to(torch.int32)
+    out = PreparedCsrSpmv(
+        data=prepared.data,
+        kernel_indices=kernel_indices,
+        kernel_indptr=kernel_indptr,
+        shape=prepared.shape,
+        n_rows=prepared.n_rows,
+        n_cols=prepared.n_cols,
+        block_nnz=prepared.block_nnz,
+        max_segments=prepared.max_segments,
+        opt_max_segments=prepared.opt_max_segments,
+        row_lengths=kernel_indptr[1:] - kernel_indptr[:-1],
+        max_row_nnz=prepared.max_row_nnz,
+        opt_buckets=None,
+        transpose=prepared.transpose,
+        op=prepared.op,
+        index_fallback_policy=prepared.index_fallback_policy,
+        index_fallback_applied=True,
+        index_fallback_reason=str(reason),
+    )
+    return out
+
+
+def _run_spmv_prepared(prepared, x, use_opt=False, opt_buckets=None):
+    # use_opt selects the same HIP kernels: their accumulation is already the
+    # accurate one and the variant choice comes from the analysis.
+    return _hip_spmv_csr_impl_prepared(prepared, x)
+
+
+def _run_spmv_prepared_with_fallback(prepared, x, use_opt=False, opt_buckets=None):
+    try:
+        return _run_spmv_prepared(prepared, x, use_opt=use_opt, opt_buckets=opt_buckets)
+    except Exception as exc:
+        if prepared.index_fallback_policy != "auto" or not _spmv_uses_int64_indices(prepared):
+            raise
+        fallback = _spmv_prepared_with_int32_indices(prepared, exc)
+        return _run_spmv_prepared(fallback, x, use_opt=use_opt)
+
+
+def flagsparse_spmv_csr(
+    data=None,
+    indices=None,
+    indptr=None,
+    x=None,
+    shape=None,
+    block_nnz=256,
+    max_segments=None,
+    out=None,
+    return_time=False,
+    return_meta=False,
+    use_opt=False,
+    prepared=None,
+    transpose=None,
+    op=None,
+    index_fallback_policy="auto",
+):
+    """CSR SpMV y = op(A) @ x on the HIP kernels.
+
+    op: 0/'non' for A @ x, 1/'trans' for A.T @ x, 2/'conj' for A.conj().T @ x.
+    prepared: cached metadata from prepare_spmv_csr for steady-state runs.
+    Returns y, (y, ms), (y, meta) or (y, ms, meta) like spmv_csr.py:813-913.
+    """
+    op_explicit = op is not None
+    op_code = _normalize_spmv_op(op, transpose=False if transpose is None else bool(transpose))
+    if op_explicit and transpose is not None and bool(transpose) != _spmv_op_transposes(op_code):
+        raise ValueError("transpose conflicts with op")
+    if prepared is None:
+        if any(arg is None for arg in (data, indices, indptr, shape)):
+            raise ValueError("data, indices, indptr, and shape are required when prepared is not provided")
+        prepared = prepare_spmv_csr(
+            data,
+            indices,
+            indptr,
+            shape,
+            block_nnz=block_nnz,
+            max_segments=max_segments,
+            op=op_code,
+            index_fallback_policy=index_fallback_policy,
+        )
+    else:
+        if op_explicit and op_code != prepared.op:
+            raise ValueError(
+                f"op={_spmv_op_to_name(op_code)} does not match prepared.op={_spmv_op_to_name(prepared.op)}"
+            )
+        if not op_explicit and transpose is not None and bool(transpose) != prepared.transpose:
+            raise ValueError(
+                f"transpose={bool(transpose)} does not match prepared.transpose={prepared.transpose}"
+            )
+    x = _validate_spmv_x(x, prepared)
+    do_timing = bool(return_time or return_meta)
+    symbolic_ms = compute_ms = op_total_ms = None
+    if do_timing:
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        symbolic_ms = 0.0
+    y = _run_spmv_prepared_with_fallback(prepared, x, use_opt=use_opt)
+    if do_timing:
+        torch.cuda.synchronize()
+        compute_ms = (time.perf_counter() - t1) * 1000.0
+        op_total_ms = symbolic_ms + compute_ms
+    if out is not None:
+        if not out.is_cuda:
+            raise ValueError("out must be a CUDA tensor")
+        if out.device != y.device:
+            raise ValueError("out must be on the same CUDA device as the result")
+        if out.shape != y.shape or out.dtype != y.dtype:
+            raise ValueError("out shape/dtype must match result")
+        out.copy_(y)
+        y = out
+    if return_meta:
+        meta = {
+            "symbolic_ms": symbolic_ms,
+            "compute_ms": compute_ms,
+            "op_total_ms": op_total_ms,
+            "bucket_count": 1 if (use_opt and prepared.supports_opt) else 0,
+            "kernel": prepared.kernel_name if prepared.n_rows > 0 else None,
+        }
+        if return_time:
+            return y, op_total_ms, meta
+        return y, meta
+    if return_time:
+        return y, op_total_ms
+    return y

@@ -1,0 +1,154 @@
+/*
+ * flagsparse_hip.h — C ABI of the MI355X (gfx950) CSR SpMV / SpMM library.
+ *
+ * The library replaces the device half of FlagSparse's CSR SpMV/SpMM path.
+ * In the reference that half is a set of Triton kernels launched from
+ * Python (src/flagsparse/sparse_operations/spmv_csr.py,
+ * spmm_csr.py); here it is hand-written HIP for gfx950 behind plain C
+ * functions.  The Python host layer (flagsparse_amd/) keeps the reference's
+ * public signatures and calls only these entry points.
+ *
+ * Conventions shared by every entry point:
+ *   - all array arguments are raw device pointers; sizes are int64_t;
+ *   - value / index types are passed as the enums below;
+ *   - every launch goes to the caller's hipStream_t and returns without
+ *     synchronising, except fs_csr_analyze (documented below);
+ *   - nothing is allocated: scratch memory comes from a caller workspace
+ *     whose size the matching *_workspace_bytes / plan fields report;
+ *   - the return value is 0 on success, a negative FS_E* code otherwise;
+ *     fs_last_error() returns a human-readable message for the calling
+ *     thread's last failure.
+ *   - op=trans/conj are expressed by transposing first (fs_csr_transpose),
+ *     exactly as the reference materialises A^T / A^H before its kernel.
+ */
+#ifndef FLAGSPARSE_HIP_H
+#define FLAGSPARSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Value types: the reference's SUPPORTED_VALUE_DTYPES minus f16/bf16
+ * (sparse_operations/_common.py:21-28). */
+enum fs_value_type { FS_F32 = 0, FS_F64 = 1, FS_C64 = 2, FS_C128 = 3 };
+/* Index types: SUPPORTED_INDEX_DTYPES (_common.py:29). */
+enum fs_index_type { FS_I32 = 0, FS_I64 = 1 };
+
+enum fs_status {
+  FS_OK = 0,
+  FS_E_INVALID = -1,   /* bad argument (type code, size, null pointer) */
+  FS_E_WORKSPACE = -2, /* caller workspace too small */
+  FS_E_HIP = -3        /* a HIP runtime call failed */
+};
+
+/* Kernel variants chosen by fs_csr_analyze. */
+enum fs_kernel { FS_KERNEL_VECTOR = 0, FS_KERNEL_MERGE = 1 };
+
+#define FS_HIST_BINS 24 /* bin b counts rows with length in [2^(b-1), 2^b); bin 0 = empty rows */
+
+/* Analysis result for one CSR matrix (plain data, host memory). */
+typedef struct fs_csr_plan {
+  int64_t n_rows, n_cols, nnz;
+  int32_t val_t, idx_t, ptr_t;
+  int32_t kernel;        /* FS_KERNEL_* chosen for SpMV */
+  int32_t vec_width;     /* lanes per row for FS_KERNEL_VECTOR */
+  int32_t tile_items;    /* merge-path items (rows + nnz) per tile */
+  int64_t n_tiles;       /* merge-path tiles */
+  int64_t max_row, min_row;
+  int64_t hist[FS_HIST_BINS];
+  size_t part_bytes;     /* device bytes for the merge-path partition */
+  size_t carry_bytes;    /* device bytes for merge-path carries (SpMV) */
+} fs_csr_plan;
+
+/* Last error message of the calling thread ("" if none). */
+const char* fs_last_error(void);
+
+/* Library version string. */
+const char* fs_version(void);
+
+/*
+ * Row-length statistics of a device CSR row pointer, and the SpMV kernel
+ * choice made from them.  Replaces the reference's host-side preparation
+ * (spmv_csr.py:591-664: max_row_nnz, block_nnz / max_segments sizing;
+ * opt buckets spmv_csr.py:353-410).  Runs one histogram kernel into
+ * `stats_dev` (>= fs_csr_stats_bytes() bytes of device memory), then
+ * synchronises `stream` and decides on the host.  force_kernel < 0 lets the
+ * analysis choose; 0/1 forces FS_KERNEL_VECTOR / FS_KERNEL_MERGE.
+ */
+size_t fs_csr_stats_bytes(void);
+int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t,
+                   int64_t n_rows, int64_t n_cols, int64_t nnz,
+                   int force_kernel, void* stats_dev, fs_csr_plan* plan,
+                   hipStream_t stream);
+
+/*
+ * Merge-path partition: for each tile t, the row coordinate where the
+ * tile's merge path starts.  Writes plan->n_tiles+1 int64 into part_dev
+ * (plan->part_bytes bytes).
+ */
+int fs_csr_partition(const fs_csr_plan* plan, const void* indptr,
+                     void* part_dev, int tile_items, int64_t n_tiles,
+                     hipStream_t stream);
+
+/*
+ * y = A x for a CSR A (n_rows x n_cols).  Replaces
+ * _triton_spmv_csr_impl_prepared (spmv_csr.py:679-723) and the opt path
+ * (spmv_csr.py:412-461).  fp32 accumulates in fp64 and rounds once, like the
+ * reference's fp32 base path (spmv_csr.py:124-130, 685-705); complex64
+ * accumulates in fp64 components.  For FS_KERNEL_MERGE, part_dev is the
+ * fs_csr_partition output and carry_dev holds plan->carry_bytes.
+ */
+int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
+                const void* indptr, const void* x, void* y,
+                const void* part_dev, void* carry_dev, size_t carry_bytes,
+                hipStream_t stream);
+
+/*
+ * C = A B, A CSR (n_rows x n_cols), B dense n_cols x n_dense with row stride
+ * ldb (elements), C dense n_rows x n_dense with row stride ldc.  Replaces
+ * _triton_spmm_csr_impl + _spmm_csr_real_kernel / _spmm_csr_complex_kernel
+ * (spmm_csr.py:2684-2789, 134-237).  fp32 accumulates in fp64 (the
+ * reference upcasts data and B to fp64, spmm_csr.py:2720-2759).  The
+ * matrix is walked along a merge path of tile_items items per tile
+ * (partition from fs_csr_partition with the same tile size); rows that
+ * cross tiles are finished by a fix-up pass using `ws`
+ * (fs_spmm_workspace_bytes bytes).
+ */
+size_t fs_spmm_workspace_bytes(int val_t, int64_t n_tiles, int64_t n_dense);
+int fs_spmm_tile_items(int val_t, int64_t n_dense);
+int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
+                const void* indptr, const void* B, int64_t ldb, void* C,
+                int64_t ldc, int64_t n_dense, const void* part_dev,
+                int tile_items, int64_t n_tiles, void* ws, size_t ws_bytes,
+                hipStream_t stream);
+
+/*
+ * Transpose (CSR -> CSR of A^T, conjugating values when conj != 0).
+ * Replaces _transpose_csr_for_spmv / _transpose_csr_for_spmm
+ * (spmv_csr.py:477-515, spmm_csr.py:300-349) and the conj step
+ * (spmv_csr.py:615-618, spmm_csr.py:341-349).  The result is identical to a
+ * stable sort of the entries by column: within each output row the entries
+ * keep ascending source-row order.  Built atomic-free by an LSD radix sort
+ * on the column index (per-tile digit counts, scan, stable scatter).
+ * Output types: out_idx_t / out_ptr_t (the reference's rules: indices keep
+ * their type unless n_rows > 2^31-1, indptr keeps its type unless
+ * nnz > 2^31-1).
+ */
+size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_cols,
+                                        int64_t nnz);
+int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t,
+                     int out_ptr_t, int64_t n_rows, int64_t n_cols,
+                     int64_t nnz, const void* vals, const void* cols,
+                     const void* indptr, int conj, void* t_vals,
+                     void* t_cols, void* t_indptr, void* ws, size_t ws_bytes,
+                     hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLAGSPARSE_HIP_H */

@@ -1,0 +1,243 @@
+"""GPU parity of CSR SpMV (HIP kernels vs the CPU oracle and dense references).
+
+Mirrors the reference's accuracy suite (tests/pytest/test_spmv_csr_accuracy.py:
+98-233): every value dtype x index dtype x op, prepared-plan contracts and
+the int64 -> int32 fallback policy; plus both kernel variants, edge cases
+(empty rows / matrix, a 50,000-nnz row) and full-size properties.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import flagsparse_amd as fs
+from flagsparse_amd import spmv_csr as spmv_mod
+from flagsparse_amd import synthetic as S
+from oracle import csr_oracle as O
+from tests._helpers import (
+    ELEM_TOL,
+    INDEX_DTYPES,
+    INDEX_IDS,
+    OPS,
+    REL_TOL,
+    VALUE_DTYPES,
+    VALUE_IDS,
+    np_,
+    rel_err,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["auto", "vector", "merge"])
+def kernel_choice(request, monkeypatch):
+    if request.param != "auto":
+        monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", request.param)
+    else:
+        monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
+    return request.param
+
+
+def _check_spmv(data, indices, indptr, shape, x, op, kernel=None):
+    y = fs.flagsparse_spmv_csr(data, indices, indptr, x, shape, op=op)
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), shape, op=op)
+    assert y.dtype == data.dtype
+    assert tuple(y.shape) == (ref.shape[0],)
+    err = rel_err(np_(y), ref)
+    assert err <= REL_TOL[data.dtype], f"rel err {err:.3e} (kernel={kernel})"
+    return y, ref
+
+
+SHAPES = [(1, 32), (160, 1024), (128, 256), (777, 3001), (4099, 517)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{m}x{n}" for m, n in SHAPES])
+@pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+@pytest.mark.parametrize("op", OPS)
+def test_spmv_matches_oracle(kernel_choice, device, shape, dtype, index_dtype, op):
+    m, n = shape
+    long_rows = ((m // 2, min(n - 1, 2900)),) if m > 100 else ()
+    data, indices, indptr, sh = S.random_csr(m, n, 0.05, dtype, index_dtype, device, seed=m + n,
+                                             empty_row_every=7 if m > 7 else 0, long_rows=long_rows)
+    x = S.vector(m if op != "non" else n, dtype, device, seed=3)
+    _check_spmv(data, indices, indptr, sh, x, op, kernel_choice)
+
+
+def _reference_style_csr(M, N, dtype, index_dtype, device):
+    # Dense-masked random matrix as in test_spmv_csr_accuracy.py:53-69.
+    g = torch.Generator(device=device)
+    g.manual_seed(M * 1000 + N)
+    p = min(0.25, max(0.06, 32.0 / max(M * N, 1)))
+    mask = torch.rand(M, N, device=device, generator=g) < p
+    if int(mask.sum().item()) == 0:
+        mask[0, 0] = True
+    vals = S.dense(M, N, dtype, device, seed=M + 7 * N, dist="normal")
+    dense = torch.where(mask, vals, torch.zeros((), dtype=dtype, device=device))
+    rows, cols = torch.nonzero(mask, as_tuple=True)
+    data = dense[rows, cols].contiguous()
+    indptr = torch.zeros(M + 1, dtype=torch.int64, device=device)
+    indptr[1:] = torch.cumsum(torch.bincount(rows, minlength=M), 0)
+    return data, cols.to(index_dtype).contiguous(), indptr.to(index_dtype), dense
+
+
+@pytest.mark.parametrize("M,N", [(1, 32), (160, 1024), (128, 256)])
+@pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+@pytest.mark.parametrize("op", OPS)
+def test_spmv_matches_dense_reference(device, M, N, dtype, index_dtype, op):
+    """The reference's own accuracy test, with its tolerance (allclose vs dense)."""
+    data, indices, indptr, dense = _reference_style_csr(M, N, dtype, index_dtype, device)
+    x = S.vector(M if op != "non" else N, dtype, device, seed=11)
+    wide = torch.complex128 if dtype.is_complex else torch.float64
+    mat = {"non": dense, "trans": dense.t(), "conj": dense.conj().t()}[op]
+    ref = (mat.to(wide) @ x.to(wide)).to(dtype)
+    out = fs.flagsparse_spmv_csr(data, indices, indptr, x, shape=(M, N), op=op, index_fallback_policy="auto")
+    tol = ELEM_TOL[dtype]
+    assert torch.allclose(out.to(wide), ref.to(wide), rtol=tol, atol=tol)
+
+
+def test_spmv_golden_fixtures(device):
+    """Committed fixtures (tests/golden/spmv_*.npz) reproduce exactly."""
+    import glob
+
+    files = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "spmv_*.npz")))
+    assert files, "golden fixtures missing"
+    for f in files:
+        z = np.load(f, allow_pickle=False)
+        d = torch.from_numpy(z["data"]).to(device)
+        i = torch.from_numpy(z["indices"]).to(device)
+        p = torch.from_numpy(z["indptr"]).to(device)
+        x = torch.from_numpy(z["x"]).to(device)
+        shape = tuple(int(v) for v in z["shape"])
+        op = str(z["op"])
+        y = fs.flagsparse_spmv_csr(d, i, p, x, shape, op=op)
+        err = rel_err(np_(y), z["y_wide"])
+        assert err <= REL_TOL[d.dtype], f"{os.path.basename(f)}: rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
+def test_spmv_edge_cases(kernel_choice, device, dtype):
+    # empty matrix (nnz = 0): zeros
+    indptr = torch.zeros(6, dtype=torch.int32, device=device)
+    data = torch.empty(0, dtype=dtype, device=device)
+    idx = torch.empty(0, dtype=torch.int32, device=device)
+    x = S.vector(4, dtype, device)
+    y = fs.flagsparse_spmv_csr(data, idx, indptr, x, (5, 4))
+    assert torch.count_nonzero(y).item() == 0 and y.shape == (5,)
+    # zero rows
+    y = fs.flagsparse_spmv_csr(data, idx, torch.zeros(1, dtype=torch.int32, device=device), x, (0, 4))
+    assert y.shape == (0,)
+    # one 50,000-nnz row between empty rows, and a single-row matrix
+    for m, n, rows in [(9, 60000, ((4, 50000),)), (1, 70000, ((0, 50000),))]:
+        d, i, p, sh = S.random_csr(m, n, 0.0, dtype, torch.int32, device, seed=5, long_rows=rows)
+        for op in ("non", "trans"):
+            xx = S.vector(m if op == "trans" else n, dtype, device, seed=9)
+            _check_spmv(d, i, p, sh, xx, op, kernel_choice)
+
+
+def test_spmv_prepared_reuse_and_out(device):
+    d, i, p, sh = S.random_csr(300, 200, 0.05, torch.float32, torch.int32, device, seed=1)
+    prep = fs.prepare_spmv_csr(d, i, p, sh)
+    x = S.vector(200, torch.float32, device, seed=2)
+    out = torch.empty(300, dtype=torch.float32, device=device)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep, out=out)
+    assert y.data_ptr() == out.data_ptr()
+    y2, ms, meta = fs.flagsparse_spmv_csr(x=x, prepared=prep, return_time=True, return_meta=True)
+    assert torch.equal(y, y2)
+    assert ms == pytest.approx(meta["op_total_ms"])
+    assert meta["symbolic_ms"] == 0.0
+    # deterministic: bit-identical across runs
+    assert torch.equal(y2, fs.flagsparse_spmv_csr(x=x, prepared=prep))
+
+
+def test_spmv_prepared_transpose_mismatch_rejected(device):
+    d, i, p, sh = S.random_csr(8, 10, 0.3, torch.float32, torch.int32, device, seed=1)
+    prepared = fs.prepare_spmv_csr(d, i, p, sh, transpose=True)
+    x = torch.randn(8, dtype=torch.float32, device=device)
+    with pytest.raises(ValueError, match="does not match prepared.transpose"):
+        fs.flagsparse_spmv_csr(x=x, prepared=prepared, transpose=False)
+
+
+def test_spmv_prepared_op_mismatch_rejected(device):
+    d, i, p, sh = S.random_csr(8, 10, 0.3, torch.complex64, torch.int32, device, seed=1)
+    prepared = fs.prepare_spmv_csr(d, i, p, sh, op="conj")
+    x = S.vector(8, torch.complex64, device)
+    with pytest.raises(ValueError, match="does not match prepared.op"):
+        fs.flagsparse_spmv_csr(x=x, prepared=prepared, op="trans")
+
+
+def test_spmv_int64_auto_fallback_to_int32(device, monkeypatch):
+    d, i, p, sh = S.random_csr(12, 9, 0.4, torch.float32, torch.int64, device, seed=2)
+    x = S.vector(9, torch.float32, device)
+    ref = O.spmv_csr_wide(np_(d), np_(i), np_(p), np_(x), sh)
+    state = {"forced": False}
+    original = spmv_mod._hip_spmv_csr_impl_prepared
+
+    def fail_int64_once(prepared, x_in):
+        if prepared.kernel_indices.dtype == torch.int64 and not state["forced"]:
+            state["forced"] = True
+            raise RuntimeError("forced int64 launch failure")
+        return original(prepared, x_in)
+
+    monkeypatch.setattr(spmv_mod, "_hip_spmv_csr_impl_prepared", fail_int64_once)
+    out = fs.flagsparse_spmv_csr(d, i, p, x, sh, index_fallback_policy="auto")
+    assert state["forced"]
+    assert rel_err(np_(out), ref) <= REL_TOL[torch.float32]
+
+
+def test_spmv_int64_strict_no_fallback(device, monkeypatch):
+    d, i, p, sh = S.random_csr(12, 9, 0.4, torch.float32, torch.int64, device, seed=2)
+    x = S.vector(9, torch.float32, device)
+
+    def fail_int64(prepared, x_in):
+        raise RuntimeError("forced int64 launch failure")
+
+    monkeypatch.setattr(spmv_mod, "_hip_spmv_csr_impl_prepared", fail_int64)
+    with pytest.raises(RuntimeError, match="forced int64 launch failure"):
+        fs.flagsparse_spmv_csr(d, i, p, x, sh, index_fallback_policy="strict")
+
+
+def _sampled_rows_check(data, indices, indptr, shape, x, y, rows, tol):
+    """Oracle on a subset of rows (cheap at full size)."""
+    p = np_(indptr).astype(np.int64)
+    d = np_(data)
+    c = np_(indices)
+    xs = np_(x)
+    ys = np_(y)
+    sub_p = [0]
+    sub_d, sub_c = [], []
+    for r in rows:
+        sub_d.append(d[p[r]:p[r + 1]])
+        sub_c.append(c[p[r]:p[r + 1]])
+        sub_p.append(sub_p[-1] + p[r + 1] - p[r])
+    ref = O.spmv_csr_wide(np.concatenate(sub_d), np.concatenate(sub_c), np.array(sub_p), xs, (len(rows), shape[1]))
+    err = rel_err(ys[np.asarray(rows)], ref)
+    assert err <= tol, f"sampled-row rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("config", ["stencil128_f64_i32", "powerlaw_f32_i32", "powerlaw_f32_i64"])
+def test_spmv_full_size_configs(device, config):
+    """BASELINE configs at full size: sampled-row oracle, linearity, determinism."""
+    if config.startswith("stencil"):
+        data, indices, indptr, sh = S.stencil27(128, torch.float64, torch.int32, device, seed=2)
+        assert data.numel() == 382**3
+    else:
+        idt = torch.int32 if config.endswith("i32") else torch.int64
+        data, indices, indptr, sh = S.powerlaw(4194304, torch.float32, idt, device, seed=3)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    x1 = S.vector(sh[1], data.dtype, device, seed=21)
+    x2 = S.vector(sh[1], data.dtype, device, seed=22)
+    y1 = fs.flagsparse_spmv_csr(x=x1, prepared=prep)
+    y2 = fs.flagsparse_spmv_csr(x=x2, prepared=prep)
+    y12 = fs.flagsparse_spmv_csr(x=x1 + x2, prepared=prep)
+    lin = rel_err(np_(y12).astype(np.float64), np_(y1).astype(np.float64) + np_(y2).astype(np.float64))
+    assert lin <= (1e-6 if data.dtype == torch.float32 else 1e-12)
+    assert torch.equal(y1, fs.flagsparse_spmv_csr(x=x1, prepared=prep))
+    lengths = (indptr[1:] - indptr[:-1]).to(torch.int64)
+    longest = int(torch.argmax(lengths).item())
+    gen = np.random.default_rng(0)
+    rows = sorted(set(gen.integers(0, sh[0], 4000).tolist()) | {0, sh[0] - 1, longest})
+    _sampled_rows_check(data, indices, indptr, sh, x1, y1, rows, REL_TOL[data.dtype])

@@ -1,0 +1,72 @@
+"""GPU transpose (op=trans/conj materialisation) is bit-exact with the oracle.
+
+The reference builds A^T with a stable argsort by column plus bincount /
+cumsum (spmv_csr.py:477-515, spmm_csr.py:300-338); indices, indptr and
+(conjugated) values must match exactly, including the output index dtypes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from flagsparse_amd import _csr
+from flagsparse_amd import synthetic as S
+from oracle import csr_oracle as O
+from tests._helpers import INDEX_DTYPES, INDEX_IDS, VALUE_DTYPES, VALUE_IDS, np_
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(data, indices, indptr, shape, conj):
+    td, ti, tp, tsh = _csr.transpose_csr(data, indices, indptr, shape, conj=conj)
+    od, oi, op, osh = O.transpose_csr(np_(data), np_(indices), np_(indptr), shape, conj=conj)
+    assert tsh == osh
+    assert np_(ti).dtype == oi.dtype and np_(tp).dtype == op.dtype
+    assert np.array_equal(np_(tp), op)
+    assert np.array_equal(np_(ti), oi)
+    assert np.array_equal(np_(td), od)  # bit-exact permutation (+ exact conj)
+
+
+@pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+@pytest.mark.parametrize("conj", [False, True], ids=["trans", "conj"])
+@pytest.mark.parametrize("shape", [(1, 1), (1, 300), (300, 1), (257, 513), (1000, 70000), (5000, 300)])
+def test_transpose_bit_exact(device, dtype, index_dtype, conj, shape):
+    m, n = shape
+    d, i, p, sh = S.random_csr(m, n, min(0.2, 40.0 / n), dtype, index_dtype, device, seed=m * 7 + n,
+                               empty_row_every=5 if m > 5 else 0)
+    _check(d, i, p, sh, conj)
+
+
+def test_transpose_duplicates_stay_stable(device):
+    # Unsorted columns with repeats inside a row: a stable sort keeps input order.
+    indptr = torch.tensor([0, 4, 4, 7], dtype=torch.int32, device=device)
+    indices = torch.tensor([3, 1, 3, 0, 1, 1, 3], dtype=torch.int32, device=device)
+    data = torch.arange(1, 8, dtype=torch.float64, device=device)
+    _check(data, indices, indptr, (3, 4), False)
+
+
+def test_transpose_multi_pass_keys(device):
+    # n_cols needing three 8-bit radix passes, power-law rows
+    d, i, p, sh = S.powerlaw(1 << 17, torch.float32, torch.int32, device, seed=4)
+    _check(d, i, p, sh, False)
+    d, i, p, sh = S.rmat(scale=14, dtype=torch.complex64, index_dtype=torch.int64, device=device, seed=1)
+    _check(d, i, p, sh, True)
+
+
+def test_transpose_empty(device):
+    d = torch.empty(0, dtype=torch.float32, device=device)
+    i = torch.empty(0, dtype=torch.int64, device=device)
+    p = torch.zeros(4, dtype=torch.int64, device=device)
+    _check(d, i, p, (3, 5), False)
+
+
+def test_transpose_full_size_roundtrip(device):
+    """C4-sized matrix: (A^T)^T == A exactly (sorted columns), colptr == counts."""
+    d, i, p, sh = S.uniform_rows(1 << 20, 1 << 20, 32, torch.float32, torch.int32, device, seed=7)
+    td, ti, tp, tsh = _csr.transpose_csr(d, i, p, sh)
+    counts = torch.bincount(i.to(torch.int64), minlength=sh[1])
+    assert torch.equal((tp[1:] - tp[:-1]).to(torch.int64), counts)
+    d2, i2, p2, sh2 = _csr.transpose_csr(td, ti, tp, tsh)
+    assert sh2 == sh
+    assert torch.equal(p2, p) and torch.equal(i2, i) and torch.equal(d2, d)
