@@ -61,6 +61,15 @@ def distinct_sorted_columns(lengths, n_cols, g):
         raise ValueError("row length exceeds n_cols")
     rows = torch.repeat_interleave(torch.arange(n_rows, device=device, dtype=torch.int64), lengths)
     cols = torch.randint(0, n_cols, (rows.numel(),), device=device, generator=g, dtype=torch.int64)
+    # Rows filling more than a quarter of the columns: a sorted prefix of a
+    # random permutation (rejection would converge slowly there).
+    dense_rows = torch.nonzero(lengths * 4 > n_cols).flatten().tolist()
+    if dense_rows:
+        starts = torch.cumsum(lengths, 0) - lengths
+        for r in dense_rows:
+            s0, ln = int(starts[r]), int(lengths[r])
+            perm = torch.randperm(n_cols, device=device, generator=g)[:ln]
+            cols[s0:s0 + ln] = torch.sort(perm)[0]
     for _ in range(64):
         key, _ = torch.sort(rows * n_cols + cols)
         cols = key - rows * n_cols
