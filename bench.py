@@ -42,6 +42,14 @@ CONFIGS = {
 }
 DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 
+# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes scaled by a 1 GiB copy calibration (the commands and raw
+# counts are in profiles/<kernel>_<workload>.md).  Reported as
+# roofline.traffic; configs not profiled with the current kernels report null.
+MEASURED_TRAFFIC = {
+    "c2_spmv_stencil128_f64_i32": 776.6e6,
+}
+
 
 def _dtypes(torch):
     return (
@@ -176,7 +184,7 @@ def run(args):
         kernel_call = lambda: lib.fs_spmv_csr(*args_abi)  # noqa: E731
         bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
         flops = S.flops_spmv(nnz, complex_values)
-        kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel"}[plan.kernel_name]
+        kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel"}[plan.kernel_name]
         extra.update(kernel_variant=plan.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:
@@ -261,7 +269,7 @@ def run(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": args.traffic_bytes,
+            "traffic": args.traffic_bytes if args.traffic_bytes is not None else MEASURED_TRAFFIC.get(args.config),
         },
         "extra": dict(extra, generate_s=round(gen_s, 2)),
     }

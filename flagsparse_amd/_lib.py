@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libflagsparse_hip.so")
 
 FS_F32, FS_F64, FS_C64, FS_C128 = 0, 1, 2, 3
 FS_I32, FS_I64 = 0, 1
-FS_KERNEL_VECTOR, FS_KERNEL_MERGE = 0, 1
+FS_KERNEL_VECTOR, FS_KERNEL_MERGE, FS_KERNEL_STREAM = 0, 1, 2
 FS_HIST_BINS = 24
 
 VALUE_TYPE_CODES = {
@@ -28,7 +28,7 @@ VALUE_TYPE_CODES = {
     torch.complex128: FS_C128,
 }
 INDEX_TYPE_CODES = {torch.int32: FS_I32, torch.int64: FS_I64}
-KERNEL_NAMES = {FS_KERNEL_VECTOR: "vector", FS_KERNEL_MERGE: "merge"}
+KERNEL_NAMES = {FS_KERNEL_VECTOR: "vector", FS_KERNEL_MERGE: "merge", FS_KERNEL_STREAM: "stream"}
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTED_SYMBOLS = (
@@ -59,6 +59,8 @@ class FsCsrPlan(ctypes.Structure):
         ("kernel", ctypes.c_int32),
         ("vec_width", ctypes.c_int32),
         ("tile_items", ctypes.c_int32),
+        ("rows_per_block", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("n_tiles", ctypes.c_int64),
         ("max_row", ctypes.c_int64),
         ("min_row", ctypes.c_int64),

@@ -17,6 +17,10 @@
 // tile order: deterministic, no floating-point atomics.
 #include "fs_common.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
 namespace fs {
 
 constexpr int kSpmmTile = 512;  // merge items per tile (rows + nnz)
@@ -50,28 +54,46 @@ __device__ inline void load_row(const V* __restrict__ p, int valid, V (&out)[VEC
   }
 }
 
+// Broadcast lane `lane` of a per-lane value to the whole wave (the index is
+// wave-uniform, so this is one v_readlane per dword into scalar registers).
+template <class T>
+__device__ inline T readlane_any(const T& v, int lane) {
+  constexpr int W = (int)(sizeof(T) / 4);
+  int w[W];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (int k = 0; k < W; ++k) w[k] = __builtin_amdgcn_readlane(w[k], lane);
+  T out;
+  __builtin_memcpy(&out, w, sizeof(T));
+  return out;
+}
+
+// Gathers per batch (double buffered, so 2x this many B rows per wave are
+// in flight).
 template <class V, int VEC>
+constexpr int spmm_batch() {
+  return 4;  // measured best on MI355X for N = 32 .. 256 (8 within 3%)
+}
+
+// One wave per merge-path tile.  The tile's nnz (<= kSpmmTile) are staged 64
+// at a time in lane registers (coalesced loads, next chunk prefetched) and
+// broadcast with readlane; row ends are staged the same way.  B-row gathers
+// are double buffered: batch k+1 is issued before batch k is accumulated,
+// so a wave keeps up to 2*U gathers in flight.
+template <class V, int VEC, int U, class I, class P>
 __global__ __launch_bounds__(256) void spmm_merge_kernel(
-    const V* __restrict__ vals, const void* __restrict__ cols_raw, int idx64,
-    const void* __restrict__ rowptr_raw, int ptr64, const V* __restrict__ B, int64_t ldb,
-    V* __restrict__ C, int64_t ldc, int64_t n_dense, const int64_t* __restrict__ part,
-    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail,
-    int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ B, int64_t ldb, V* __restrict__ C, int64_t ldc, int64_t n_dense,
+    const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
+    typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz, int64_t n_tiles) {
   using T = VT<V>;
   using A = typename T::acc;
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= n_tiles) return;  // wave-uniform, no barriers below
   const int64_t col0 = (int64_t)blockIdx.y * 64 * VEC + (int64_t)lane * VEC;
-  int64_t vrem = n_dense - col0;
+  const int64_t vrem = n_dense - col0;
   const int valid = vrem <= 0 ? 0 : (vrem >= VEC ? VEC : (int)vrem);
-
-  const int32_t* rp32 = static_cast<const int32_t*>(rowptr_raw);
-  const int64_t* rp64 = static_cast<const int64_t*>(rowptr_raw);
-  const int32_t* ci32 = static_cast<const int32_t*>(cols_raw);
-  const int64_t* ci64 = static_cast<const int64_t*>(cols_raw);
-  auto rowptr = [&](int64_t r) -> int64_t { return ptr64 ? rp64[r] : (int64_t)rp32[r]; };
-  auto colidx = [&](int64_t j) -> int64_t { return idx64 ? ci64[j] : (int64_t)ci32[j]; };
 
   const int64_t r0 = part[t];
   const int64_t r1 = part[t + 1];
@@ -79,25 +101,58 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
   const int64_t total = n_rows + nnz;
   const int64_t dend = d0 + kSpmmTile < total ? d0 + kSpmmTile : total;
   const int64_t n0 = d0 - r0;
-  const int64_t n1 = dend - r1;
-  const bool head_partial = r1 > r0 && rowptr(r0) < n0;
+  const int nz = (int)(dend - r1 - n0);  // nnz in the tile
+  const int R = (int)(r1 - r0);          // row ends in the tile
+  const bool head_partial = R > 0 && (int64_t)rowptr[r0] < n0;
+
+  // nnz chunks (current + prefetched next)
+  I colC, colN;
+  V valC, valN;
+  auto load_chunk = [&](int ch, I& cc, V& vv) {
+    const int q = ch * 64 + lane;
+    cc = 0;
+    vv = V{};
+    if (q < nz) {
+      cc = cols[n0 + q];
+      vv = vals[n0 + q];
+    }
+  };
+  load_chunk(0, colC, valC);
+  load_chunk(1, colN, valN);
+  int chunk = 0;
+  // row-end chunks, as offsets from n0
+  int reC, reN;
+  auto load_re = [&](int base, int& dst) {
+    const int k = base + lane;
+    dst = k < R ? (int)((int64_t)rowptr[r0 + 1 + k] - n0) : 0x7fffffff;
+  };
+  load_re(0, reC);
+  load_re(64, reN);
+  int rbase = 0;
+  int row = 0;  // tile-local
+  int re = R > 0 ? readlane_any(reC, 0) : 0x7fffffff;
+  auto next_row = [&]() {
+    ++row;
+    if (row - rbase == 64) {
+      reC = reN;
+      rbase += 64;
+      load_re(rbase + 64, reN);
+    }
+    re = row < R ? readlane_any(reC, row - rbase) : 0x7fffffff;
+  };
 
   A acc[VEC];
 #pragma unroll
   for (int k = 0; k < VEC; ++k) acc[k] = T::zero();
-
-  int64_t row = r0;
-  int64_t re = row < r1 ? rowptr(row + 1) : n1;  // end of the current row inside the tile
-
-  auto emit = [&](int64_t r) {
+  auto emit = [&]() {
     if (valid > 0) {
-      if (r == r0 && head_partial) {
+      if (row == 0 && head_partial) {
         A* h = head + t * n_dense + col0;
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
           if (k < valid) h[k] = acc[k];
       } else {
-        V* c = C + r * ldc + col0;
+        V* c = C + (r0 + row) * ldc + col0;
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
           if (k < valid) c[k] = T::out(acc[k]);
@@ -107,40 +162,54 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
     for (int k = 0; k < VEC; ++k) acc[k] = T::zero();
   };
 
-  for (int64_t jb = n0; jb < n1; jb += kBatch) {
-    V a[kBatch];
-    int64_t c[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int64_t j = jb + u;
-      a[u] = V{};
-      c[u] = 0;
-      if (j < n1) {
-        a[u] = vals[j];
-        c[u] = colidx(j);
-      }
-    }
-    V b[kBatch][VEC];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      if (jb + u < n1) load_row<V, VEC>(B + c[u] * ldb + col0, valid, b[u]);
+  auto issue = [&](int kb, V (&bb)[U][VEC], V (&aa)[U]) {
+    const int ch = (kb * U) >> 6;
+    if (ch != chunk) {
+      colC = colN;
+      valC = valN;
+      chunk = ch;
+      load_chunk(ch + 1, colN, valN);
     }
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int64_t j = jb + u;
-      if (j >= n1) break;
-      while (row < r1 && re <= j) {  // rows ending before nnz j (incl. empty rows)
-        emit(row);
-        ++row;
-        re = row < r1 ? rowptr(row + 1) : n1;
+    for (int u = 0; u < U; ++u) {
+      const int q = kb * U + u;
+      if (q < nz) {
+        const int li = q & 63;
+        const int64_t c = (int64_t)readlane_any(colC, li);
+        aa[u] = readlane_any(valC, li);
+        load_row<V, VEC>(B + c * ldb + col0, valid, bb[u]);
+      }
+    }
+  };
+  auto consume = [&](int kb, V (&bb)[U][VEC], V (&aa)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = kb * U + u;
+      if (q >= nz) break;
+      while (re <= q) {  // rows that end before nnz q (empty rows included)
+        emit();
+        next_row();
       }
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) acc[k] = T::fma(a[u], b[u][k], acc[k]);
+      for (int k = 0; k < VEC; ++k) acc[k] = T::fma(aa[u], bb[u][k], acc[k]);
+    }
+  };
+
+  const int nb = (nz + U - 1) / U;
+  V bA[U][VEC], bB[U][VEC];
+  V aA[U], aB[U];
+  if (nb > 0) issue(0, bA, aA);
+  for (int kb = 0; kb < nb; kb += 2) {
+    if (kb + 1 < nb) issue(kb + 1, bB, aB);
+    consume(kb, bA, aA);
+    if (kb + 1 < nb) {
+      if (kb + 2 < nb) issue(kb + 2, bA, aA);
+      consume(kb + 1, bB, aB);
     }
   }
-  while (row < r1) {  // rows ending at the tile's last nnz, and trailing empty rows
-    emit(row);
-    ++row;
+  while (row < R) {  // rows ending at the tile's last nnz, and trailing empty rows
+    emit();
+    next_row();
   }
   if (r1 < n_rows && valid > 0) {
     A* tl = tail + t * n_dense + col0;
@@ -178,7 +247,7 @@ __global__ __launch_bounds__(256) void spmm_fixup_kernel(
 }
 
 int spmm_vec_for(int val_t, int64_t n_dense) {
-  const int max_vec = (val_t == FS_F32) ? 4 : (val_t == FS_C128 ? 1 : 2);
+  const int max_vec = (val_t == FS_C128) ? 1 : 2;
   int vec = 1;
   while (vec < max_vec && n_dense > 64 * vec) vec <<= 1;
   return vec;
@@ -194,10 +263,28 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   const int64_t col_tiles = ceil_div(n_dense, 64 * VEC);
   const int64_t blocks = ceil_div(n_tiles, 4);
   if (blocks > 0x7fffffffLL || col_tiles > 65535) return fail(FS_E_INVALID, "fs_spmm_csr: grid too large");
-  hipLaunchKernelGGL((spmm_merge_kernel<V, VEC>), dim3((unsigned)blocks, (unsigned)col_tiles), dim3(256), 0,
-                     stream, static_cast<const V*>(vals), cols, plan->idx_t == FS_I64 ? 1 : 0, indptr,
-                     plan->ptr_t == FS_I64 ? 1 : 0, static_cast<const V*>(B), ldb, static_cast<V*>(C), ldc,
-                     n_dense, part, head, tail, plan->n_rows, plan->nnz, n_tiles);
+  dim3 g((unsigned)blocks, (unsigned)col_tiles);
+  int u = spmm_batch<V, VEC>();
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_U")) u = std::atoi(e);
+  auto go = [&](auto icode, auto pcode) {
+    using I = std::conditional_t<decltype(icode)::value, int64_t, int32_t>;
+    using P = std::conditional_t<decltype(pcode)::value, int64_t, int32_t>;
+    auto launch = [&](auto uc) {
+      hipLaunchKernelGGL((spmm_merge_kernel<V, VEC, decltype(uc)::value, I, P>), g, dim3(256), 0, stream,
+                         static_cast<const V*>(vals), static_cast<const I*>(cols), static_cast<const P*>(indptr),
+                         static_cast<const V*>(B), ldb, static_cast<V*>(C), ldc, n_dense, part, head, tail,
+                         plan->n_rows, plan->nnz, n_tiles);
+    };
+    if (u <= 4) launch(std::integral_constant<int, 4>{});
+    else launch(std::integral_constant<int, 8>{});
+  };
+  using T1 = std::true_type;
+  using F1 = std::false_type;
+  const bool i64 = plan->idx_t == FS_I64, p64 = plan->ptr_t == FS_I64;
+  if (i64 && p64) go(T1{}, T1{});
+  else if (i64) go(T1{}, F1{});
+  else if (p64) go(F1{}, T1{});
+  else go(F1{}, F1{});
   FS_CHECK_LAUNCH("spmm_merge_kernel");
   const int64_t fix_cols = ceil_div(n_dense, 64) < 64 ? ceil_div(n_dense, 64) : 64;
   hipLaunchKernelGGL((spmm_fixup_kernel<V>), dim3((unsigned)blocks, (unsigned)fix_cols), dim3(256), 0, stream,
@@ -258,6 +345,10 @@ extern "C" int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void
   if (ws_bytes < fs_spmm_workspace_bytes(plan->val_t, n_tiles, n_dense) || (!ws && n_tiles > 0))
     return fail(FS_E_WORKSPACE, "fs_spmm_csr: workspace too small");
   int vec = spmm_vec_for(plan->val_t, n_dense);
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_VEC")) {
+    const int v = std::atoi(e);
+    if (v == 1 || v == 2 || v == 4) vec = std::min(vec, v);
+  }
   // Vector loads need every lane's B/C slice aligned to the vector width.
   const size_t vsz[] = {4, 8, 8, 16};
   const size_t esz = vsz[plan->val_t];

@@ -12,6 +12,7 @@
 #include "fs_common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 #include <cstring>
 
@@ -83,31 +84,61 @@ __global__ __launch_bounds__(256) void partition_kernel(const P* __restrict__ ro
 }
 
 // ---------------------------------------------------------------------------
-// K1: vector-per-row.  VW lanes share a row; products accumulate in the
-// accumulator type and are combined with a DPP / ds_swizzle butterfly.
+// K1: vector-per-row.  VW lanes share a row; each lane walks the row with
+// stride VW and issues kUnroll loads before using any of them, so a wave
+// keeps (64/VW rows) x kUnroll value/index loads and x gathers in flight.
+// Products accumulate in the accumulator type and are combined with a DPP /
+// ds_swizzle butterfly.
 // ---------------------------------------------------------------------------
+constexpr int kUnroll = 4;
+constexpr int kXcds = 8;  // MI355X: workgroup w is dispatched to XCD w % 8
+
+// Logical workgroup index.  With remap, the grid (padded to a multiple of 8)
+// is split into 8 contiguous ranges and XCD k walks range k in order, so the
+// rows an XCD works on at any moment are adjacent and their x slice stays
+// in that XCD's L2.  Returns -1 for padding workgroups.
+__device__ inline int64_t logical_block(int remap, int64_t n_blocks) {
+  if (!remap) return blockIdx.x;
+  const int64_t per = (n_blocks + kXcds - 1) / kXcds;
+  const int64_t b = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  return b < n_blocks ? b : -1;
+}
+
 template <int VW, class V, class I, class P>
 __global__ __launch_bounds__(256) void spmv_vector_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
-    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows) {
+    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_blocks, int remap) {
   using T = VT<V>;
   using A = typename T::acc;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t blk = logical_block(remap, n_blocks);
+  if (blk < 0) return;
+  const int64_t gid = blk * blockDim.x + threadIdx.x;
   const int64_t row = gid / VW;
   const int sub = threadIdx.x & (VW - 1);
   if (row >= n_rows) return;  // whole VW-group leaves together
   const int64_t s = (int64_t)rowptr[row];
   const int64_t e = (int64_t)rowptr[row + 1];
-  A a0 = T::zero(), a1 = T::zero();
-  int64_t j = s + sub;
-  for (; j + VW < e; j += 2 * VW) {
-    V v0 = vals[j], v1 = vals[j + VW];
-    I c0 = cols[j], c1 = cols[j + VW];
-    a0 = T::fma(v0, x[c0], a0);
-    a1 = T::fma(v1, x[c1], a1);
+  A acc = T::zero();
+  for (int64_t j = s + sub; j < e; j += kUnroll * VW) {
+    V v[kUnroll];
+    I c[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t jj = j + (int64_t)u * VW;
+      c[u] = 0;
+      if (jj < e) {
+        v[u] = vals[jj];
+        c[u] = cols[jj];
+      }
+    }
+    V xv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (j + (int64_t)u * VW < e) xv[u] = x[c[u]];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (j + (int64_t)u * VW < e) acc = T::fma(v[u], xv[u], acc);
   }
-  if (j < e) a0 = T::fma(vals[j], x[cols[j]], a0);
-  A acc = add(a0, a1);
   if constexpr (VW <= 32) {
     acc = group_sum<VW>(acc);
   } else {
@@ -115,6 +146,201 @@ __global__ __launch_bounds__(256) void spmv_vector_kernel(
     acc = add(acc, shfl(acc, (threadIdx.x & 63) ^ 32));
   }
   if (sub == 0) y[row] = T::out(acc);
+}
+
+// ---------------------------------------------------------------------------
+// K3: row-block streaming SpMV for matrices whose rows are all short.
+//
+// A workgroup owns R = 256/TPR consecutive rows, whose nnz form one
+// contiguous range of at most stream_items(A) entries.  The 256 threads
+// stream that range with unit stride (every load instruction covers
+// consecutive addresses), gather x, and stage the products in LDS; then
+// TPR threads per row add the row's products and combine them with a DPP
+// butterfly.  The plan picks R so that R * max_row fits the LDS stage.
+// ---------------------------------------------------------------------------
+template <class A>
+constexpr int stream_items() {
+  return 16384 / (int)sizeof(A);
+}
+
+// One workgroup per row block (variants: KMUL scales the LDS stage, NT
+// streams values / indices with non-temporal loads so they do not displace
+// x from the caches).
+template <bool NT, class Tp>
+__device__ inline Tp ld_nt(const Tp* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+
+template <int TPR, int KMUL, bool NT, class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_stream_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_blocks, int remap) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  constexpr int R = 256 / TPR * KMUL;
+  constexpr int kItems = stream_items<A>() * KMUL;
+  constexpr int K = kItems / 256;
+  __shared__ A s_prod[kItems];
+  __shared__ int64_t s_ptr[R + 1];
+  const int t = threadIdx.x;
+  const int64_t blk = logical_block(remap, n_blocks);
+  if (blk < 0) return;  // whole workgroup
+  const int64_t rb0 = blk * R;
+  const int rows = n_rows - rb0 < R ? (int)(n_rows - rb0) : R;
+  for (int k = t; k <= rows; k += 256) s_ptr[k] = (int64_t)rowptr[rb0 + k];  // rows + 1 pointers
+  const int64_t S = (int64_t)rowptr[rb0];
+  const int cnt = (int)((int64_t)rowptr[rb0 + rows] - S);
+  V v[K];
+  I c[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = t + 256 * k;
+    c[k] = 0;
+    if (q < cnt) {
+      if constexpr (VT<V>::complex) {
+        v[k] = vals[S + q];
+      } else {
+        v[k] = ld_nt<NT>(vals + S + q);
+      }
+      c[k] = ld_nt<NT>(cols + S + q);
+    }
+  }
+  V xv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (t + 256 * k < cnt) xv[k] = x[c[k]];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(v[k], xv[k]);
+  __syncthreads();
+#pragma unroll
+  for (int rr = 0; rr < KMUL; ++rr) {
+    const int r = t / TPR + rr * (256 / TPR);
+    const int sub = t % TPR;
+    A acc = T::zero();
+    if (r < rows) {
+      const int a = (int)(s_ptr[r] - S);
+      const int b = (int)(s_ptr[r + 1] - S);
+      for (int q = a + sub; q < b; q += TPR) acc = add(acc, s_prod[q]);
+    }
+    if constexpr (TPR > 1) acc = group_sum<TPR>(acc);
+    if (sub == 0 && r < rows) y[rb0 + r] = T::out(acc);
+  }
+}
+
+// Row blocks are handed out persistently: the grid holds a few workgroups
+// per CU and each walks row blocks with a stride; while the products of the
+// current block are gathered, reduced and stored, the row pointers and the
+// value / index stream of the next block are already in flight.  With
+// xcd_split, workgroup w (which the dispatcher places on XCD w % 8) walks
+// the row blocks of one contiguous eighth of the matrix, so each XCD's L2
+// caches the slice of x that its rows touch.
+template <class V, class I, int K>
+struct StreamChunk {
+  V v[K];
+  I c[K];
+};
+
+template <int TPR, class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_stream_persistent_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int xcd_split) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  constexpr int R = 256 / TPR;
+  constexpr int kItems = stream_items<A>();
+  constexpr int K = kItems / 256;
+  __shared__ A s_prod[kItems];
+  __shared__ int64_t s_ptr[R + 1];
+  const int t = threadIdx.x;
+  const int64_t n_blocks = (n_rows + R - 1) / R;
+  // block walk: [first, last) with stride
+  int64_t first, last, stride;
+  if (xcd_split) {
+    const int groups = 8;
+    const int g = blockIdx.x % groups;
+    const int64_t per = (n_blocks + groups - 1) / groups;
+    first = g * per + blockIdx.x / groups;
+    last = (g + 1) * per < n_blocks ? (g + 1) * per : n_blocks;
+    stride = (gridDim.x + groups - 1 - g) / groups;  // workgroups of this XCD
+  } else {
+    first = blockIdx.x;
+    last = n_blocks;
+    stride = gridDim.x;
+  }
+  auto rows_of = [&](int64_t blk) -> int {
+    const int64_t r = n_rows - blk * R;
+    return r < R ? (int)r : R;
+  };
+  auto load_chunk = [&](int64_t S, int cnt, StreamChunk<V, I, K>& ch) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int q = t + 256 * k;
+      ch.c[k] = 0;
+      if (q < cnt) {
+        ch.v[k] = vals[S + q];
+        ch.c[k] = cols[S + q];
+      }
+    }
+  };
+  if (first >= last) return;  // uniform per workgroup
+  // prologue: pointers + stream of the first block
+  int64_t blk = first;
+  int rows = rows_of(blk);
+  int64_t my_ptr = (t <= rows) ? (int64_t)rowptr[blk * R + t] : 0;
+  int64_t S = (int64_t)rowptr[blk * R];
+  int64_t E = (int64_t)rowptr[blk * R + rows];
+  StreamChunk<V, I, K> cur;
+  load_chunk(S, (int)(E - S), cur);
+  while (true) {
+    const int64_t nblk = blk + stride;
+    const bool has_next = nblk < last;
+    // gathers of the current block
+    V xv[K];
+    const int cnt = (int)(E - S);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (t + 256 * k < cnt) xv[k] = x[cur.c[k]];
+    // next block's pointers and stream go out before the gathers return
+    int nrows = 0;
+    int64_t nS = 0, nE = 0, nptr = 0;
+    StreamChunk<V, I, K> nxt;
+    if (has_next) {
+      nrows = rows_of(nblk);
+      nS = (int64_t)rowptr[nblk * R];
+      nE = (int64_t)rowptr[nblk * R + nrows];
+      nptr = (t <= nrows) ? (int64_t)rowptr[nblk * R + t] : 0;
+      load_chunk(nS, (int)(nE - nS), nxt);
+    }
+    if (t <= rows) s_ptr[t] = my_ptr;
+    if (t == 0 && rows == 256) s_ptr[256] = E;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(cur.v[k], xv[k]);
+    __syncthreads();
+    const int r = t / TPR;
+    const int sub = t % TPR;
+    A acc = T::zero();
+    if (r < rows) {
+      const int a = (int)(s_ptr[r] - S);
+      const int b = (int)(s_ptr[r + 1] - S);
+      for (int q = a + sub; q < b; q += TPR) acc = add(acc, s_prod[q]);
+    }
+    if constexpr (TPR > 1) acc = group_sum<TPR>(acc);
+    if (sub == 0 && r < rows) y[blk * R + r] = T::out(acc);
+    __syncthreads();
+    if (!has_next) break;
+    blk = nblk;
+    rows = nrows;
+    S = nS;
+    E = nE;
+    my_ptr = nptr;
+    cur = nxt;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -341,6 +567,25 @@ __global__ __launch_bounds__(256) void merge_fixup_kernel(
 // ---------------------------------------------------------------------------
 // Host dispatch.
 // ---------------------------------------------------------------------------
+// XCD-contiguous workgroup mapping (FLAGSPARSE_XCD_REMAP=0/1 for A/B).
+inline int xcd_remap() {
+  if (const char* e = std::getenv("FLAGSPARSE_XCD_REMAP")) return std::atoi(e) != 0;
+  return 0;  // measured neutral (within 5%) on the stencil and uniform matrices
+}
+
+// Compute units of the current device (cached per device id).
+inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <class V, class I, class P>
 int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
                 const void* x, void* y, const void* part, void* carry, size_t carry_bytes,
@@ -355,20 +600,72 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
   V* yv = static_cast<V*>(y);
   if (plan->kernel == FS_KERNEL_VECTOR) {
     const int vw = plan->vec_width;
-    const int64_t threads = n_rows * vw;
-    const int64_t blocks = ceil_div(threads, 256);
-    if (blocks > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr: grid too large for vector kernel");
-    dim3 g((unsigned)blocks);
+    const int64_t blocks = ceil_div(n_rows * vw, 256);
+    const int remap = xcd_remap();
+    const int64_t grid = remap ? ceil_div(blocks, kXcds) * kXcds : blocks;
+    if (grid > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr: grid too large for vector kernel");
+    dim3 g((unsigned)grid);
     switch (vw) {
-      case 2: hipLaunchKernelGGL((spmv_vector_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
-      case 4: hipLaunchKernelGGL((spmv_vector_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
-      case 8: hipLaunchKernelGGL((spmv_vector_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
-      case 16: hipLaunchKernelGGL((spmv_vector_kernel<16, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
-      case 32: hipLaunchKernelGGL((spmv_vector_kernel<32, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
-      case 64: hipLaunchKernelGGL((spmv_vector_kernel<64, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows); break;
+      case 2: hipLaunchKernelGGL((spmv_vector_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 4: hipLaunchKernelGGL((spmv_vector_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 8: hipLaunchKernelGGL((spmv_vector_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 16: hipLaunchKernelGGL((spmv_vector_kernel<16, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 32: hipLaunchKernelGGL((spmv_vector_kernel<32, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 64: hipLaunchKernelGGL((spmv_vector_kernel<64, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
       default: return fail(FS_E_INVALID, "fs_spmv_csr: vec_width must be a power of two in [2, 64]");
     }
     FS_CHECK_LAUNCH("spmv_vector_kernel");
+    return FS_OK;
+  }
+  if (plan->kernel == FS_KERNEL_STREAM) {
+    using Acc = typename VT<V>::acc;
+    const int rpb = plan->rows_per_block;
+    if (rpb < 32 || rpb > 256 || (rpb & (rpb - 1)) || (int64_t)plan->max_row * rpb > stream_items<Acc>())
+      return fail(FS_E_INVALID, "fs_spmv_csr: rows_per_block does not fit the stream kernel");
+    int variant = 0;
+    if (const char* e = std::getenv("FLAGSPARSE_STREAM_VARIANT")) variant = std::atoi(e);
+    if (variant == 4) {
+      const int64_t n_blocks = ceil_div(n_rows, rpb);
+      int per_cu = 4;
+      if (const char* e = std::getenv("FLAGSPARSE_STREAM_WG_PER_CU")) per_cu = std::max(1, std::atoi(e));
+      int xcd_split = 0;
+      if (const char* e = std::getenv("FLAGSPARSE_STREAM_XCD")) xcd_split = std::atoi(e) != 0;
+      dim3 g((unsigned)std::min<int64_t>(n_blocks, (int64_t)device_cus() * per_cu));
+      switch (256 / rpb) {
+        case 1: hipLaunchKernelGGL((spmv_stream_persistent_kernel<1, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
+        case 2: hipLaunchKernelGGL((spmv_stream_persistent_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
+        case 4: hipLaunchKernelGGL((spmv_stream_persistent_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
+        default: hipLaunchKernelGGL((spmv_stream_persistent_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
+      }
+    } else {
+      const int kmul = (variant & 2) ? 2 : 1;
+      const bool nt = variant & 1;
+      const int64_t blocks = ceil_div(n_rows, (int64_t)rpb * kmul);
+      const int remap = xcd_remap();
+      dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
+      auto go = [&](auto tpr_c, auto kmul_c, auto nt_c) {
+        hipLaunchKernelGGL((spmv_stream_kernel<decltype(tpr_c)::value, decltype(kmul_c)::value, decltype(nt_c)::value, V, I, P>),
+                           g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap);
+      };
+      auto go_k = [&](auto tpr_c) {
+        using B2 = std::integral_constant<int, 2>;
+        using B1 = std::integral_constant<int, 1>;
+        using NT1 = std::integral_constant<bool, true>;
+        using NT0 = std::integral_constant<bool, false>;
+        if (kmul == 2) {
+          if (nt) go(tpr_c, B2{}, NT1{}); else go(tpr_c, B2{}, NT0{});
+        } else {
+          if (nt) go(tpr_c, B1{}, NT1{}); else go(tpr_c, B1{}, NT0{});
+        }
+      };
+      switch (256 / rpb) {
+        case 1: go_k(std::integral_constant<int, 1>{}); break;
+        case 2: go_k(std::integral_constant<int, 2>{}); break;
+        case 4: go_k(std::integral_constant<int, 4>{}); break;
+        default: go_k(std::integral_constant<int, 8>{}); break;
+      }
+    }
+    FS_CHECK_LAUNCH("spmv_stream_kernel");
     return FS_OK;
   }
   if (plan->kernel != FS_KERNEL_MERGE) return fail(FS_E_INVALID, "fs_spmv_csr: unknown kernel");
@@ -415,18 +712,30 @@ size_t acc_bytes(int val_t) {
 void choose_spmv_kernel(fs_csr_plan* plan, int force_kernel) {
   const int64_t n_rows = plan->n_rows;
   const double mean = n_rows > 0 ? (double)plan->nnz / (double)n_rows : 0.0;
-  int kernel = FS_KERNEL_MERGE;
-  // Vector-per-row wins only when every row fits one short vector pass and
-  // rows are close to uniform; any long or skewed row goes to the merge
-  // path, which balances rows + nnz exactly.
-  if (n_rows > 0 && plan->max_row <= 64 && (double)plan->max_row <= 2.0 * mean + 4.0) kernel = FS_KERNEL_VECTOR;
+  const int items = (plan->val_t == FS_C64 || plan->val_t == FS_C128) ? stream_items<c64>() : stream_items<double>();
+  // Rows per workgroup for the streaming kernel: as many as fit the LDS stage.
+  int rpb = 256;
+  while (rpb > 32 && (int64_t)rpb * plan->max_row > items) rpb >>= 1;
+  const bool stream_fits = (int64_t)rpb * plan->max_row <= items;
+  // Short rows only -> stream a row block through LDS; anything longer or
+  // skewed -> the merge path, which balances rows + nnz exactly.
+  int kernel = stream_fits ? FS_KERNEL_STREAM : FS_KERNEL_MERGE;
   const char* env = std::getenv("FLAGSPARSE_SPMV_KERNEL");
   if (env && std::strcmp(env, "vector") == 0) kernel = FS_KERNEL_VECTOR;
   if (env && std::strcmp(env, "merge") == 0) kernel = FS_KERNEL_MERGE;
-  if (force_kernel == FS_KERNEL_VECTOR || force_kernel == FS_KERNEL_MERGE) kernel = force_kernel;
+  if (env && std::strcmp(env, "stream") == 0) kernel = FS_KERNEL_STREAM;
+  if (force_kernel == FS_KERNEL_VECTOR || force_kernel == FS_KERNEL_MERGE || force_kernel == FS_KERNEL_STREAM)
+    kernel = force_kernel;
+  if (kernel == FS_KERNEL_STREAM && !stream_fits) kernel = FS_KERNEL_MERGE;
   plan->kernel = kernel;
+  plan->rows_per_block = rpb;
   int vw = 2;
-  while (vw < 64 && (double)vw < mean) vw <<= 1;
+  while (vw < 64 && (double)vw * kUnroll < mean) vw <<= 1;
+  const char* env_vw = std::getenv("FLAGSPARSE_SPMV_VW");
+  if (env_vw) {
+    const int v = std::atoi(env_vw);
+    if (v >= 2 && v <= 64 && (v & (v - 1)) == 0) vw = v;
+  }
   plan->vec_width = vw;
   plan->tile_items = kMergeTile;
   plan->n_tiles = ceil_div(n_rows + plan->nnz, kMergeTile);

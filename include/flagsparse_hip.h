@@ -46,7 +46,7 @@ enum fs_status {
 };
 
 /* Kernel variants chosen by fs_csr_analyze. */
-enum fs_kernel { FS_KERNEL_VECTOR = 0, FS_KERNEL_MERGE = 1 };
+enum fs_kernel { FS_KERNEL_VECTOR = 0, FS_KERNEL_MERGE = 1, FS_KERNEL_STREAM = 2 };
 
 #define FS_HIST_BINS 24 /* bin b counts rows with length in [2^(b-1), 2^b); bin 0 = empty rows */
 
@@ -57,6 +57,8 @@ typedef struct fs_csr_plan {
   int32_t kernel;        /* FS_KERNEL_* chosen for SpMV */
   int32_t vec_width;     /* lanes per row for FS_KERNEL_VECTOR */
   int32_t tile_items;    /* merge-path items (rows + nnz) per tile */
+  int32_t rows_per_block; /* rows per workgroup for FS_KERNEL_STREAM */
+  int32_t reserved;
   int64_t n_tiles;       /* merge-path tiles */
   int64_t max_row, min_row;
   int64_t hist[FS_HIST_BINS];
@@ -77,7 +79,8 @@ const char* fs_version(void);
  * opt buckets spmv_csr.py:353-410).  Runs one histogram kernel into
  * `stats_dev` (>= fs_csr_stats_bytes() bytes of device memory), then
  * synchronises `stream` and decides on the host.  force_kernel < 0 lets the
- * analysis choose; 0/1 forces FS_KERNEL_VECTOR / FS_KERNEL_MERGE.
+ * analysis choose; 0/1/2 forces FS_KERNEL_VECTOR / FS_KERNEL_MERGE /
+ * FS_KERNEL_STREAM (STREAM falls back to MERGE when rows are too long).
  */
 size_t fs_csr_stats_bytes(void);
 int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t,

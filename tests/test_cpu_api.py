@@ -70,9 +70,9 @@ def test_abi_rejects_bad_arguments_without_touching_the_gpu():
 
 def test_plan_struct_layout():
     # offsets must match the C struct (natural alignment, x86-64)
-    assert _lib.FsCsrPlan.n_tiles.offset == 48
-    assert _lib.FsCsrPlan.hist.offset == 72
-    assert ctypes.sizeof(_lib.FsCsrPlan) == 72 + 8 * _lib.FS_HIST_BINS + 16
+    assert _lib.FsCsrPlan.n_tiles.offset == 56
+    assert _lib.FsCsrPlan.hist.offset == 80
+    assert ctypes.sizeof(_lib.FsCsrPlan) == 80 + 8 * _lib.FS_HIST_BINS + 16
 
 
 @pytest.mark.parametrize("op,expected", [(None, 0), ("non", 0), ("trans", 1), ("conj", 2), (" Trans ", 1), (2, 2)])

@@ -31,7 +31,7 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge"])
+@pytest.fixture(params=["auto", "vector", "merge", "stream"])
 def kernel_choice(request, monkeypatch):
     if request.param != "auto":
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", request.param)
