@@ -16,6 +16,21 @@ from ._common import (
     _INDEX_LIMIT_INT32,
     _tolerance_for_dtype,
 )
+from .coo import coo_to_csr_for_spmv, flagsparse_spmv_coo_tocsr, prepare_spmv_coo_tocsr
+from .spmm_opt import (
+    PreparedCsrSpmmOpt,
+    PreparedCsrSpmmOptAlg2,
+    flagsparse_spmm_csr_opt,
+    flagsparse_spmm_csr_opt_alg1,
+    flagsparse_spmm_csr_opt_alg1_preprocess,
+    flagsparse_spmm_csr_opt_alg2,
+    flagsparse_spmm_csr_opt_alg2_preprocess,
+    prepare_spmm_csr_opt,
+    prepare_spmm_csr_opt_alg1,
+    prepare_spmm_csr_opt_alg1_preprocess,
+    prepare_spmm_csr_opt_alg2,
+    prepare_spmm_csr_opt_alg2_preprocess,
+)
 from .spmm_csr import (
     SPMM_CSR_ALGORITHMS,
     PreparedCsrSpmmRoute,
@@ -44,4 +59,19 @@ __all__ = [
     "SpmmCsrAlgorithm",
     "SpmmCsrAlgorithmUnavailable",
     "PreparedCsrSpmmRoute",
+    "PreparedCsrSpmmOpt",
+    "PreparedCsrSpmmOptAlg2",
+    "prepare_spmm_csr_opt",
+    "prepare_spmm_csr_opt_alg1",
+    "prepare_spmm_csr_opt_alg1_preprocess",
+    "prepare_spmm_csr_opt_alg2",
+    "prepare_spmm_csr_opt_alg2_preprocess",
+    "flagsparse_spmm_csr_opt",
+    "flagsparse_spmm_csr_opt_alg1",
+    "flagsparse_spmm_csr_opt_alg1_preprocess",
+    "flagsparse_spmm_csr_opt_alg2",
+    "flagsparse_spmm_csr_opt_alg2_preprocess",
+    "coo_to_csr_for_spmv",
+    "prepare_spmv_coo_tocsr",
+    "flagsparse_spmv_coo_tocsr",
 ]

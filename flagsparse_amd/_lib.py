@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "fs_spmm_csr",
     "fs_csr_transpose_workspace_bytes",
     "fs_csr_transpose",
+    "fs_coo_to_csr_workspace_bytes",
+    "fs_coo_to_csr",
 )
 
 
@@ -108,6 +110,10 @@ def _declare(lib):
     lib.fs_csr_transpose.restype = _i32
     lib.fs_csr_transpose.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32,
                                      _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.fs_coo_to_csr_workspace_bytes.restype = _sz
+    lib.fs_coo_to_csr_workspace_bytes.argtypes = [_i64, _i64, _i64]
+    lib.fs_coo_to_csr.restype = _i32
+    lib.fs_coo_to_csr.argtypes = [_i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _sz, _vp]
 
 
 def load_library(path=None):

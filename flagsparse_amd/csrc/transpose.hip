@@ -423,6 +423,83 @@ int transpose_ptr(const Layout& L, char* ws, int idx_t, int ptr_t, int oi, int o
   return transpose_out<V, int64_t>(L, ws, idx_t, oi, op, n_rows, n_cols, nnz, vals, cols, indptr, conj, tv, tc, tp, s);
 }
 
+
+// ---- COO -> CSR (stable lexicographic sort by (row, col)) ----
+template <class IR, class K>
+__global__ __launch_bounds__(256) void coo_keys_kernel(const IR* __restrict__ rows, const IR* __restrict__ cols,
+                                                       int64_t n, int64_t n_cols, K* __restrict__ keys) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < n) keys[k] = (K)((uint64_t)rows[k] * (uint64_t)n_cols + (uint64_t)cols[k]);
+}
+
+template <class V, class K, class Pos>
+__global__ __launch_bounds__(256) void coo_gather_kernel(const V* __restrict__ vals, const K* __restrict__ keys,
+                                                         const Pos* __restrict__ perm, int64_t n, int64_t n_cols,
+                                                         V* __restrict__ out_vals, int32_t* __restrict__ out_cols) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n) return;
+  const int64_t p = perm ? (int64_t)perm[k] : k;
+  out_vals[k] = vals[p];
+  out_cols[k] = (int32_t)((uint64_t)keys[k] % (uint64_t)n_cols);
+}
+
+// indptr[r] = first position whose row >= r, read off the sorted keys.
+template <class K>
+__global__ __launch_bounds__(256) void coo_indptr_kernel(const K* __restrict__ keys, int64_t n, int64_t n_rows,
+                                                         int64_t n_cols, int64_t* __restrict__ indptr) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k > n) return;
+  const int64_t prev = k > 0 ? (int64_t)((uint64_t)keys[k - 1] / (uint64_t)n_cols) : -1;
+  const int64_t cur = k < n ? (int64_t)((uint64_t)keys[k] / (uint64_t)n_cols) : n_rows;
+  for (int64_t r = prev + 1; r <= cur; ++r) indptr[r] = k;
+}
+
+template <class V, class IR, class K, class Pos>
+int coo_to_csr_typed(const Layout& L, char* ws, int64_t n, int64_t n_rows, int64_t n_cols, const void* vals,
+                     const void* rows, const void* cols, int assume_sorted, void* out_vals, void* out_cols,
+                     void* out_indptr, hipStream_t s) {
+  K* keys0 = reinterpret_cast<K*>(ws + L.off_rowid);  // unsorted keys (rowid slot holds 8 B / entry)
+  const unsigned blocks = (unsigned)ceil_div(n, 256);
+  hipLaunchKernelGGL((coo_keys_kernel<IR, K>), dim3(blocks), dim3(256), 0, s, static_cast<const IR*>(rows),
+                     static_cast<const IR*>(cols), n, n_cols, keys0);
+  FS_CHECK_LAUNCH("coo_keys_kernel");
+  const K* sorted = keys0;
+  const Pos* perm = nullptr;
+  if (!assume_sorted) {
+    int rc = radix_sort_cols<K, Pos>(L, ws, keys0, 2, n, n_rows * n_cols, &sorted, &perm, s);
+    if (rc != FS_OK) return rc;
+  }
+  hipLaunchKernelGGL((coo_gather_kernel<V, K, Pos>), dim3(blocks), dim3(256), 0, s, static_cast<const V*>(vals),
+                     sorted, perm, n, n_cols, static_cast<V*>(out_vals), static_cast<int32_t*>(out_cols));
+  FS_CHECK_LAUNCH("coo_gather_kernel");
+  hipLaunchKernelGGL((coo_indptr_kernel<K>), dim3((unsigned)ceil_div(n + 1, 256)), dim3(256), 0, s, sorted, n, n_rows,
+                     n_cols, static_cast<int64_t*>(out_indptr));
+  FS_CHECK_LAUNCH("coo_indptr_kernel");
+  return FS_OK;
+}
+
+template <class V, class IR>
+int coo_to_csr_keys(const Layout& L, char* ws, int64_t n, int64_t n_rows, int64_t n_cols, const void* vals,
+                    const void* rows, const void* cols, int assume_sorted, void* ov, void* oc, void* op,
+                    hipStream_t s) {
+  if (L.key_bytes == 4 && L.pos_bytes == 4)
+    return coo_to_csr_typed<V, IR, uint32_t, uint32_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
+  if (L.key_bytes == 4)
+    return coo_to_csr_typed<V, IR, uint32_t, uint64_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
+  if (L.pos_bytes == 4)
+    return coo_to_csr_typed<V, IR, uint64_t, uint32_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
+  return coo_to_csr_typed<V, IR, uint64_t, uint64_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
+}
+
+template <class V>
+int coo_to_csr_idx(const Layout& L, char* ws, int idx_t, int64_t n, int64_t n_rows, int64_t n_cols, const void* vals,
+                   const void* rows, const void* cols, int assume_sorted, void* ov, void* oc, void* op,
+                   hipStream_t s) {
+  if (idx_t == FS_I32)
+    return coo_to_csr_keys<V, int32_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
+  return coo_to_csr_keys<V, int64_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
+}
+
 }  // namespace fs
 
 using namespace fs;
@@ -462,5 +539,41 @@ extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, 
     case FS_F64: return transpose_ptr<double>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
     case FS_C64: return transpose_ptr<c32>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
     default: return transpose_ptr<c64>(L, w, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
+  }
+}
+
+// Key range of a COO matrix: n_rows * n_cols lexicographic keys.
+static Layout coo_layout(int64_t n_rows, int64_t n_cols, int64_t nnz) {
+  const int64_t range = (n_cols > 0 && n_rows > INT64_MAX / n_cols) ? INT64_MAX : n_rows * n_cols;
+  return make_layout(n_rows, range, nnz);
+}
+
+extern "C" size_t fs_coo_to_csr_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t nnz) {
+  if (nnz <= 0) return 0;
+  return coo_layout(n_rows, n_cols, nnz).total;
+}
+
+extern "C" int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz, const void* vals,
+                             const void* rows, const void* cols, int assume_sorted, void* out_vals, void* out_cols,
+                             void* out_indptr, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!valid_types(val_t, idx_t, FS_I64)) return fail(FS_E_INVALID, "fs_coo_to_csr: bad type code");
+  if (n_rows < 0 || n_cols < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_coo_to_csr: negative size");
+  if (n_cols > 0 && n_rows > INT64_MAX / n_cols) return fail(FS_E_INVALID, "fs_coo_to_csr: n_rows * n_cols overflows");
+  if (!out_indptr) return fail(FS_E_INVALID, "fs_coo_to_csr: out_indptr is null");
+  if (nnz == 0) {
+    hipLaunchKernelGGL((fill_kernel<int64_t>), dim3((unsigned)ceil_div(n_rows + 1, 256)), dim3(256), 0, stream,
+                       static_cast<int64_t*>(out_indptr), n_rows + 1, (int64_t)0);
+    FS_CHECK_LAUNCH("fill_kernel");
+    return FS_OK;
+  }
+  if (!vals || !rows || !cols || !out_vals || !out_cols) return fail(FS_E_INVALID, "fs_coo_to_csr: null pointer");
+  const Layout L = coo_layout(n_rows, n_cols, nnz);
+  if (!ws || ws_bytes < L.total) return fail(FS_E_WORKSPACE, "fs_coo_to_csr: workspace too small");
+  char* w = static_cast<char*>(ws);
+  switch (val_t) {
+    case FS_F32: return coo_to_csr_idx<float>(L, w, idx_t, nnz, n_rows, n_cols, vals, rows, cols, assume_sorted, out_vals, out_cols, out_indptr, stream);
+    case FS_F64: return coo_to_csr_idx<double>(L, w, idx_t, nnz, n_rows, n_cols, vals, rows, cols, assume_sorted, out_vals, out_cols, out_indptr, stream);
+    case FS_C64: return coo_to_csr_idx<c32>(L, w, idx_t, nnz, n_rows, n_cols, vals, rows, cols, assume_sorted, out_vals, out_cols, out_indptr, stream);
+    default: return coo_to_csr_idx<c64>(L, w, idx_t, nnz, n_rows, n_cols, vals, rows, cols, assume_sorted, out_vals, out_cols, out_indptr, stream);
   }
 }

@@ -150,6 +150,23 @@ int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t,
                      void* t_cols, void* t_indptr, void* ws, size_t ws_bytes,
                      hipStream_t stream);
 
+/*
+ * COO -> CSR.  Replaces coo_to_csr_for_spmv (spmv_csr.py:926-950): entries
+ * are ordered by the lexicographic key row * n_cols + col (a stable sort, so
+ * already-sorted input keeps its order and duplicates keep input order; the
+ * reference's non-stable argsort leaves duplicate order unspecified), the
+ * column indices are written as int32 and the row pointer as int64, as the
+ * reference does.  rows / cols share idx_t.  assume_sorted != 0 skips the
+ * sort (the caller guarantees lexicographic order).
+ */
+size_t fs_coo_to_csr_workspace_bytes(int64_t n_rows, int64_t n_cols,
+                                     int64_t nnz);
+int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_cols,
+                  int64_t nnz, const void* vals, const void* rows,
+                  const void* cols, int assume_sorted, void* out_vals,
+                  void* out_cols, void* out_indptr, void* ws, size_t ws_bytes,
+                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -178,3 +178,22 @@ def relative_error(candidate, reference):
     if den == 0:
         return 0.0 if num == 0 else float("inf")
     return float(num / den)
+
+
+def coo_to_csr(data, row, col, shape):
+    """COO -> (data, int32 cols, int64 indptr), spmv_csr.py:926-950.
+
+    Entries ordered by the key row * n_cols + col.  The reference sorts with
+    a non-stable argsort (duplicate order unspecified); this restatement uses
+    a stable sort, which is the order the HIP path produces."""
+    n_rows, n_cols = int(shape[0]), int(shape[1])
+    data = np.asarray(data)
+    row = np.asarray(row).astype(np.int64)
+    col = np.asarray(col).astype(np.int64)
+    indptr = np.zeros(n_rows + 1, dtype=np.int64)
+    if row.size == 0:
+        return data.copy(), col.astype(np.int32), indptr
+    key = row * max(1, n_cols) + col
+    order = np.argsort(key, kind="stable")
+    indptr[1:] = np.cumsum(np.bincount(row[order], minlength=n_rows))
+    return data[order], col[order].astype(np.int32), indptr

@@ -36,7 +36,12 @@ def test_public_surface():
         "flagsparse_spmv_csr", "prepare_spmv_csr", "PreparedCsrSpmv", "flagsparse_spmm_csr",
         "flagsparse_spmm_csr_run", "prepare_spmm_csr_route", "list_spmm_csr_algorithms",
         "resolve_spmm_csr_algorithm", "SPMM_CSR_ALGORITHMS", "SpmmCsrAlgorithm",
-        "SpmmCsrAlgorithmUnavailable", "PreparedCsrSpmmRoute",
+        "SpmmCsrAlgorithmUnavailable", "PreparedCsrSpmmRoute", "PreparedCsrSpmmOpt", "PreparedCsrSpmmOptAlg2",
+        "prepare_spmm_csr_opt", "prepare_spmm_csr_opt_alg1", "prepare_spmm_csr_opt_alg1_preprocess",
+        "prepare_spmm_csr_opt_alg2", "prepare_spmm_csr_opt_alg2_preprocess", "flagsparse_spmm_csr_opt",
+        "flagsparse_spmm_csr_opt_alg1", "flagsparse_spmm_csr_opt_alg1_preprocess", "flagsparse_spmm_csr_opt_alg2",
+        "flagsparse_spmm_csr_opt_alg2_preprocess", "coo_to_csr_for_spmv", "prepare_spmv_coo_tocsr",
+        "flagsparse_spmv_coo_tocsr",
     }
     assert expected <= set(dir(fs)) and expected <= set(fs.__all__)
 

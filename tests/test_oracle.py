@@ -188,3 +188,22 @@ def test_golden_fixtures_reproduce():
             td, ti, tp, _ = O.transpose_csr(z["data"], z["indices"], z["indptr"], shape, conj=(op == "conj"))
             assert np.array_equal(tp, z["t_indptr"]) and np.array_equal(ti, z["t_indices"])
             assert np.array_equal(td, z["t_data"])
+
+
+def test_coo_to_csr_vs_scipy_and_stability():
+    rng = np.random.default_rng(5)
+    n_rows, n_cols, nnz = 50, 40, 300
+    flat = rng.choice(n_rows * n_cols, nnz, replace=False)
+    row, col = flat // n_cols, flat % n_cols
+    data = rng.uniform(-1, 1, nnz)
+    d, c, p = O.coo_to_csr(data, row, col, (n_rows, n_cols))
+    ref = sp.coo_matrix((data, (row, col)), shape=(n_rows, n_cols)).tocsr()
+    ref.sort_indices()
+    assert c.dtype == np.int32 and p.dtype == np.int64
+    assert np.array_equal(p, ref.indptr) and np.array_equal(c, ref.indices) and np.array_equal(d, ref.data)
+    # duplicates keep input order; already-sorted input is unchanged
+    row = np.array([1, 0, 1, 1]); col = np.array([2, 3, 2, 0]); data = np.array([10.0, 20.0, 30.0, 40.0])
+    d, c, p = O.coo_to_csr(data, row, col, (2, 4))
+    assert np.array_equal(d, [20.0, 40.0, 10.0, 30.0]) and np.array_equal(c, [3, 0, 2, 2]) and np.array_equal(p, [0, 1, 4])
+    d2, c2, p2 = O.coo_to_csr(d, np.array([0, 1, 1, 1]), c, (2, 4))
+    assert np.array_equal(d2, d) and np.array_equal(c2, c)
