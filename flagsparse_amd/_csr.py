@@ -11,7 +11,7 @@ These replace the reference's torch-op implementations:
 import torch
 
 from . import _lib
-from ._common import _INDEX_LIMIT_INT32, _is_complex_dtype
+from ._common import _INDEX_LIMIT_INT32, _compute_dtype, _is_complex_dtype
 
 
 class CsrPlan:
@@ -70,7 +70,7 @@ def analyze_csr(data, indices, indptr, n_rows, n_cols, force_kernel=-1):
             _lib.ptr(indptr),
             _lib.index_code(indptr.dtype),
             _lib.index_code(indices.dtype),
-            _lib.value_code(data.dtype),
+            _lib.value_code(_compute_dtype(data.dtype)),
             int(n_rows),
             int(n_cols),
             int(data.numel()),
@@ -99,6 +99,10 @@ def transpose_csr(data, indices, indptr, shape, conj=False):
     n_rows, n_cols = int(shape[0]), int(shape[1])
     nnz = data.numel()
     device = data.device
+    if data.dtype in (torch.float16, torch.bfloat16):
+        # the permutation is exact through float32 (16-bit values round-trip)
+        td, ti, tp, tsh = transpose_csr(data.to(torch.float32), indices, indptr, shape, conj=False)
+        return td.to(data.dtype), ti, tp, tsh
     out_index_dtype, out_indptr_dtype = transpose_out_dtypes(indices.dtype, indptr.dtype, n_rows, nnz)
     t_indptr = torch.empty(n_cols + 1, dtype=out_indptr_dtype, device=device)
     if nnz == 0:

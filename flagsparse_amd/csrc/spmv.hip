@@ -245,6 +245,11 @@ struct StreamChunk {
   I c[K];
 };
 
+// Persistent row-block walk (variant 4): a few workgroups per CU walk row
+// blocks with a grid-sized stride; only the next block's row pointers are
+// prefetched (its data loads wait for them anyway), which removes the
+// pointer round trip from each block's critical path without holding a
+// second copy of the data in registers.
 template <int TPR, class V, class I, class P>
 __global__ __launch_bounds__(256) void spmv_stream_persistent_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
@@ -258,69 +263,51 @@ __global__ __launch_bounds__(256) void spmv_stream_persistent_kernel(
   __shared__ int64_t s_ptr[R + 1];
   const int t = threadIdx.x;
   const int64_t n_blocks = (n_rows + R - 1) / R;
-  // block walk: [first, last) with stride
-  int64_t first, last, stride;
-  if (xcd_split) {
-    const int groups = 8;
-    const int g = blockIdx.x % groups;
-    const int64_t per = (n_blocks + groups - 1) / groups;
-    first = g * per + blockIdx.x / groups;
-    last = (g + 1) * per < n_blocks ? (g + 1) * per : n_blocks;
-    stride = (gridDim.x + groups - 1 - g) / groups;  // workgroups of this XCD
-  } else {
-    first = blockIdx.x;
-    last = n_blocks;
-    stride = gridDim.x;
-  }
-  auto rows_of = [&](int64_t blk) -> int {
-    const int64_t r = n_rows - blk * R;
+  int64_t blk = blockIdx.x;
+  const int64_t stride = gridDim.x;
+  (void)xcd_split;
+  if (blk >= n_blocks) return;  // uniform per workgroup
+  auto rows_of = [&](int64_t b) -> int {
+    const int64_t r = n_rows - b * R;
     return r < R ? (int)r : R;
   };
-  auto load_chunk = [&](int64_t S, int cnt, StreamChunk<V, I, K>& ch) {
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int q = t + 256 * k;
-      ch.c[k] = 0;
-      if (q < cnt) {
-        ch.v[k] = vals[S + q];
-        ch.c[k] = cols[S + q];
-      }
-    }
-  };
-  if (first >= last) return;  // uniform per workgroup
-  // prologue: pointers + stream of the first block
-  int64_t blk = first;
   int rows = rows_of(blk);
   int64_t my_ptr = (t <= rows) ? (int64_t)rowptr[blk * R + t] : 0;
   int64_t S = (int64_t)rowptr[blk * R];
   int64_t E = (int64_t)rowptr[blk * R + rows];
-  StreamChunk<V, I, K> cur;
-  load_chunk(S, (int)(E - S), cur);
   while (true) {
-    const int64_t nblk = blk + stride;
-    const bool has_next = nblk < last;
-    // gathers of the current block
-    V xv[K];
     const int cnt = (int)(E - S);
+    V v[K];
+    I c[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (t + 256 * k < cnt) xv[k] = x[cur.c[k]];
-    // next block's pointers and stream go out before the gathers return
+    for (int k = 0; k < K; ++k) {
+      const int q = t + 256 * k;
+      c[k] = 0;
+      if (q < cnt) {
+        v[k] = vals[S + q];
+        c[k] = cols[S + q];
+      }
+    }
+    // next block's pointers go out with the current data loads
+    const int64_t nblk = blk + stride;
+    const bool has_next = nblk < n_blocks;
     int nrows = 0;
     int64_t nS = 0, nE = 0, nptr = 0;
-    StreamChunk<V, I, K> nxt;
     if (has_next) {
       nrows = rows_of(nblk);
       nS = (int64_t)rowptr[nblk * R];
       nE = (int64_t)rowptr[nblk * R + nrows];
       nptr = (t <= nrows) ? (int64_t)rowptr[nblk * R + t] : 0;
-      load_chunk(nS, (int)(nE - nS), nxt);
     }
+    V xv[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (t + 256 * k < cnt) xv[k] = x[c[k]];
     if (t <= rows) s_ptr[t] = my_ptr;
     if (t == 0 && rows == 256) s_ptr[256] = E;
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(cur.v[k], xv[k]);
+      if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(v[k], xv[k]);
     __syncthreads();
     const int r = t / TPR;
     const int sub = t % TPR;
@@ -339,26 +326,25 @@ __global__ __launch_bounds__(256) void spmv_stream_persistent_kernel(
     S = nS;
     E = nE;
     my_ptr = nptr;
-    cur = nxt;
   }
 }
 
 // ---------------------------------------------------------------------------
-// K2: merge-path SpMV, one wave per tile of kSlabs*64 merge items.
+// K2: merge-path SpMV, one wave per tile of 512 merge items (row ends +
+// nnz; the partition balances their sum, so long and short rows cost the
+// same per item).
 //
-// Item d of the tile is either a row end or one nnz.  For every 64-item
-// slab the wave
-//   1. marks which items are row ends (row-end positions are scattered into
-//      a 64-entry LDS table and read back, then ballot -> 64-bit mask held in
-//      scalar registers);
-//   2. loads the nnz of the slab (contiguous, coalesced) and gathers x;
-//   3. runs a segmented inclusive scan across the wave with DPP row shifts
-//      and row broadcasts; the lane holding a row end then owns that row's
-//      sum.
-// A running carry links slabs.  Rows that start in an earlier tile write
-// their in-tile part to head[t]; the part of the last open row goes to
-// tail[t]; merge_fixup_kernel adds them in tile order, so results are
-// deterministic and no floating-point atomics are used.
+// The tile's nnz are loaded with unit stride, x is gathered, and the
+// products are staged in LDS.  Row ends become a 512-bit tile mask in LDS
+// (one ds_or per row end).  Each lane then walks 8 consecutive items
+// sequentially: its starting row comes from popcounts of the mask, rows
+// that start and end inside the lane are stored directly, the first row it
+// closes waits for the lane carry.  One segmented scan of the 64 lane
+// tails per tile (DPP row shifts and row broadcasts) supplies the carries.
+// Rows that start in an earlier tile write their in-tile part to head[t];
+// the part of the last open row goes to tail[t]; merge_fixup_kernel adds
+// them in tile order, so results are deterministic and no floating-point
+// atomics are used.
 // ---------------------------------------------------------------------------
 constexpr int kSlabs = 8;
 constexpr int kMergeTile = kSlabs * 64;
@@ -431,6 +417,13 @@ __device__ inline c64 readlane_acc<c64>(c64 v, int lane) {
   return c64{readlane_f64(v.re, lane), readlane_f64(v.im, lane)};
 }
 
+// Item layout of a tile: item d (0..511) is a row end if bit d of the
+// tile mask is set, otherwise the next nnz.  Lane l walks items
+// [8l, 8l+8) sequentially; the products it needs were staged in LDS by
+// coalesced loads (index padded by j/8 so that lanes starting 8 products
+// apart hit different banks).
+__device__ inline int prod_slot(int j) { return j + (j >> 3); }
+
 template <class V, class I, class P>
 __global__ __launch_bounds__(256) void spmv_merge_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
@@ -439,8 +432,10 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
     int64_t n_rows, int64_t nnz, int64_t n_tiles) {
   using T = VT<V>;
   using A = typename T::acc;
-  __shared__ P s_end[kMergeWaves][kMergeTile];
-  __shared__ int s_tab[kMergeWaves][64];
+  constexpr int kIpt = kMergeTile / 64;  // items per lane
+  __shared__ unsigned s_mask[kMergeWaves][kMergeTile / 32];
+  __shared__ int s_pre[kMergeWaves][kMergeTile / 32];
+  __shared__ A s_prod[kMergeWaves][kMergeTile + kMergeTile / 8];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -453,92 +448,97 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
   const int64_t total = n_rows + nnz;
   const int64_t dend = d0 + kMergeTile < total ? d0 + kMergeTile : total;
   const int64_t n0 = d0 - r0;
-  const int64_t n1 = dend - r1;  // exclusive nnz end of the tile
   const int R = (int)(r1 - r0);
-  P* end = s_end[w];
-  int* tab = s_tab[w];
+  const int Nz = (int)(dend - r1 - n0);
+  const int items = R + Nz;
+  unsigned* msk = s_mask[w];
+  A* prod = s_prod[w];
 
-  for (int k = lane; k < R; k += 64) end[k] = rowptr[r0 + 1 + k];
+  // 1. products of the tile's nnz: coalesced loads, x gathers, LDS stage.
+  V av[kIpt];
+  I cv[kIpt];
+#pragma unroll
+  for (int k = 0; k < kIpt; ++k) {
+    const int j = k * 64 + lane;
+    cv[k] = 0;
+    if (j < Nz) {
+      av[k] = vals[n0 + j];
+      cv[k] = cols[n0 + j];
+    }
+  }
+  // 2. row-end mask (one ds_or per row end).
+  if (lane < kMergeTile / 32) msk[lane] = 0u;
+  V xv[kIpt];
+#pragma unroll
+  for (int k = 0; k < kIpt; ++k)
+    if (k * 64 + lane < Nz) xv[k] = x[cv[k]];
+  wave_sync();
+#pragma unroll
+  for (int i = 0; i < kIpt; ++i) {
+    const int k = lane + 64 * i;
+    if (k < R) {
+      const int q = (int)((r0 + k) + (int64_t)rowptr[r0 + 1 + k] - d0);
+      atomicOr(&msk[q >> 5], 1u << (q & 31));
+    }
+  }
   const bool head_partial = R > 0 && (int64_t)rowptr[r0] < n0;
+#pragma unroll
+  for (int k = 0; k < kIpt; ++k) {
+    const int j = k * 64 + lane;
+    if (j < Nz) prod[prod_slot(j)] = T::mul(av[k], xv[k]);
+  }
+  wave_sync();
+  // exclusive prefix of row ends per 32-item word
+  if (lane == 0) {
+    int run = 0;
+#pragma unroll
+    for (int q = 0; q < kMergeTile / 32; ++q) {
+      s_pre[w][q] = run;
+      run += __popc(msk[q]);
+    }
+  }
   wave_sync();
 
-  // Pass 1: classify items of every slab (row end or nnz).
-  uint64_t masks[kSlabs];
-  int is_[kSlabs];
-  int js_[kSlabs];
-  int i_s = 0, j_s = 0;
+  // 3. sequential walk of this lane's 8 items.
+  const int d = kIpt * lane;                          // first item of the lane
+  const unsigned word = msk[d >> 5];
+  const unsigned pattern = (word >> (d & 31)) & 0xFFu;  // 8 items never straddle a word
+  const int i_l = s_pre[w][d >> 5] + __popc(word & ((1u << (d & 31)) - 1u));
+  int j = d - i_l;                                     // tile-local nnz index
+  int ends = 0;
+  A acc = T::zero(), first = T::zero();
 #pragma unroll
-  for (int s = 0; s < kSlabs; ++s) {
-    tab[lane] = 0;
-    wave_sync();
-    const int k = i_s + lane;
-    if (k < R) {
-      int64_t q = (r0 + k) + (int64_t)end[k] - (d0 + 64 * s);
-      if (q < 64) tab[(int)q] = 1;
+  for (int u = 0; u < kIpt; ++u) {
+    if (d + u < items) {
+      if ((pattern >> u) & 1u) {
+        if (ends == 0) {
+          first = acc;
+        } else {
+          y[r0 + i_l + ends] = T::out(acc);
+        }
+        ++ends;
+        acc = T::zero();
+      } else {
+        acc = add(acc, prod[prod_slot(j)]);
+        ++j;
+      }
     }
-    wave_sync();
-    const bool e = tab[lane] != 0;
-    const uint64_t m = __ballot(e);
-    masks[s] = m;
-    is_[s] = i_s;
-    js_[s] = j_s;
-    const int cnt = __popcll(m);
-    i_s += cnt;
-    j_s += 64 - cnt;
-    wave_sync();
   }
 
-  // Pass 2: issue every slab's loads before any arithmetic.
-  V av[kSlabs];
-  I cv[kSlabs];
-  bool ok[kSlabs];
-#pragma unroll
-  for (int s = 0; s < kSlabs; ++s) {
-    const uint64_t m = masks[s];
-    const bool is_end = (m >> lane) & 1ull;
-    const int64_t j = n0 + js_[s] + lane - count_below(m);
-    ok[s] = !is_end && j < n1;
-    if (ok[s]) {
-      av[s] = vals[j];
-      cv[s] = cols[j];
-    } else {
-      cv[s] = 0;
-    }
-  }
-  V xv[kSlabs];
-#pragma unroll
-  for (int s = 0; s < kSlabs; ++s) {
-    if (ok[s]) xv[s] = x[cv[s]];
-  }
-
-  // Pass 3: segmented scan per slab.
-  A carry = T::zero();
-#pragma unroll
-  for (int s = 0; s < kSlabs; ++s) {
-    const uint64_t m = masks[s];
-    const bool is_end = (m >> lane) & 1ull;
-    const int before = count_below(m);
-    A v = ok[s] ? T::mul(av[s], xv[s]) : T::zero();
-    const int f = (lane == 0) || ((m >> (lane - 1)) & 1ull) ? 1 : 0;
-    v = seg_scan(v, f);
-    if (is_end) {
-      A sum = v;
-      if (before == 0) sum = add(sum, carry);
-      const int64_t row = r0 + is_[s] + before;
-      if (row == r0 && head_partial)
-        head[t] = sum;
-      else
-        y[row] = T::out(sum);
-    }
-    const A last = readlane_acc(v, 63);
-    if ((m >> 63) & 1ull)
-      carry = T::zero();
-    else if (m == 0)
-      carry = add(carry, last);
+  // 4. carry across lanes: inclusive segmented scan of lane tails (a lane
+  // with a row end starts a new segment), shifted to exclusive.
+  const A incl = seg_scan(acc, ends > 0 ? 1 : 0);
+  A carry_in = shfl(incl, lane > 0 ? lane - 1 : 0);
+  if (lane == 0) carry_in = T::zero();
+  if (ends > 0) {
+    const A v = add(carry_in, first);
+    const int64_t row = r0 + i_l;
+    if (row == r0 && head_partial)
+      head[t] = v;
     else
-      carry = last;
+      y[row] = T::out(v);
   }
-  if (lane == 0 && r1 < n_rows) tail[t] = carry;
+  if (lane == 63 && r1 < n_rows) tail[t] = incl;
 }
 
 // Rows that span tiles: y[row] = tail[f] + ... + tail[t-1] + head[t], where

@@ -206,7 +206,7 @@ class _SpmmPlan:
 
     def __init__(self, data, indices, indptr, n_rows, n_cols):
         self.csr = analyze_csr(data, indices, indptr, n_rows, n_cols)
-        self.tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(data.dtype), 0))
+        self.tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(_compute_dtype(data.dtype)), 0))
         self.n_tiles = self.csr.n_tiles(self.tile_items)
         self.part = self.csr.partition(indptr, self.tile_items)
 

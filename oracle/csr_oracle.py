@@ -197,3 +197,53 @@ def coo_to_csr(data, row, col, shape):
     order = np.argsort(key, kind="stable")
     indptr[1:] = np.cumsum(np.bincount(row[order], minlength=n_rows))
     return data[order], col[order].astype(np.int32), indptr
+
+
+def load_mtx_reference(file_path):
+    """Literal restatement of the reference's loader (tests/test_spmv.py:103-176):
+    per-row dicts accumulated in file order, sorted columns.  Returns float64
+    data, int64 indices / indptr and the shape."""
+    with open(file_path, "r", encoding="utf-8") as f:
+        lines = f.readlines()
+    field, symmetry = "real", "general"
+    data_lines, header = [], None
+    for line in lines:
+        s = line.strip()
+        if s.startswith("%%MatrixMarket"):
+            tok = s.split()
+            if len(tok) >= 5:
+                field, symmetry = tok[3].lower(), tok[4].lower()
+            continue
+        if s.startswith("%"):
+            continue
+        if not header and s:
+            p = s.split()
+            header = (int(p[0]), int(p[1]), int(p[2]) if len(p) > 2 else 0)
+            continue
+        if s:
+            data_lines.append(s)
+    n_rows, n_cols, nnz = header
+    if nnz == 0:
+        return np.empty(0), np.empty(0, dtype=np.int64), np.zeros(n_rows + 1, dtype=np.int64), (n_rows, n_cols)
+    pattern = field == "pattern"
+    sym = symmetry in ("symmetric", "hermitian")
+    skew = symmetry == "skew-symmetric"
+    rows = [dict() for _ in range(n_rows)]
+    for line in data_lines[:nnz]:
+        p = line.split()
+        r, c = int(p[0]) - 1, int(p[1]) - 1
+        v = 1.0 if pattern else float(p[2])
+        if 0 <= r < n_rows and 0 <= c < n_cols:
+            rows[r][c] = rows[r].get(c, 0.0) + v
+            if r != c:
+                if sym and 0 <= c < n_rows and 0 <= r < n_cols:
+                    rows[c][r] = rows[c].get(r, 0.0) + v
+                elif skew and 0 <= c < n_rows and 0 <= r < n_cols:
+                    rows[c][r] = rows[c].get(r, 0.0) - v
+    cols, vals, indptr = [], [], [0]
+    for row in rows:
+        for c in sorted(row):
+            cols.append(c)
+            vals.append(row[c])
+        indptr.append(len(cols))
+    return np.array(vals, dtype=np.float64), np.array(cols, dtype=np.int64), np.array(indptr, dtype=np.int64), (n_rows, n_cols)

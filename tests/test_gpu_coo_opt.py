@@ -105,3 +105,23 @@ def test_spmm_opt_rejects_complex(device):
         fs.flagsparse_spmm_csr_opt_alg2(d, i, p, B, sh)
     with pytest.raises(TypeError, match="prepared must be a PreparedCsrSpmmOpt instance"):
         fs.flagsparse_spmm_csr_opt(B=B, prepared=object())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["float16", "bfloat16"])
+@pytest.mark.parametrize("op", ["non", "trans"])
+def test_half_precision_spmv_spmm(device, dtype, op):
+    """f16 / bf16 are accepted and computed in f32 (reference: spmv_csr.py:124-127,
+    spmm_csr.py:2716-2719); outputs keep the input dtype."""
+    d32, i, p, sh = S.random_csr(300, 200, 0.05, torch.float32, torch.int32, device, seed=6, long_rows=((3, 190),))
+    d = d32.to(dtype)
+    m_in = 300 if op != "non" else 200
+    x = S.vector(m_in, torch.float32, device, seed=7).to(dtype)
+    y = fs.flagsparse_spmv_csr(d, i, p, x, sh, op=op)
+    assert y.dtype == dtype
+    ref = O.spmv_csr_wide(np_(d.float()), np_(i), np_(p), np_(x.float()), sh, op=op)
+    assert rel_err(np_(y.float()), ref) <= REL_TOL[dtype]
+    B = S.dense(m_in, 20, torch.float32, device, seed=8).to(dtype)
+    C = fs.flagsparse_spmm_csr(d, i, p, B, sh, op=op)
+    assert C.dtype == dtype
+    refC = O.spmm_csr_wide(np_(d.float()), np_(i), np_(p), np_(B.float()), sh, op=op)
+    assert rel_err(np_(C.float()), refC) <= REL_TOL[dtype]
