@@ -182,10 +182,22 @@ def run(args):
             _lib.stream_handle(device),
         )
         kernel_call = lambda: lib.fs_spmv_csr(*args_abi)  # noqa: E731
+        pan = prep._panels
+        if pan is not None:
+            # column panels: the timed call is the whole panel sequence
+            # (block table, panel merge, fixup, panel reduction)
+            args_abi = (
+                pan.plan.plan, pan.n_panels, pan.panel_nnz, _lib.ptr(pan.data), _lib.ptr(pan.indices), _lib.ptr(pan.indptr),
+                _lib.ptr(x), _lib.ptr(y), _lib.ptr(pan.part), _lib.ptr(pan.ws), pan.ws.numel(),
+                _lib.stream_handle(device),
+            )
+            kernel_call = lambda: lib.fs_spmv_csr_panels(*args_abi)  # noqa: E731
+            extra["n_panels"] = pan.n_panels
         bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
         flops = S.flops_spmv(nnz, complex_values)
-        kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel"}[plan.kernel_name]
-        extra.update(kernel_variant=plan.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
+        kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
+                       "panel": "spmv_panel_merge_kernel"}[prep.kernel_name]
+        extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:
         n_dense = cfg["n"]

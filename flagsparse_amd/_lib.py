@@ -45,6 +45,10 @@ EXPORTED_SYMBOLS = (
     "fs_csr_transpose",
     "fs_coo_to_csr_workspace_bytes",
     "fs_coo_to_csr",
+    "fs_csr_panelize_workspace_bytes",
+    "fs_csr_panelize",
+    "fs_spmv_panels_workspace_bytes",
+    "fs_spmv_csr_panels",
 )
 
 
@@ -114,6 +118,16 @@ def _declare(lib):
     lib.fs_coo_to_csr_workspace_bytes.argtypes = [_i64, _i64, _i64]
     lib.fs_coo_to_csr.restype = _i32
     lib.fs_coo_to_csr.argtypes = [_i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.fs_csr_panelize_workspace_bytes.restype = _sz
+    lib.fs_csr_panelize_workspace_bytes.argtypes = [_i64, _i64, _i64, _i32]
+    lib.fs_csr_panelize.restype = _i32
+    lib.fs_csr_panelize.argtypes = [_i32, _i32, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                    ctypes.POINTER(_i64), _vp, _sz, _vp]
+    lib.fs_spmv_panels_workspace_bytes.restype = _sz
+    lib.fs_spmv_panels_workspace_bytes.argtypes = [ctypes.POINTER(FsCsrPlan), _i32]
+    lib.fs_spmv_csr_panels.restype = _i32
+    lib.fs_spmv_csr_panels.argtypes = [ctypes.POINTER(FsCsrPlan), _i32, ctypes.POINTER(_i64), _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _vp, _sz, _vp]
 
 
 def load_library(path=None):

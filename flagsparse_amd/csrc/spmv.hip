@@ -424,23 +424,27 @@ __device__ inline c64 readlane_acc<c64>(c64 v, int lane) {
 // apart hit different banks).
 __device__ inline int prod_slot(int j) { return j + (j >> 3); }
 
-template <class V, class I, class P>
-__global__ __launch_bounds__(256) void spmv_merge_kernel(
-    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
-    const V* __restrict__ x, V* __restrict__ y, const int64_t* __restrict__ part,
-    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail,
-    int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+// Row results go to y as the value type, or (for column-panel partials)
+// as the accumulator type, so that a later reduction rounds only once.
+template <class V, class Y>
+__device__ inline void store_row(Y* y, int64_t row, typename VT<V>::acc v) {
+  if constexpr (std::is_same<Y, typename VT<V>::acc>::value)
+    y[row] = v;
+  else
+    y[row] = VT<V>::out(v);
+}
+
+// One merge tile, processed by one wave (per-wave LDS slices passed in).
+template <class V, class I, class P, class Y>
+__device__ inline void merge_tile(const V* __restrict__ vals, const I* __restrict__ cols,
+                                  const P* __restrict__ rowptr, const V* __restrict__ x, Y* __restrict__ y,
+                                  const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
+                                  typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz,
+                                  int64_t t, unsigned* msk, typename VT<V>::acc* prod) {
   using T = VT<V>;
   using A = typename T::acc;
   constexpr int kIpt = kMergeTile / 64;  // items per lane
-  __shared__ unsigned s_mask[kMergeWaves][kMergeTile / 32];
-  __shared__ int s_pre[kMergeWaves][kMergeTile / 32];
-  __shared__ A s_prod[kMergeWaves][kMergeTile + kMergeTile / 8];
-
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * kMergeWaves + w;
-  if (t >= n_tiles) return;  // per-wave work only; no block barriers below
 
   const int64_t r0 = part[t];
   const int64_t r1 = part[t + 1];
@@ -451,8 +455,6 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
   const int R = (int)(r1 - r0);
   const int Nz = (int)(dend - r1 - n0);
   const int items = R + Nz;
-  unsigned* msk = s_mask[w];
-  A* prod = s_prod[w];
 
   // 1. products of the tile's nnz: coalesced loads, x gathers, LDS stage.
   V av[kIpt];
@@ -488,22 +490,21 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
     if (j < Nz) prod[prod_slot(j)] = T::mul(av[k], xv[k]);
   }
   wave_sync();
-  // exclusive prefix of row ends per 32-item word
-  if (lane == 0) {
-    int run = 0;
-#pragma unroll
-    for (int q = 0; q < kMergeTile / 32; ++q) {
-      s_pre[w][q] = run;
-      run += __popc(msk[q]);
-    }
-  }
-  wave_sync();
-
-  // 3. sequential walk of this lane's 8 items.
+  // 3. sequential walk of this lane's 8 items.  Row ends before the lane:
+  // popcounts of the 16 mask words, scanned over lanes 0..15 with DPP row
+  // shifts (one 16-lane row), read back from lane d/32 by a permute.
+  static_assert(kMergeTile / 32 == 16, "word scan covers one DPP row");
   const int d = kIpt * lane;                          // first item of the lane
   const unsigned word = msk[d >> 5];
+  const int cnt = lane < 16 ? __popc(msk[lane]) : 0;
+  int inc = cnt;
+  inc += dpp_shift<0x111, 0xF>(inc);  // row_shr:1
+  inc += dpp_shift<0x112, 0xF>(inc);  // row_shr:2
+  inc += dpp_shift<0x114, 0xF>(inc);  // row_shr:4
+  inc += dpp_shift<0x118, 0xF>(inc);  // row_shr:8
+  const int word_pre = __shfl(inc - cnt, d >> 5);
   const unsigned pattern = (word >> (d & 31)) & 0xFFu;  // 8 items never straddle a word
-  const int i_l = s_pre[w][d >> 5] + __popc(word & ((1u << (d & 31)) - 1u));
+  const int i_l = word_pre + __popc(word & ((1u << (d & 31)) - 1u));
   int j = d - i_l;                                     // tile-local nnz index
   int ends = 0;
   A acc = T::zero(), first = T::zero();
@@ -514,7 +515,7 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
         if (ends == 0) {
           first = acc;
         } else {
-          y[r0 + i_l + ends] = T::out(acc);
+          store_row<V>(y, r0 + i_l + ends, acc);
         }
         ++ends;
         acc = T::zero();
@@ -536,18 +537,98 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
     if (row == r0 && head_partial)
       head[t] = v;
     else
-      y[row] = T::out(v);
+      store_row<V>(y, row, v);
   }
   if (lane == 63 && r1 < n_rows) tail[t] = incl;
 }
 
+template <class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_merge_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, const int64_t* __restrict__ part,
+    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail,
+    int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+  using A = typename VT<V>::acc;
+  __shared__ unsigned s_mask[kMergeWaves][kMergeTile / 32];
+  __shared__ A s_prod[kMergeWaves][kMergeTile + kMergeTile / 8];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int64_t t = (int64_t)blockIdx.x * kMergeWaves + w;
+  if (t >= n_tiles) return;  // per-wave work only; no block barriers
+  merge_tile<V, I, P, V>(vals, cols, rowptr, x, y, part, head, tail, n_rows, nnz, t, s_mask[w], s_prod[w]);
+}
+
+// ---------------------------------------------------------------------------
+// K2p: merge-path SpMV over a column-panelled matrix.  The stacked CSR holds
+// panel p's entries (columns [p*width, (p+1)*width)) as rows p*n + r, so the
+// x gathers of one panel touch one slice of x.  Workgroups are handed out to
+// the 8 XCDs round-robin by workgroup id; workgroup b runs on XCD b % 8 and
+// takes the tile blocks of panel (b % 8), so each XCD's L2 holds one x
+// slice instead of all of x.  Panel results are accumulator-typed partials
+// (panel-major); panel_reduce_kernel sums them per row in panel order.
+// ---------------------------------------------------------------------------
+constexpr int kMaxPanels = 64;
+struct PanelTable {
+  int64_t first[kMaxPanels + 1];  // first merge block of each panel; [n_panels] = number of blocks
+};
+
+template <class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_panel_merge_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, typename VT<V>::acc* __restrict__ y, const int64_t* __restrict__ part,
+    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail, const PanelTable tab,
+    int n_panels, int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+  using A = typename VT<V>::acc;
+  __shared__ unsigned s_mask[kMergeWaves][kMergeTile / 32];
+  __shared__ A s_prod[kMergeWaves][kMergeTile + kMergeTile / 8];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  // With fewer panels than XCDs (n_panels dividing 8) panel p is shared by
+  // XCDs p, p + n_panels, ...; each takes every G-th block of the panel.
+  // Otherwise XCD x owns panels x, x + 8, ... and its workgroups (slot 0,
+  // 1, ...) take their blocks in that order.  One block per workgroup.
+  const int xcd = (int)(blockIdx.x % kXcds);
+  int64_t slot = blockIdx.x / kXcds;
+  int64_t b = -1;
+  if (n_panels < kXcds && kXcds % n_panels == 0) {
+    const int G = kXcds / n_panels;
+    const int p = xcd % n_panels;
+    b = tab.first[p] + slot * G + xcd / n_panels;
+    if (b >= tab.first[p + 1]) return;
+  } else {
+    for (int p = xcd; p < n_panels; p += kXcds) {
+      const int64_t nb = tab.first[p + 1] - tab.first[p];
+      if (slot < nb) {
+        b = tab.first[p] + slot;
+        break;
+      }
+      slot -= nb;
+    }
+    if (b < 0) return;
+  }
+  const int64_t t = b * kMergeWaves + w;
+  if (t >= n_tiles) return;
+  merge_tile<V, I, P, A>(vals, cols, rowptr, x, y, part, head, tail, n_rows, nnz, t, s_mask[w], s_prod[w]);
+}
+
+// y[r] = sum over panels p (in order) of partial[p * n_rows + r], rounded once.
+template <class V>
+__global__ __launch_bounds__(256) void panel_reduce_kernel(const typename VT<V>::acc* __restrict__ partial,
+                                                           V* __restrict__ y, int64_t n_rows, int n_panels) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  A sum = partial[r];
+  for (int p = 1; p < n_panels; ++p) sum = add(sum, partial[(int64_t)p * n_rows + r]);
+  y[r] = T::out(sum);
+}
+
 // Rows that span tiles: y[row] = tail[f] + ... + tail[t-1] + head[t], where
 // tiles f..t-1 all end inside `row` and tile t holds its row end.
-template <class V, class P>
+template <class V, class P, class Y = V>
 __global__ __launch_bounds__(256) void merge_fixup_kernel(
     const P* __restrict__ rowptr, const int64_t* __restrict__ part,
     const typename VT<V>::acc* __restrict__ head, const typename VT<V>::acc* __restrict__ tail,
-    V* __restrict__ y, int64_t n_tiles, int64_t tile_items) {
+    Y* __restrict__ y, int64_t n_tiles, int64_t tile_items) {
   using T = VT<V>;
   using A = typename T::acc;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -561,7 +642,7 @@ __global__ __launch_bounds__(256) void merge_fixup_kernel(
   A sum = tail[f];
   for (int64_t k = f + 1; k < t; ++k) sum = add(sum, tail[k]);
   sum = add(sum, head[t]);
-  y[r0] = T::out(sum);
+  store_row<V>(y, r0, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -686,6 +767,69 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
                      stream, p, static_cast<const int64_t*>(part), head, tail, yv, n_tiles,
                      (int64_t)kMergeTile);
   FS_CHECK_LAUNCH("merge_fixup_kernel");
+  return FS_OK;
+}
+
+// Column-panel SpMV: workspace = head/tail carries and accumulator partials
+// (one per stacked row).
+struct PanelWs {
+  size_t off_carry, off_partial, total;
+};
+inline size_t align256s(size_t v) { return (v + 255) & ~(size_t)255; }
+inline PanelWs panel_ws(const fs_csr_plan* plan, int n_panels, size_t acc) {
+  PanelWs L{};
+  size_t o = 0;
+  L.off_carry = o; o = align256s(o + (size_t)plan->n_tiles * 2 * acc);
+  L.off_partial = o; o = align256s(o + (size_t)plan->n_rows * acc);
+  L.total = o;
+  return L;
+}
+
+template <class V, class I, class P>
+int launch_spmv_panels(const fs_csr_plan* plan, int n_panels, const int64_t* panel_nnz, const void* vals,
+                       const void* cols, const void* indptr, const void* x, void* y, const void* part, void* ws,
+                       size_t ws_bytes, int64_t n_out, hipStream_t stream) {
+  using A = typename VT<V>::acc;
+  const PanelWs L = panel_ws(plan, n_panels, sizeof(A));
+  if (ws == nullptr || ws_bytes < L.total) return fail(FS_E_WORKSPACE, "fs_spmv_csr_panels: workspace too small");
+  char* w = static_cast<char*>(ws);
+  A* head = reinterpret_cast<A*>(w + L.off_carry);
+  A* tail = head + plan->n_tiles;
+  A* partial = reinterpret_cast<A*>(w + L.off_partial);
+  const P* p = static_cast<const P*>(indptr);
+  const int64_t n_tiles = plan->n_tiles;
+  const int64_t n_blocks = ceil_div(n_tiles, kMergeWaves);
+  // Block table from the panel starts: panel q begins at merge item
+  // q * n_out + panel_nnz[q]; a block shared by two panels goes to the later.
+  PanelTable tab{};
+  tab.first[0] = 0;
+  for (int q = 1; q < n_panels; ++q) {
+    const int64_t item = (int64_t)q * n_out + panel_nnz[q];
+    tab.first[q] = std::min<int64_t>(item / ((int64_t)kMergeTile * kMergeWaves), n_blocks);
+  }
+  tab.first[n_panels] = n_blocks;
+  int64_t per_xcd = 1;
+  if (n_panels < kXcds && kXcds % n_panels == 0) {
+    const int G = kXcds / n_panels;
+    for (int q = 0; q < n_panels; ++q) per_xcd = std::max(per_xcd, ceil_div(tab.first[q + 1] - tab.first[q], G));
+  } else {
+    for (int xcd = 0; xcd < kXcds; ++xcd) {
+      int64_t sum = 0;
+      for (int q = xcd; q < n_panels; q += kXcds) sum += tab.first[q + 1] - tab.first[q];
+      per_xcd = std::max(per_xcd, sum);
+    }
+  }
+  if (per_xcd * kXcds > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr_panels: grid too large");
+  hipLaunchKernelGGL((spmv_panel_merge_kernel<V, I, P>), dim3((unsigned)(per_xcd * kXcds)), dim3(256), 0, stream,
+                     static_cast<const V*>(vals), static_cast<const I*>(cols), p, static_cast<const V*>(x), partial,
+                     static_cast<const int64_t*>(part), head, tail, tab, n_panels, plan->n_rows, plan->nnz, n_tiles);
+  FS_CHECK_LAUNCH("spmv_panel_merge_kernel");
+  hipLaunchKernelGGL((merge_fixup_kernel<V, P, A>), dim3((unsigned)ceil_div(n_tiles, 256)), dim3(256), 0, stream, p,
+                     static_cast<const int64_t*>(part), head, tail, partial, n_tiles, (int64_t)kMergeTile);
+  FS_CHECK_LAUNCH("merge_fixup_kernel");
+  hipLaunchKernelGGL((panel_reduce_kernel<V>), dim3((unsigned)ceil_div(n_out, 256)), dim3(256), 0, stream, partial,
+                     static_cast<V*>(y), n_out, n_panels);
+  FS_CHECK_LAUNCH("panel_reduce_kernel");
   return FS_OK;
 }
 
@@ -819,5 +963,48 @@ extern "C" int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void
     case FS_F64: return dispatch_idx<double>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
     case FS_C64: return dispatch_idx<c32>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
     default: return dispatch_idx<c64>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
+  }
+}
+
+extern "C" size_t fs_spmv_panels_workspace_bytes(const fs_csr_plan* plan, int n_panels) {
+  if (!plan || n_panels <= 0) return 0;
+  return panel_ws(plan, n_panels, acc_bytes(plan->val_t)).total;
+}
+
+extern "C" int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels, const int64_t* panel_nnz,
+                                  const void* vals, const void* cols, const void* indptr, const void* x, void* y,
+                                  const void* part_dev, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!plan) return fail(FS_E_INVALID, "fs_spmv_csr_panels: plan is null");
+  if (!valid_types(plan->val_t, plan->idx_t, plan->ptr_t))
+    return fail(FS_E_INVALID, "fs_spmv_csr_panels: bad type code");
+  if (n_panels <= 0 || n_panels > kMaxPanels || plan->n_rows % n_panels != 0)
+    return fail(FS_E_INVALID, "fs_spmv_csr_panels: n_rows of the stacked matrix must be a multiple of n_panels (<= 64)");
+  if (plan->tile_items != kMergeTile || plan->n_tiles != ceil_div(plan->n_rows + plan->nnz, kMergeTile))
+    return fail(FS_E_INVALID, "fs_spmv_csr_panels: plan does not describe merge tiles");
+  if (!panel_nnz) return fail(FS_E_INVALID, "fs_spmv_csr_panels: panel_nnz is null");
+  if (panel_nnz[0] != 0 || panel_nnz[n_panels] != plan->nnz)
+    return fail(FS_E_INVALID, "fs_spmv_csr_panels: panel_nnz must run from 0 to nnz");
+  for (int q = 0; q < n_panels; ++q)
+    if (panel_nnz[q + 1] < panel_nnz[q]) return fail(FS_E_INVALID, "fs_spmv_csr_panels: panel_nnz must not decrease");
+  const int64_t n_out = plan->n_rows / n_panels;
+  if (n_out == 0) return FS_OK;
+  if (!indptr || !y || !part_dev || (plan->nnz > 0 && (!vals || !cols || !x)))
+    return fail(FS_E_INVALID, "fs_spmv_csr_panels: null pointer");
+  auto by_idx = [&](auto vtag) -> int {
+    using V = decltype(vtag);
+    if (plan->idx_t == FS_I32) {
+      if (plan->ptr_t == FS_I32)
+        return launch_spmv_panels<V, int32_t, int32_t>(plan, n_panels, panel_nnz, vals, cols, indptr, x, y, part_dev, ws, ws_bytes, n_out, stream);
+      return launch_spmv_panels<V, int32_t, int64_t>(plan, n_panels, panel_nnz, vals, cols, indptr, x, y, part_dev, ws, ws_bytes, n_out, stream);
+    }
+    if (plan->ptr_t == FS_I32)
+      return launch_spmv_panels<V, int64_t, int32_t>(plan, n_panels, panel_nnz, vals, cols, indptr, x, y, part_dev, ws, ws_bytes, n_out, stream);
+    return launch_spmv_panels<V, int64_t, int64_t>(plan, n_panels, panel_nnz, vals, cols, indptr, x, y, part_dev, ws, ws_bytes, n_out, stream);
+  };
+  switch (plan->val_t) {
+    case FS_F32: return by_idx(float{});
+    case FS_F64: return by_idx(double{});
+    case FS_C64: return by_idx(c32{});
+    default: return by_idx(c64{});
   }
 }

@@ -18,6 +18,7 @@
 // sorted keys (colptr[c] = first position whose key >= c).
 #include "fs_common.hpp"
 
+#include <algorithm>
 #include <cstring>
 
 namespace fs {
@@ -262,6 +263,7 @@ struct Layout {
   size_t key_bytes, pos_bytes, rowid_bytes;
   int64_t n_sub, n_counts, n_partials;
   size_t off_keys_a, off_keys_b, off_pos_a, off_pos_b, off_rowid, off_counts, off_partials, total;
+  size_t off_counts_extra = 0, off_key2 = 0;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -500,6 +502,112 @@ int coo_to_csr_idx(const Layout& L, char* ws, int idx_t, int64_t n, int64_t n_ro
   return coo_to_csr_keys<V, int64_t>(L, ws, n, n_rows, n_cols, vals, rows, cols, assume_sorted, ov, oc, op, s);
 }
 
+// ---- column panels (stacked CSR: panel-major rows) ----
+// Panel of an entry = col / panel_width.  A stable partition by panel keeps
+// CSR order inside every panel, so the stacked matrix with rows
+// (panel * n_rows + row) is again a CSR, read off the sorted composite keys.
+template <class I, class K>
+__global__ __launch_bounds__(256) void panel_keys_kernel(const I* __restrict__ cols, int64_t n, int64_t width,
+                                                         K* __restrict__ keys) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < n) keys[k] = (K)((int64_t)cols[k] / width);
+}
+
+template <class V, class I, class OP, class Pos>
+__global__ __launch_bounds__(256) void panel_gather_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
+                                                           const int64_t* __restrict__ rowid,
+                                                           const Pos* __restrict__ perm, int64_t n, int64_t n_rows,
+                                                           int64_t width, V* __restrict__ p_vals,
+                                                           I* __restrict__ p_cols, int64_t* __restrict__ key2) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n) return;
+  const int64_t p = perm ? (int64_t)perm[k] : k;
+  const I c = cols[p];
+  p_vals[k] = vals[p];
+  p_cols[k] = c;
+  key2[k] = ((int64_t)c / width) * n_rows + rowid[p];
+}
+
+template <class OP>
+__global__ __launch_bounds__(256) void panel_indptr_kernel(const int64_t* __restrict__ key2, int64_t n, int64_t n_out,
+                                                           OP* __restrict__ indptr) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k > n) return;
+  const int64_t prev = k > 0 ? key2[k - 1] : -1;
+  const int64_t cur = k < n ? key2[k] : n_out;
+  for (int64_t r = prev + 1; r <= cur; ++r) indptr[r] = (OP)k;
+}
+
+template <class OP>
+__global__ void panel_starts_kernel(const OP* __restrict__ indptr, int64_t n_rows, int n_panels,
+                                    int64_t* __restrict__ out) {
+  const int q = threadIdx.x;
+  if (q <= n_panels) out[q] = (int64_t)indptr[(int64_t)q * n_rows];
+}
+
+template <class V, class I, class P, class K, class Pos>
+int panelize_typed(const Layout& L, char* ws, int64_t n_rows, int64_t n_cols, int64_t nnz, int n_panels,
+                   const void* vals, const void* cols, const void* indptr, void* p_vals, void* p_cols,
+                   void* p_indptr, hipStream_t s) {
+  const int64_t width = ceil_div(n_cols, n_panels);
+  K* keys0 = reinterpret_cast<K*>(ws + L.off_counts_extra);
+  int64_t* rowid = reinterpret_cast<int64_t*>(ws + L.off_rowid);
+  int64_t* key2 = reinterpret_cast<int64_t*>(ws + L.off_key2);
+  const unsigned blocks = (unsigned)ceil_div(nnz, 256);
+  hipLaunchKernelGGL((panel_keys_kernel<I, K>), dim3(blocks), dim3(256), 0, s, static_cast<const I*>(cols), nnz,
+                     width, keys0);
+  FS_CHECK_LAUNCH("panel_keys_kernel");
+  const K* sorted = nullptr;
+  const Pos* perm = nullptr;
+  int rc = radix_sort_cols<K, Pos>(L, ws, keys0, 2, nnz, n_panels, &sorted, &perm, s);
+  if (rc != FS_OK) return rc;
+  hipLaunchKernelGGL((expand_rows_kernel<P, int64_t>), dim3((unsigned)ceil_div(ceil_div(nnz, kExpandItems), 256)),
+                     dim3(256), 0, s, static_cast<const P*>(indptr), n_rows, nnz, rowid);
+  FS_CHECK_LAUNCH("expand_rows_kernel");
+  hipLaunchKernelGGL((panel_gather_kernel<V, I, P, Pos>), dim3(blocks), dim3(256), 0, s, static_cast<const V*>(vals),
+                     static_cast<const I*>(cols), rowid, perm, nnz, n_rows, width, static_cast<V*>(p_vals),
+                     static_cast<I*>(p_cols), key2);
+  FS_CHECK_LAUNCH("panel_gather_kernel");
+  const int64_t n_out = (int64_t)n_panels * n_rows;
+  hipLaunchKernelGGL((panel_indptr_kernel<P>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, key2, nnz,
+                     n_out, static_cast<P*>(p_indptr));
+  FS_CHECK_LAUNCH("panel_indptr_kernel");
+  return FS_OK;
+}
+
+// Entry offsets of the panels in the stacked CSR, copied to the host.
+template <class P>
+int read_panel_starts(const void* p_indptr, int64_t n_rows, int n_panels, int64_t* dev_tmp, int64_t* host,
+                      hipStream_t s) {
+  hipLaunchKernelGGL((panel_starts_kernel<P>), dim3(1), dim3(128), 0, s, static_cast<const P*>(p_indptr), n_rows,
+                     n_panels, dev_tmp);
+  FS_CHECK_LAUNCH("panel_starts_kernel");
+  FS_CHECK_HIP(hipMemcpyAsync(host, dev_tmp, sizeof(int64_t) * (n_panels + 1), hipMemcpyDeviceToHost, s));
+  FS_CHECK_HIP(hipStreamSynchronize(s));
+  return FS_OK;
+}
+
+template <class V, class I, class P>
+int panelize_pos(const Layout& L, char* ws, int64_t n_rows, int64_t n_cols, int64_t nnz, int n_panels,
+                 const void* vals, const void* cols, const void* indptr, void* pv, void* pc, void* pp, hipStream_t s) {
+  if (L.pos_bytes == 4)
+    return panelize_typed<V, I, P, uint32_t, uint32_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+  return panelize_typed<V, I, P, uint32_t, uint64_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+}
+
+template <class V>
+int panelize_idx(const Layout& L, char* ws, int idx_t, int ptr_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                 int n_panels, const void* vals, const void* cols, const void* indptr, void* pv, void* pc, void* pp,
+                 hipStream_t s) {
+  if (idx_t == FS_I32 && ptr_t == FS_I32)
+    return panelize_pos<V, int32_t, int32_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+  if (idx_t == FS_I32)
+    return panelize_pos<V, int32_t, int64_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+  if (ptr_t == FS_I32)
+    return panelize_pos<V, int64_t, int32_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+  return panelize_pos<V, int64_t, int64_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+}
+
 }  // namespace fs
 
 using namespace fs;
@@ -576,4 +684,63 @@ extern "C" int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_col
     case FS_C64: return coo_to_csr_idx<c32>(L, w, idx_t, nnz, n_rows, n_cols, vals, rows, cols, assume_sorted, out_vals, out_cols, out_indptr, stream);
     default: return coo_to_csr_idx<c64>(L, w, idx_t, nnz, n_rows, n_cols, vals, rows, cols, assume_sorted, out_vals, out_cols, out_indptr, stream);
   }
+}
+
+// Panel layout: the radix buffers sized for keys in [0, n_panels) plus the
+// unsorted keys, row ids and composite (panel, row) keys.
+static Layout panel_layout(int64_t n_rows, int64_t n_panels, int64_t nnz) {
+  Layout L = make_layout(n_rows, n_panels, nnz);
+  size_t o = L.total;
+  L.off_counts_extra = o;
+  o = align256(o + 4 * (size_t)nnz);
+  L.off_key2 = o;  // also stages the n_panels + 1 panel starts afterwards
+  o = align256(o + 8 * (size_t)std::max<int64_t>(nnz, n_panels + 1));
+  L.total = o;
+  return L;
+}
+
+extern "C" size_t fs_csr_panelize_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t nnz, int n_panels) {
+  (void)n_cols;
+  if (n_panels <= 0) return 0;
+  if (nnz <= 0) return 256;  // the panel-start staging slot
+  return panel_layout(n_rows, n_panels, nnz).total;
+}
+
+extern "C" int fs_csr_panelize(int val_t, int idx_t, int ptr_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                               int n_panels, const void* vals, const void* cols, const void* indptr, void* p_vals,
+                               void* p_cols, void* p_indptr, int64_t* panel_nnz, void* ws, size_t ws_bytes,
+                               hipStream_t stream) {
+  if (!valid_types(val_t, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_csr_panelize: bad type code");
+  if (n_rows < 0 || n_cols <= 0 || nnz < 0 || n_panels <= 0 || n_panels > 64)
+    return fail(FS_E_INVALID, "fs_csr_panelize: bad size");
+  if (!p_indptr || !panel_nnz) return fail(FS_E_INVALID, "fs_csr_panelize: p_indptr / panel_nnz is null");
+  const int64_t n_out = (int64_t)n_panels * n_rows;
+  if (!ws || ws_bytes < fs_csr_panelize_workspace_bytes(n_rows, n_cols, nnz, n_panels))
+    return fail(FS_E_WORKSPACE, "fs_csr_panelize: workspace too small");
+  if (nnz == 0) {
+    if (ptr_t == FS_I32)
+      hipLaunchKernelGGL((fill_kernel<int32_t>), dim3((unsigned)ceil_div(n_out + 1, 256)), dim3(256), 0, stream,
+                         static_cast<int32_t*>(p_indptr), n_out + 1, 0);
+    else
+      hipLaunchKernelGGL((fill_kernel<int64_t>), dim3((unsigned)ceil_div(n_out + 1, 256)), dim3(256), 0, stream,
+                         static_cast<int64_t*>(p_indptr), n_out + 1, (int64_t)0);
+    FS_CHECK_LAUNCH("fill_kernel");
+    for (int q = 0; q <= n_panels; ++q) panel_nnz[q] = 0;
+    return FS_OK;
+  }
+  if (!vals || !cols || !indptr || !p_vals || !p_cols) return fail(FS_E_INVALID, "fs_csr_panelize: null pointer");
+  const Layout L = panel_layout(n_rows, n_panels, nnz);
+  char* w = static_cast<char*>(ws);
+  int rc = FS_OK;
+  switch (val_t) {
+    case FS_F32: rc = panelize_idx<float>(L, w, idx_t, ptr_t, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, p_vals, p_cols, p_indptr, stream); break;
+    case FS_F64: rc = panelize_idx<double>(L, w, idx_t, ptr_t, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, p_vals, p_cols, p_indptr, stream); break;
+    case FS_C64: rc = panelize_idx<c32>(L, w, idx_t, ptr_t, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, p_vals, p_cols, p_indptr, stream); break;
+    default: rc = panelize_idx<c64>(L, w, idx_t, ptr_t, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, p_vals, p_cols, p_indptr, stream); break;
+  }
+  if (rc != FS_OK) return rc;
+  // the composite-key slot is free once the indptr is built (stream order)
+  int64_t* tmp = reinterpret_cast<int64_t*>(w + L.off_key2);
+  if (ptr_t == FS_I32) return read_panel_starts<int32_t>(p_indptr, n_rows, n_panels, tmp, panel_nnz, stream);
+  return read_panel_starts<int64_t>(p_indptr, n_rows, n_panels, tmp, panel_nnz, stream);
 }

@@ -14,6 +14,8 @@ unchanged.  The device work (transpose, analysis, SpMV) is one call each
 into libflagsparse_hip; there is no CPU path.
 """
 
+import ctypes
+import os
 import time
 
 import torch
@@ -104,6 +106,7 @@ class PreparedCsrSpmv:
         "_plan",
         "_part",
         "_carry",
+        "_panels",
     )
 
     def __init__(
@@ -152,6 +155,7 @@ class PreparedCsrSpmv:
         self._plan = None
         self._part = None
         self._carry = None
+        self._panels = None
 
     # -- HIP plan (built lazily on first run, then cached) ------------------
     def hip_plan(self):
@@ -162,8 +166,14 @@ class PreparedCsrSpmv:
             )
             p = self._plan.plan
             if p.kernel == _lib.FS_KERNEL_MERGE:
-                self._part = self._plan.partition(self.kernel_indptr, int(p.tile_items))
-                self._carry = _lib.workspace(p.carry_bytes, data.device)
+                n_panels = _spmv_panel_count(p, data.dtype)
+                if n_panels > 1:
+                    self._panels = PanelledCsr(
+                        data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols, n_panels
+                    )
+                else:
+                    self._part = self._plan.partition(self.kernel_indptr, int(p.tile_items))
+                    self._carry = _lib.workspace(p.carry_bytes, data.device)
         return self._plan
 
     def compute_data(self):
@@ -177,7 +187,79 @@ class PreparedCsrSpmv:
 
     @property
     def kernel_name(self):
-        return self.hip_plan().kernel_name
+        plan = self.hip_plan()
+        return "panel" if self._panels is not None else plan.kernel_name
+
+
+# Column panels pay off once x is larger than an XCD's 4 MiB L2: the random
+# gather rate measured on MI355X drops from ~150-190 to ~70 gathers/ns when
+# x (16.8 MB) no longer fits.  A panel slice of up to ~4.5 MiB measured best
+# (4 panels on a 16.8 MB x: 0.61 ms against 0.67 ms with 8 and 1.01 ms with
+# none) since every panel adds n_rows row ends and partials.
+_PANEL_X_BYTES = 6 << 20
+_PANEL_SLICE_BYTES = 9 << 19
+
+
+def _spmv_panel_count(plan, dtype):
+    """Column panels for a merge-path matrix (0 = none).  FLAGSPARSE_SPMV_PANELS=N
+    forces N (0/1 off); otherwise the fewest of 2, 4, 8 whose x slice is at most
+    ~4.5 MiB, for x above 6 MiB and rows averaging at least 2 entries per panel."""
+    env = os.environ.get("FLAGSPARSE_SPMV_PANELS")
+    if env is not None:
+        return max(0, int(env))
+    n_rows, n_cols, nnz = int(plan.n_rows), int(plan.n_cols), int(plan.nnz)
+    x_bytes = n_cols * torch.empty(0, dtype=dtype).element_size()
+    if n_rows == 0 or x_bytes <= _PANEL_X_BYTES:
+        return 0
+    n_panels = 2
+    while n_panels < 8 and x_bytes > _PANEL_SLICE_BYTES * n_panels:
+        n_panels *= 2
+    return n_panels if nnz >= 2 * n_panels * n_rows else 0
+
+
+class PanelledCsr:
+    """A in n_panels column panels, stacked into one CSR with n_panels*n_rows
+    rows, plus its merge plan, partition and SpMV workspace (built once)."""
+
+    __slots__ = ("n_panels", "panel_nnz", "data", "indices", "indptr", "plan", "part", "ws")
+
+    def __init__(self, data, indices, indptr, n_rows, n_cols, n_panels):
+        device = data.device
+        nnz = data.numel()
+        lib = _lib.lib()
+        self.n_panels = int(n_panels)
+        self.data = torch.empty_like(data)
+        self.indices = torch.empty_like(indices)
+        self.indptr = torch.empty(self.n_panels * n_rows + 1, dtype=indptr.dtype, device=device)
+        ws = _lib.workspace(lib.fs_csr_panelize_workspace_bytes(n_rows, n_cols, nnz, self.n_panels), device)
+        self.panel_nnz = (ctypes.c_int64 * (self.n_panels + 1))()
+        _lib.check(
+            lib.fs_csr_panelize(
+                _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype),
+                n_rows, n_cols, nnz, self.n_panels, _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr),
+                _lib.ptr(self.data), _lib.ptr(self.indices), _lib.ptr(self.indptr), self.panel_nnz,
+                _lib.ptr(ws), ws.numel(), _lib.stream_handle(device),
+            ),
+            "fs_csr_panelize",
+        )
+        del ws
+        self.plan = analyze_csr(
+            self.data, self.indices, self.indptr, self.n_panels * n_rows, n_cols, force_kernel=_lib.FS_KERNEL_MERGE
+        )
+        self.part = self.plan.partition(self.indptr, int(self.plan.plan.tile_items))
+        self.ws = _lib.workspace(lib.fs_spmv_panels_workspace_bytes(self.plan.plan, self.n_panels), device)
+
+    def spmv(self, x, y):
+        device = self.data.device
+        _lib.check(
+            _lib.lib().fs_spmv_csr_panels(
+                self.plan.plan, self.n_panels, self.panel_nnz, _lib.ptr(self.data), _lib.ptr(self.indices),
+                _lib.ptr(self.indptr),
+                _lib.ptr(x), _lib.ptr(y), _lib.ptr(self.part), _lib.ptr(self.ws), self.ws.numel(),
+                _lib.stream_handle(device),
+            ),
+            "fs_spmv_csr_panels",
+        )
 
 
 def _normalize_spmv_index_fallback_policy(index_fallback_policy):
@@ -366,6 +448,11 @@ def _hip_spmv_csr_impl_prepared(prepared, x):
     x_in = x if x.dtype == cdt else x.to(cdt)
     y_out = y if cdt == dtype else torch.empty(prepared.n_rows, dtype=cdt, device=device)
     plan = prepared.hip_plan()
+    if prepared._panels is not None:
+        prepared._panels.spmv(x_in, y_out)
+        if y_out is not y:
+            y.copy_(y_out)
+        return y
     carry = prepared._carry
     _lib.check(
         _lib.lib().fs_spmv_csr(

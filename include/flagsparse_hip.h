@@ -167,6 +167,45 @@ int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_cols,
                   void* out_cols, void* out_indptr, void* ws, size_t ws_bytes,
                   hipStream_t stream);
 
+/*
+ * Column panels for SpMV on matrices whose x does not fit one XCD's L2.
+ * No counterpart call in the reference: it is part of what prepare_spmv_csr
+ * (spmv_csr.py:591-676) may precompute once per matrix, and
+ * fs_spmv_csr_panels then replaces _triton_spmv_csr_impl_prepared
+ * (spmv_csr.py:679-723) for such a prepared matrix, with the same result
+ * up to the order of the floating-point additions.
+ *
+ * fs_csr_panelize splits A (n_rows x n_cols) into n_panels (<= 64) column
+ * panels of width ceil(n_cols / n_panels) and writes them as one stacked CSR
+ * with n_panels * n_rows rows: row p * n_rows + r holds the entries of row r
+ * whose column lies in panel p, in their CSR order; column indices are
+ * unchanged.  p_vals / p_cols hold nnz entries, p_indptr n_panels * n_rows + 1.
+ * panel_nnz (host, n_panels + 1) receives the entry offset of each panel; the
+ * call synchronises `stream` to return it.
+ *
+ * fs_spmv_csr_panels computes y = A x from the stacked matrix: `plan` is
+ * fs_csr_analyze of the stacked CSR (merge tiles), part_dev its partition
+ * (fs_csr_partition with plan->tile_items), panel_nnz the host offsets from
+ * fs_csr_panelize.  Each panel's tiles go to one XCD (workgroup b runs on
+ * XCD b % 8); per-row panel partials stay in the accumulator type and are
+ * summed in panel order (deterministic; float32 is still rounded once from
+ * float64).  Does not synchronise.
+ */
+size_t fs_csr_panelize_workspace_bytes(int64_t n_rows, int64_t n_cols,
+                                       int64_t nnz, int n_panels);
+int fs_csr_panelize(int val_t, int idx_t, int ptr_t, int64_t n_rows,
+                    int64_t n_cols, int64_t nnz, int n_panels,
+                    const void* vals, const void* cols, const void* indptr,
+                    void* p_vals, void* p_cols, void* p_indptr,
+                    int64_t* panel_nnz, void* ws, size_t ws_bytes,
+                    hipStream_t stream);
+size_t fs_spmv_panels_workspace_bytes(const fs_csr_plan* plan, int n_panels);
+int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
+                       const int64_t* panel_nnz, const void* vals,
+                       const void* cols, const void* indptr, const void* x,
+                       void* y, const void* part_dev, void* ws,
+                       size_t ws_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,9 +31,14 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge", "stream"])
+@pytest.fixture(params=["auto", "vector", "merge", "stream", "panel2", "panel3", "panel8", "panel16"])
 def kernel_choice(request, monkeypatch):
-    if request.param != "auto":
+    """Kernel variant under test; panelN = merge path over N column panels."""
+    monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
+    if request.param.startswith("panel"):
+        monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
+        monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", request.param[len("panel"):])
+    elif request.param != "auto":
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", request.param)
     else:
         monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
@@ -42,6 +47,9 @@ def kernel_choice(request, monkeypatch):
 
 def _check_spmv(data, indices, indptr, shape, x, op, kernel=None):
     y = fs.flagsparse_spmv_csr(data, indices, indptr, x, shape, op=op)
+    if kernel is not None and kernel.startswith("panel") and shape[0] > 0:
+        prep = fs.prepare_spmv_csr(data, indices, indptr, shape, op=op)
+        assert prep.kernel_name == "panel"
     ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), shape, op=op)
     assert y.dtype == data.dtype
     assert tuple(y.shape) == (ref.shape[0],)
@@ -241,3 +249,53 @@ def test_spmv_full_size_configs(device, config):
     gen = np.random.default_rng(0)
     rows = sorted(set(gen.integers(0, sh[0], 4000).tolist()) | {0, sh[0] - 1, longest})
     _sampled_rows_check(data, indices, indptr, sh, x1, y1, rows, REL_TOL[data.dtype])
+
+
+def test_spmv_panels_match_unpanelled(device, monkeypatch):
+    """Power-law matrix at the BASELINE size: the column-panel path (chosen by
+    default there) agrees with the single-pass merge path and the oracle on
+    sampled rows, and is deterministic."""
+    monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
+    data, indices, indptr, sh = S.powerlaw(4194304, torch.float32, torch.int32, device, seed=3)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep.kernel_name == "panel"
+    x = S.vector(sh[1], data.dtype, device, seed=23)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=prep))
+    monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", "0")
+    prep0 = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep0.kernel_name == "merge"
+    y0 = fs.flagsparse_spmv_csr(x=x, prepared=prep0)
+    # both are f64 sums rounded once to f32: at most one ulp apart
+    diff = (y.double() - y0.double()).abs()
+    assert bool((diff <= y0.double().abs() * 2.0**-23 + 1e-30).all())
+    gen = np.random.default_rng(1)
+    rows = sorted(set(gen.integers(0, sh[0], 3000).tolist()) | {0, sh[0] - 1})
+    _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[data.dtype])
+
+
+@pytest.mark.parametrize("n_panels", [1, 2, 4, 8, 13, 64])
+def test_csr_panelize_layout(device, n_panels):
+    """fs_csr_panelize writes, for row r and panel p, exactly the entries of r
+    whose column lies in panel p, in CSR order (checked against numpy)."""
+    from flagsparse_amd.spmv_csr import PanelledCsr
+
+    m, n = 1500, 7001
+    data, indices, indptr, sh = S.random_csr(m, n, 0.01, torch.float64, torch.int32, device, seed=4,
+                                             empty_row_every=5, long_rows=((3, 6000),))
+    pc = PanelledCsr(data, indices, indptr, m, n, n_panels)
+    width = -(-n // n_panels)
+    d, c, p = np_(data), np_(indices).astype(np.int64), np_(indptr).astype(np.int64)
+    exp_d, exp_c, exp_p = [], [], [0]
+    for panel in range(n_panels):
+        for r in range(m):
+            seg = slice(p[r], p[r + 1])
+            keep = (c[seg] // width) == panel
+            exp_d.append(d[seg][keep])
+            exp_c.append(c[seg][keep])
+            exp_p.append(exp_p[-1] + int(keep.sum()))
+    assert np.array_equal(np_(pc.indptr).astype(np.int64), np.array(exp_p))
+    assert np.array_equal(np_(pc.indices).astype(np.int64), np.concatenate(exp_c))
+    assert np.array_equal(np_(pc.data), np.concatenate(exp_d))
+    assert pc.indptr.dtype == indptr.dtype and pc.indices.dtype == indices.dtype
