@@ -196,7 +196,7 @@ def run(args):
         bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
         flops = S.flops_spmv(nnz, complex_values)
         kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
-                       "panel": "spmv_panel_merge_kernel"}[prep.kernel_name]
+                       "panel": "spmv_panel_merge_kernel", "nnzblock": "spmv_nnzblock_kernel"}[prep.kernel_name]
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:

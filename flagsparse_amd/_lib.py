@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libflagsparse_hip.so")
 
 FS_F32, FS_F64, FS_C64, FS_C128 = 0, 1, 2, 3
 FS_I32, FS_I64 = 0, 1
-FS_KERNEL_VECTOR, FS_KERNEL_MERGE, FS_KERNEL_STREAM = 0, 1, 2
+FS_KERNEL_VECTOR, FS_KERNEL_MERGE, FS_KERNEL_STREAM, FS_KERNEL_NNZBLOCK = 0, 1, 2, 3
 FS_HIST_BINS = 24
 
 VALUE_TYPE_CODES = {
@@ -28,7 +28,12 @@ VALUE_TYPE_CODES = {
     torch.complex128: FS_C128,
 }
 INDEX_TYPE_CODES = {torch.int32: FS_I32, torch.int64: FS_I64}
-KERNEL_NAMES = {FS_KERNEL_VECTOR: "vector", FS_KERNEL_MERGE: "merge", FS_KERNEL_STREAM: "stream"}
+KERNEL_NAMES = {
+    FS_KERNEL_VECTOR: "vector",
+    FS_KERNEL_MERGE: "merge",
+    FS_KERNEL_STREAM: "stream",
+    FS_KERNEL_NNZBLOCK: "nnzblock",
+}
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTED_SYMBOLS = (
@@ -37,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "fs_csr_stats_bytes",
     "fs_csr_analyze",
     "fs_csr_partition",
+    "fs_spmv_partition",
     "fs_spmv_csr",
     "fs_spmm_workspace_bytes",
     "fs_spmm_tile_items",
@@ -100,6 +106,8 @@ def _declare(lib):
                                    ctypes.POINTER(FsCsrPlan), _vp]
     lib.fs_csr_partition.restype = _i32
     lib.fs_csr_partition.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _i32, _i64, _vp]
+    lib.fs_spmv_partition.restype = _i32
+    lib.fs_spmv_partition.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp]
     lib.fs_spmv_csr.restype = _i32
     lib.fs_spmv_csr.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]
     lib.fs_spmm_workspace_bytes.restype = _sz

@@ -150,6 +150,14 @@ __device__ inline double readlane_f64(double v, int lane) {
   return __hiloint2double(hi, lo);
 }
 
+// Sum over the whole wave, returned uniformly (lanes 0 and 32 hold the two
+// half totals after the 32-lane butterfly).
+__device__ inline double wave_total(double v) {
+  v = group_sum<32>(v);
+  return readlane_f64(v, 0) + readlane_f64(v, 32);
+}
+__device__ inline c64 wave_total(c64 v) { return c64{wave_total(v.re), wave_total(v.im)}; }
+
 // Generic shuffle (ds_bpermute) of 64-bit values, used for scans.
 __device__ inline double shfl_f64(double v, int src_lane) {
   int lo = __builtin_amdgcn_ds_bpermute(src_lane << 2, __double2loint(v));

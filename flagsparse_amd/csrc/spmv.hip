@@ -163,26 +163,15 @@ constexpr int stream_items() {
   return 16384 / (int)sizeof(A);
 }
 
-// One workgroup per row block (variants: KMUL scales the LDS stage, NT
-// streams values / indices with non-temporal loads so they do not displace
-// x from the caches).
-template <bool NT, class Tp>
-__device__ inline Tp ld_nt(const Tp* p) {
-  if constexpr (NT) {
-    return __builtin_nontemporal_load(p);
-  } else {
-    return *p;
-  }
-}
-
-template <int TPR, int KMUL, bool NT, class V, class I, class P>
+// One workgroup per row block.
+template <int TPR, class V, class I, class P>
 __global__ __launch_bounds__(256) void spmv_stream_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
     const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_blocks, int remap) {
   using T = VT<V>;
   using A = typename T::acc;
-  constexpr int R = 256 / TPR * KMUL;
-  constexpr int kItems = stream_items<A>() * KMUL;
+  constexpr int R = 256 / TPR;
+  constexpr int kItems = stream_items<A>();
   constexpr int K = kItems / 256;
   __shared__ A s_prod[kItems];
   __shared__ int64_t s_ptr[R + 1];
@@ -201,12 +190,8 @@ __global__ __launch_bounds__(256) void spmv_stream_kernel(
     const int q = t + 256 * k;
     c[k] = 0;
     if (q < cnt) {
-      if constexpr (VT<V>::complex) {
-        v[k] = vals[S + q];
-      } else {
-        v[k] = ld_nt<NT>(vals + S + q);
-      }
-      c[k] = ld_nt<NT>(cols + S + q);
+      v[k] = vals[S + q];
+      c[k] = cols[S + q];
     }
   }
   V xv[K];
@@ -217,116 +202,160 @@ __global__ __launch_bounds__(256) void spmv_stream_kernel(
   for (int k = 0; k < K; ++k)
     if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(v[k], xv[k]);
   __syncthreads();
+  const int r = t / TPR;
+  const int sub = t % TPR;
+  A acc = T::zero();
+  if (r < rows) {
+    const int a = (int)(s_ptr[r] - S);
+    const int b = (int)(s_ptr[r + 1] - S);
+    for (int q = a + sub; q < b; q += TPR) acc = add(acc, s_prod[q]);
+  }
+  if constexpr (TPR > 1) acc = group_sum<TPR>(acc);
+  if (sub == 0 && r < rows) y[rb0 + r] = T::out(acc);
+}
+
+// ---------------------------------------------------------------------------
+// K3b: entry-aligned streaming SpMV.  Block b owns the entry range
+// [b*C, (b+1)*C) (C = the LDS stage), so its value / index loads depend on
+// nothing and go out at once; the rows it owns (those whose last entry, or
+// position when empty, falls in the range) come from a precomputed table
+// part[b] and their row pointers load in parallel with the data.  Owned
+// rows are summed from the LDS stage by TPR threads each, in passes of
+// 256/TPR rows.  A row that begins in an earlier block stores its in-block
+// part to head[b]; the entries after the last owned row go to tail[b]
+// (they belong to row part[b+1]); nnz_fixup_kernel adds these in block
+// order, so the result is deterministic.
+// ---------------------------------------------------------------------------
+template <int TPR, class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_nnzblock_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, const int64_t* __restrict__ part,
+    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  constexpr int C = stream_items<A>();
+  constexpr int K = C / 256;
+  constexpr int RP = 256 / TPR;  // rows per pass
+  __shared__ A s_prod[C];
+  __shared__ int64_t s_ptr[RP + 1];
+  __shared__ A s_red[4];
+  const int t = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int64_t e0 = blk * C;
+  const int cnt = nnz - e0 < C ? (int)(nnz - e0) : C;
+  V v[K];
+  I c[K];
 #pragma unroll
-  for (int rr = 0; rr < KMUL; ++rr) {
-    const int r = t / TPR + rr * (256 / TPR);
-    const int sub = t % TPR;
+  for (int k = 0; k < K; ++k) {
+    const int q = t + 256 * k;
+    c[k] = 0;
+    if (q < cnt) {
+      v[k] = vals[e0 + q];
+      c[k] = cols[e0 + q];
+    }
+  }
+  const int64_t ra = part[blk];
+  const int64_t rb = part[blk + 1];
+  // first pass's row pointers go out with the data
+  // rows + 1 pointers per pass: thread t < rows loads row t's start,
+  // thread 0 also the pass's end pointer (rows can equal 256)
+  int rows = rb - ra < RP ? (int)(rb - ra) : RP;
+  int64_t my_ptr = t < rows ? (int64_t)rowptr[ra + t] : 0;
+  int64_t end_ptr = t == 0 ? (int64_t)rowptr[ra + rows] : 0;
+  V xv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (t + 256 * k < cnt) xv[k] = x[c[k]];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(v[k], xv[k]);
+  const int r = t / TPR;
+  const int sub = t % TPR;
+  for (int64_t base = ra;;) {
+    if (t < rows) s_ptr[t] = my_ptr;
+    if (t == 0) s_ptr[rows] = end_ptr;
+    __syncthreads();
     A acc = T::zero();
+    int64_t start = 0;
     if (r < rows) {
-      const int a = (int)(s_ptr[r] - S);
-      const int b = (int)(s_ptr[r + 1] - S);
+      start = s_ptr[r];
+      const int a = (int)((start > e0 ? start : e0) - e0);
+      const int b = (int)(s_ptr[r + 1] - e0);
       for (int q = a + sub; q < b; q += TPR) acc = add(acc, s_prod[q]);
     }
     if constexpr (TPR > 1) acc = group_sum<TPR>(acc);
-    if (sub == 0 && r < rows) y[rb0 + r] = T::out(acc);
+    if (sub == 0 && r < rows) {
+      if (start < e0)
+        head[blk] = acc;  // only the first owned row can begin before e0
+      else
+        y[base + r] = T::out(acc);
+    }
+    base += rows;
+    if (base >= rb) break;
+    rows = rb - base < RP ? (int)(rb - base) : RP;
+    my_ptr = t < rows ? (int64_t)rowptr[base + t] : 0;
+    end_ptr = t == 0 ? (int64_t)rowptr[base + rows] : 0;
+    __syncthreads();  // s_ptr is rewritten
+  }
+  if (rb < n_rows) {
+    // entries after the last owned row end belong to row rb
+    const int64_t rs = (int64_t)rowptr[rb];
+    const int ts = (int)((rs > e0 ? rs : e0) - e0);
+    A acc = T::zero();
+    for (int q = ts + t; q < cnt; q += 256) acc = add(acc, s_prod[q]);
+    acc = wave_total(acc);
+    if ((t & 63) == 0) s_red[t >> 6] = acc;
+    __syncthreads();
+    if (t == 0) tail[blk] = add(add(s_red[0], s_red[1]), add(s_red[2], s_red[3]));
   }
 }
 
-// Row blocks are handed out persistently: the grid holds a few workgroups
-// per CU and each walks row blocks with a stride; while the products of the
-// current block are gathered, reduced and stored, the row pointers and the
-// value / index stream of the next block are already in flight.  With
-// xcd_split, workgroup w (which the dispatcher places on XCD w % 8) walks
-// the row blocks of one contiguous eighth of the matrix, so each XCD's L2
-// caches the slice of x that its rows touch.
-template <class V, class I, int K>
-struct StreamChunk {
-  V v[K];
-  I c[K];
-};
-
-// Persistent row-block walk (variant 4): a few workgroups per CU walk row
-// blocks with a grid-sized stride; only the next block's row pointers are
-// prefetched (its data loads wait for them anyway), which removes the
-// pointer round trip from each block's critical path without holding a
-// second copy of the data in registers.
-template <int TPR, class V, class I, class P>
-__global__ __launch_bounds__(256) void spmv_stream_persistent_kernel(
-    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
-    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int xcd_split) {
+// Rows that begin in an earlier block: y[row] = tail[f] + ... + tail[b-1] +
+// head[b], where blocks f..b-1 end inside `row` and block b owns its end.
+template <class V, class P>
+__global__ __launch_bounds__(256) void nnz_fixup_kernel(const P* __restrict__ rowptr, const int64_t* __restrict__ part,
+                                                        const typename VT<V>::acc* __restrict__ head,
+                                                        const typename VT<V>::acc* __restrict__ tail,
+                                                        V* __restrict__ y, int64_t n_blocks, int64_t C) {
   using T = VT<V>;
   using A = typename T::acc;
-  constexpr int R = 256 / TPR;
-  constexpr int kItems = stream_items<A>();
-  constexpr int K = kItems / 256;
-  __shared__ A s_prod[kItems];
-  __shared__ int64_t s_ptr[R + 1];
-  const int t = threadIdx.x;
-  const int64_t n_blocks = (n_rows + R - 1) / R;
-  int64_t blk = blockIdx.x;
-  const int64_t stride = gridDim.x;
-  (void)xcd_split;
-  if (blk >= n_blocks) return;  // uniform per workgroup
-  auto rows_of = [&](int64_t b) -> int {
-    const int64_t r = n_rows - b * R;
-    return r < R ? (int)r : R;
-  };
-  int rows = rows_of(blk);
-  int64_t my_ptr = (t <= rows) ? (int64_t)rowptr[blk * R + t] : 0;
-  int64_t S = (int64_t)rowptr[blk * R];
-  int64_t E = (int64_t)rowptr[blk * R + rows];
-  while (true) {
-    const int cnt = (int)(E - S);
-    V v[K];
-    I c[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int q = t + 256 * k;
-      c[k] = 0;
-      if (q < cnt) {
-        v[k] = vals[S + q];
-        c[k] = cols[S + q];
-      }
-    }
-    // next block's pointers go out with the current data loads
-    const int64_t nblk = blk + stride;
-    const bool has_next = nblk < n_blocks;
-    int nrows = 0;
-    int64_t nS = 0, nE = 0, nptr = 0;
-    if (has_next) {
-      nrows = rows_of(nblk);
-      nS = (int64_t)rowptr[nblk * R];
-      nE = (int64_t)rowptr[nblk * R + nrows];
-      nptr = (t <= nrows) ? (int64_t)rowptr[nblk * R + t] : 0;
-    }
-    V xv[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (t + 256 * k < cnt) xv[k] = x[c[k]];
-    if (t <= rows) s_ptr[t] = my_ptr;
-    if (t == 0 && rows == 256) s_ptr[256] = E;
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (t + 256 * k < cnt) s_prod[t + 256 * k] = T::mul(v[k], xv[k]);
-    __syncthreads();
-    const int r = t / TPR;
-    const int sub = t % TPR;
-    A acc = T::zero();
-    if (r < rows) {
-      const int a = (int)(s_ptr[r] - S);
-      const int b = (int)(s_ptr[r + 1] - S);
-      for (int q = a + sub; q < b; q += TPR) acc = add(acc, s_prod[q]);
-    }
-    if constexpr (TPR > 1) acc = group_sum<TPR>(acc);
-    if (sub == 0 && r < rows) y[blk * R + r] = T::out(acc);
-    __syncthreads();
-    if (!has_next) break;
-    blk = nblk;
-    rows = nrows;
-    S = nS;
-    E = nE;
-    my_ptr = nptr;
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n_blocks) return;
+  const int64_t ra = part[b];
+  if (part[b + 1] == ra) return;                // owns no row
+  if ((int64_t)rowptr[ra] >= b * C) return;     // first row begins inside
+  int64_t f = b - 1;
+  while (f > 0 && part[f] == ra) --f;           // blocks f..b-1 have tails for row ra
+  A sum = tail[f];
+  for (int64_t k = f + 1; k < b; ++k) sum = add(sum, tail[k]);
+  y[ra] = T::out(add(sum, head[b]));
+}
+
+// part[b] = first row whose end pointer exceeds b*C (part[0] = 0,
+// part[n_blocks] = n_rows): block b owns rows [part[b], part[b+1]).
+template <class P>
+__global__ __launch_bounds__(256) void nnz_partition_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                                            int64_t C, int64_t n_blocks, int64_t* __restrict__ part) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b > n_blocks) return;
+  if (b == 0) {
+    part[0] = 0;
+    return;
   }
+  if (b == n_blocks) {
+    part[b] = n_rows;
+    return;
+  }
+  const int64_t e = b * C;
+  int64_t lo = 0, hi = n_rows;  // count of rows r with rowptr[r + 1] <= e
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)rowptr[mid + 1] <= e)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  part[b] = lo;
 }
 
 // ---------------------------------------------------------------------------
@@ -703,50 +732,44 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
     const int rpb = plan->rows_per_block;
     if (rpb < 32 || rpb > 256 || (rpb & (rpb - 1)) || (int64_t)plan->max_row * rpb > stream_items<Acc>())
       return fail(FS_E_INVALID, "fs_spmv_csr: rows_per_block does not fit the stream kernel");
-    int variant = 0;
-    if (const char* e = std::getenv("FLAGSPARSE_STREAM_VARIANT")) variant = std::atoi(e);
-    if (variant == 4) {
-      const int64_t n_blocks = ceil_div(n_rows, rpb);
-      int per_cu = 4;
-      if (const char* e = std::getenv("FLAGSPARSE_STREAM_WG_PER_CU")) per_cu = std::max(1, std::atoi(e));
-      int xcd_split = 0;
-      if (const char* e = std::getenv("FLAGSPARSE_STREAM_XCD")) xcd_split = std::atoi(e) != 0;
-      dim3 g((unsigned)std::min<int64_t>(n_blocks, (int64_t)device_cus() * per_cu));
-      switch (256 / rpb) {
-        case 1: hipLaunchKernelGGL((spmv_stream_persistent_kernel<1, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
-        case 2: hipLaunchKernelGGL((spmv_stream_persistent_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
-        case 4: hipLaunchKernelGGL((spmv_stream_persistent_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
-        default: hipLaunchKernelGGL((spmv_stream_persistent_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, xcd_split); break;
-      }
-    } else {
-      const int kmul = (variant & 2) ? 2 : 1;
-      const bool nt = variant & 1;
-      const int64_t blocks = ceil_div(n_rows, (int64_t)rpb * kmul);
-      const int remap = xcd_remap();
-      dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
-      auto go = [&](auto tpr_c, auto kmul_c, auto nt_c) {
-        hipLaunchKernelGGL((spmv_stream_kernel<decltype(tpr_c)::value, decltype(kmul_c)::value, decltype(nt_c)::value, V, I, P>),
-                           g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap);
-      };
-      auto go_k = [&](auto tpr_c) {
-        using B2 = std::integral_constant<int, 2>;
-        using B1 = std::integral_constant<int, 1>;
-        using NT1 = std::integral_constant<bool, true>;
-        using NT0 = std::integral_constant<bool, false>;
-        if (kmul == 2) {
-          if (nt) go(tpr_c, B2{}, NT1{}); else go(tpr_c, B2{}, NT0{});
-        } else {
-          if (nt) go(tpr_c, B1{}, NT1{}); else go(tpr_c, B1{}, NT0{});
-        }
-      };
-      switch (256 / rpb) {
-        case 1: go_k(std::integral_constant<int, 1>{}); break;
-        case 2: go_k(std::integral_constant<int, 2>{}); break;
-        case 4: go_k(std::integral_constant<int, 4>{}); break;
-        default: go_k(std::integral_constant<int, 8>{}); break;
-      }
+    const int64_t blocks = ceil_div(n_rows, (int64_t)rpb);
+    const int remap = xcd_remap();
+    dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
+    switch (256 / rpb) {
+      case 1: hipLaunchKernelGGL((spmv_stream_kernel<1, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 2: hipLaunchKernelGGL((spmv_stream_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      case 4: hipLaunchKernelGGL((spmv_stream_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
+      default: hipLaunchKernelGGL((spmv_stream_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
     }
     FS_CHECK_LAUNCH("spmv_stream_kernel");
+    return FS_OK;
+  }
+  if (plan->kernel == FS_KERNEL_NNZBLOCK) {
+    constexpr int C = stream_items<A>();
+    const int64_t n_blocks = plan->n_tiles;
+    if (plan->tile_items != C || n_blocks != ceil_div(plan->nnz, C) || n_blocks == 0)
+      return fail(FS_E_INVALID, "fs_spmv_csr: plan does not describe entry blocks");
+    if (part == nullptr) return fail(FS_E_INVALID, "fs_spmv_csr: entry-block kernel needs the partition");
+    if (carry == nullptr || carry_bytes < (size_t)n_blocks * 2 * sizeof(A))
+      return fail(FS_E_WORKSPACE, "fs_spmv_csr: carry workspace too small");
+    if (n_blocks > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr: grid too large");
+    A* head = static_cast<A*>(carry);
+    A* tail = head + n_blocks;
+    const int64_t* pt = static_cast<const int64_t*>(part);
+    dim3 g((unsigned)n_blocks);
+    switch (plan->vec_width) {
+      case 1: hipLaunchKernelGGL((spmv_nnzblock_kernel<1, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
+      case 2: hipLaunchKernelGGL((spmv_nnzblock_kernel<2, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
+      case 4: hipLaunchKernelGGL((spmv_nnzblock_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
+      case 8: hipLaunchKernelGGL((spmv_nnzblock_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
+      case 16: hipLaunchKernelGGL((spmv_nnzblock_kernel<16, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
+      case 32: hipLaunchKernelGGL((spmv_nnzblock_kernel<32, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
+      default: return fail(FS_E_INVALID, "fs_spmv_csr: entry-block threads per row must be a power of two in [1, 32]");
+    }
+    FS_CHECK_LAUNCH("spmv_nnzblock_kernel");
+    hipLaunchKernelGGL((nnz_fixup_kernel<V, P>), dim3((unsigned)ceil_div(n_blocks, 256)), dim3(256), 0, stream, p, pt,
+                       head, tail, yv, n_blocks, (int64_t)C);
+    FS_CHECK_LAUNCH("nnz_fixup_kernel");
     return FS_OK;
   }
   if (plan->kernel != FS_KERNEL_MERGE) return fail(FS_E_INVALID, "fs_spmv_csr: unknown kernel");
@@ -868,9 +891,12 @@ void choose_spmv_kernel(fs_csr_plan* plan, int force_kernel) {
   if (env && std::strcmp(env, "vector") == 0) kernel = FS_KERNEL_VECTOR;
   if (env && std::strcmp(env, "merge") == 0) kernel = FS_KERNEL_MERGE;
   if (env && std::strcmp(env, "stream") == 0) kernel = FS_KERNEL_STREAM;
-  if (force_kernel == FS_KERNEL_VECTOR || force_kernel == FS_KERNEL_MERGE || force_kernel == FS_KERNEL_STREAM)
+  if (env && std::strcmp(env, "nnzblock") == 0) kernel = FS_KERNEL_NNZBLOCK;
+  if (force_kernel == FS_KERNEL_VECTOR || force_kernel == FS_KERNEL_MERGE || force_kernel == FS_KERNEL_STREAM ||
+      force_kernel == FS_KERNEL_NNZBLOCK)
     kernel = force_kernel;
   if (kernel == FS_KERNEL_STREAM && !stream_fits) kernel = FS_KERNEL_MERGE;
+  if (kernel == FS_KERNEL_NNZBLOCK && plan->nnz == 0) kernel = FS_KERNEL_STREAM;  // nothing to block
   plan->kernel = kernel;
   plan->rows_per_block = rpb;
   int vw = 2;
@@ -883,6 +909,15 @@ void choose_spmv_kernel(fs_csr_plan* plan, int force_kernel) {
   plan->vec_width = vw;
   plan->tile_items = kMergeTile;
   plan->n_tiles = ceil_div(n_rows + plan->nnz, kMergeTile);
+  if (kernel == FS_KERNEL_NNZBLOCK) {
+    // entries per block = the LDS stage; threads per row from the mean row
+    // so that one pass of 256 / tpr rows covers a block's rows on average
+    plan->tile_items = items;
+    plan->n_tiles = ceil_div(plan->nnz, items);
+    int tpr = 1;
+    while (tpr < 32 && (double)(2 * tpr) * items <= 256.0 * mean) tpr <<= 1;
+    plan->vec_width = tpr;
+  }
   plan->part_bytes = (size_t)(plan->n_tiles + 1) * sizeof(int64_t);
   plan->carry_bytes = (size_t)plan->n_tiles * 2 * acc_bytes(plan->val_t);
 }
@@ -947,6 +982,25 @@ extern "C" int fs_csr_partition(const fs_csr_plan* plan, const void* indptr, voi
                        static_cast<const int64_t*>(indptr), plan->n_rows, plan->nnz, (int64_t)tile_items,
                        n_tiles, static_cast<int64_t*>(part_dev));
   FS_CHECK_LAUNCH("partition_kernel");
+  return FS_OK;
+}
+
+extern "C" int fs_spmv_partition(const fs_csr_plan* plan, const void* indptr, void* part_dev, hipStream_t stream) {
+  if (!plan || !part_dev) return fail(FS_E_INVALID, "fs_spmv_partition: null pointer");
+  if (plan->kernel == FS_KERNEL_MERGE) return fs_csr_partition(plan, indptr, part_dev, plan->tile_items, plan->n_tiles, stream);
+  if (plan->kernel != FS_KERNEL_NNZBLOCK) return FS_OK;  // no partition needed
+  if (!indptr) return fail(FS_E_INVALID, "fs_spmv_partition: indptr is null");
+  const int64_t n_blocks = plan->n_tiles;
+  const unsigned blocks = (unsigned)ceil_div(n_blocks + 1, 256);
+  if (plan->ptr_t == FS_I32)
+    hipLaunchKernelGGL((nnz_partition_kernel<int32_t>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const int32_t*>(indptr), plan->n_rows, (int64_t)plan->tile_items, n_blocks,
+                       static_cast<int64_t*>(part_dev));
+  else
+    hipLaunchKernelGGL((nnz_partition_kernel<int64_t>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const int64_t*>(indptr), plan->n_rows, (int64_t)plan->tile_items, n_blocks,
+                       static_cast<int64_t*>(part_dev));
+  FS_CHECK_LAUNCH("nnz_partition_kernel");
   return FS_OK;
 }
 

@@ -174,6 +174,15 @@ class PreparedCsrSpmv:
                 else:
                     self._part = self._plan.partition(self.kernel_indptr, int(p.tile_items))
                     self._carry = _lib.workspace(p.carry_bytes, data.device)
+            elif p.kernel == _lib.FS_KERNEL_NNZBLOCK:
+                self._part = torch.empty(int(p.n_tiles) + 1, dtype=torch.int64, device=data.device)
+                _lib.check(
+                    _lib.lib().fs_spmv_partition(
+                        p, _lib.ptr(self.kernel_indptr), _lib.ptr(self._part), _lib.stream_handle(data.device)
+                    ),
+                    "fs_spmv_partition",
+                )
+                self._carry = _lib.workspace(p.carry_bytes, data.device)
         return self._plan
 
     def compute_data(self):

@@ -46,7 +46,7 @@ enum fs_status {
 };
 
 /* Kernel variants chosen by fs_csr_analyze. */
-enum fs_kernel { FS_KERNEL_VECTOR = 0, FS_KERNEL_MERGE = 1, FS_KERNEL_STREAM = 2 };
+enum fs_kernel { FS_KERNEL_VECTOR = 0, FS_KERNEL_MERGE = 1, FS_KERNEL_STREAM = 2, FS_KERNEL_NNZBLOCK = 3 };
 
 #define FS_HIST_BINS 24 /* bin b counts rows with length in [2^(b-1), 2^b); bin 0 = empty rows */
 
@@ -55,15 +55,16 @@ typedef struct fs_csr_plan {
   int64_t n_rows, n_cols, nnz;
   int32_t val_t, idx_t, ptr_t;
   int32_t kernel;        /* FS_KERNEL_* chosen for SpMV */
-  int32_t vec_width;     /* lanes per row for FS_KERNEL_VECTOR */
-  int32_t tile_items;    /* merge-path items (rows + nnz) per tile */
+  int32_t vec_width;     /* lanes per row (FS_KERNEL_VECTOR, FS_KERNEL_NNZBLOCK) */
+  int32_t tile_items;    /* merge-path items (rows + nnz) per tile; entries
+                            per block for FS_KERNEL_NNZBLOCK */
   int32_t rows_per_block; /* rows per workgroup for FS_KERNEL_STREAM */
   int32_t reserved;
-  int64_t n_tiles;       /* merge-path tiles */
+  int64_t n_tiles;       /* merge-path tiles / entry blocks */
   int64_t max_row, min_row;
   int64_t hist[FS_HIST_BINS];
-  size_t part_bytes;     /* device bytes for the merge-path partition */
-  size_t carry_bytes;    /* device bytes for merge-path carries (SpMV) */
+  size_t part_bytes;     /* device bytes for the SpMV partition */
+  size_t carry_bytes;    /* device bytes for the SpMV carries */
 } fs_csr_plan;
 
 /* Last error message of the calling thread ("" if none). */
@@ -79,8 +80,9 @@ const char* fs_version(void);
  * opt buckets spmv_csr.py:353-410).  Runs one histogram kernel into
  * `stats_dev` (>= fs_csr_stats_bytes() bytes of device memory), then
  * synchronises `stream` and decides on the host.  force_kernel < 0 lets the
- * analysis choose; 0/1/2 forces FS_KERNEL_VECTOR / FS_KERNEL_MERGE /
- * FS_KERNEL_STREAM (STREAM falls back to MERGE when rows are too long).
+ * analysis choose; 0/1/2/3 forces FS_KERNEL_VECTOR / FS_KERNEL_MERGE /
+ * FS_KERNEL_STREAM / FS_KERNEL_NNZBLOCK (STREAM falls back to MERGE when
+ * rows are too long; NNZBLOCK to STREAM when nnz == 0).
  */
 size_t fs_csr_stats_bytes(void);
 int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t,
@@ -96,6 +98,16 @@ int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t,
 int fs_csr_partition(const fs_csr_plan* plan, const void* indptr,
                      void* part_dev, int tile_items, int64_t n_tiles,
                      hipStream_t stream);
+
+/*
+ * The partition fs_spmv_csr needs for the plan's kernel: the merge-path
+ * partition (FS_KERNEL_MERGE) or, for FS_KERNEL_NNZBLOCK, the first owned
+ * row of every entry block (block b owns the rows whose end pointer lies in
+ * (b*C, (b+1)*C], C = plan->tile_items).  Writes plan->part_bytes bytes;
+ * nothing for the other kernels.
+ */
+int fs_spmv_partition(const fs_csr_plan* plan, const void* indptr,
+                      void* part_dev, hipStream_t stream);
 
 /*
  * y = A x for a CSR A (n_rows x n_cols).  Replaces

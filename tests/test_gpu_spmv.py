@@ -31,7 +31,7 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge", "stream", "panel2", "panel3", "panel8", "panel16"])
+@pytest.fixture(params=["auto", "vector", "merge", "stream", "nnzblock", "panel2", "panel3", "panel8", "panel16"])
 def kernel_choice(request, monkeypatch):
     """Kernel variant under test; panelN = merge path over N column panels."""
     monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
