@@ -79,19 +79,31 @@ constexpr int spmm_batch() {
 // at a time in lane registers (coalesced loads, next chunk prefetched) and
 // broadcast with readlane; row ends are staged the same way.  B-row gathers
 // are double buffered: batch k+1 is issued before batch k is accumulated,
-// so a wave keeps up to 2*U gathers in flight.
-template <class V, int VEC, int U, class I, class P>
+// so a wave keeps up to 2*U*G gathers in flight.
+//
+// G = 2 splits the wave into two 32-lane halves for narrow B (at most
+// 32*VEC columns per column tile): each step takes a pair of nnz, the lower
+// half gathers the B row of the even one and the upper half that of the odd
+// one, so every gather instruction uses all 64 lanes.  The walk stays
+// wave-uniform: a row end between the two nnz of a pair is handled between
+// the two predicated accumulations, and a row's sum is the sum of the two
+// halves' accumulators (one cross-half permute per row).
+template <class V, int VEC, int U, int G, class I, class P>
 __global__ __launch_bounds__(256) void spmm_merge_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
     const V* __restrict__ B, int64_t ldb, V* __restrict__ C, int64_t ldc, int64_t n_dense,
     const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
     typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+  static_assert(G == 1 || G == 2, "one or two lane groups per wave");
   using T = VT<V>;
   using A = typename T::acc;
+  constexpr int LG = 64 / G;  // lanes per group
   const int lane = threadIdx.x & 63;
+  const int grp = G == 1 ? 0 : lane / LG;
+  const int gl = lane % LG;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= n_tiles) return;  // wave-uniform, no barriers below
-  const int64_t col0 = (int64_t)blockIdx.y * 64 * VEC + (int64_t)lane * VEC;
+  const int64_t col0 = (int64_t)blockIdx.y * LG * VEC + (int64_t)gl * VEC;
   const int64_t vrem = n_dense - col0;
   const int valid = vrem <= 0 ? 0 : (vrem >= VEC ? VEC : (int)vrem);
 
@@ -144,26 +156,38 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
   A acc[VEC];
 #pragma unroll
   for (int k = 0; k < VEC; ++k) acc[k] = T::zero();
+  // row total in the lanes of group 0
+  auto combine = [&](int k) -> A {
+    if constexpr (G == 1) {
+      return acc[k];
+    } else {
+      return add(acc[k], shfl(acc[k], lane ^ 32));
+    }
+  };
   auto emit = [&]() {
-    if (valid > 0) {
+    A s[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) s[k] = combine(k);
+    if (valid > 0 && grp == 0) {
       if (row == 0 && head_partial) {
         A* h = head + t * n_dense + col0;
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
-          if (k < valid) h[k] = acc[k];
+          if (k < valid) h[k] = s[k];
       } else {
         V* c = C + (r0 + row) * ldc + col0;
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
-          if (k < valid) c[k] = T::out(acc[k]);
+          if (k < valid) c[k] = T::out(s[k]);
       }
     }
 #pragma unroll
     for (int k = 0; k < VEC; ++k) acc[k] = T::zero();
   };
 
+  // Batch kb covers steps [kb*U, kb*U + U); step s covers nnz [s*G, s*G + G).
   auto issue = [&](int kb, V (&bb)[U][VEC], V (&aa)[U]) {
-    const int ch = (kb * U) >> 6;
+    const int ch = (kb * U * G) >> 6;
     if (ch != chunk) {
       colC = colN;
       valC = valN;
@@ -172,30 +196,46 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int q = kb * U + u;
-      if (q < nz) {
-        const int li = q & 63;
-        const int64_t c = (int64_t)readlane_any(colC, li);
-        aa[u] = readlane_any(valC, li);
-        load_row<V, VEC>(B + c * ldb + col0, valid, bb[u]);
+      const int s = kb * U + u;
+      if (s * G < nz) {
+        const int li = (s * G) & 63;  // G divides 64: a step never straddles a chunk
+        I cc = readlane_any(colC, li);
+        V av = readlane_any(valC, li);
+        if constexpr (G == 2) {
+          const I c1 = readlane_any(colC, li + 1);
+          const V a1 = readlane_any(valC, li + 1);
+          if (grp) {
+            cc = c1;
+            av = a1;
+          }
+        }
+        aa[u] = av;
+        if (s * G + grp < nz) load_row<V, VEC>(B + (int64_t)cc * ldb + col0, valid, bb[u]);
       }
     }
   };
   auto consume = [&](int kb, V (&bb)[U][VEC], V (&aa)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int q = kb * U + u;
-      if (q >= nz) break;
-      while (re <= q) {  // rows that end before nnz q (empty rows included)
-        emit();
-        next_row();
-      }
+      const int s = kb * U + u;
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) acc[k] = T::fma(aa[u], bb[u][k], acc[k]);
+      for (int g = 0; g < G; ++g) {
+        const int q = s * G + g;
+        if (q >= nz) break;
+        while (re <= q) {  // rows that end before nnz q (empty rows included)
+          emit();
+          next_row();
+        }
+        if (grp == g) {
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) acc[k] = T::fma(aa[u], bb[u][k], acc[k]);
+        }
+      }
     }
   };
 
-  const int nb = (nz + U - 1) / U;
+  const int steps = (nz + G - 1) / G;
+  const int nb = (steps + U - 1) / U;
   V bA[U][VEC], bB[U][VEC];
   V aA[U], aB[U];
   if (nb > 0) issue(0, bA, aA);
@@ -211,11 +251,16 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
     emit();
     next_row();
   }
-  if (r1 < n_rows && valid > 0) {
-    A* tl = tail + t * n_dense + col0;
+  if (r1 < n_rows) {
+    A s[VEC];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k)
-      if (k < valid) tl[k] = acc[k];
+    for (int k = 0; k < VEC; ++k) s[k] = combine(k);
+    if (valid > 0 && grp == 0) {
+      A* tl = tail + t * n_dense + col0;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k)
+        if (k < valid) tl[k] = s[k];
+    }
   }
 }
 
@@ -253,14 +298,14 @@ int spmm_vec_for(int val_t, int64_t n_dense) {
   return vec;
 }
 
-template <class V, int VEC>
+template <class V, int VEC, int G>
 int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
                     const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense,
                     const int64_t* part, int64_t n_tiles, void* ws, hipStream_t stream) {
   using A = typename VT<V>::acc;
   A* head = static_cast<A*>(ws);
   A* tail = head + n_tiles * n_dense;
-  const int64_t col_tiles = ceil_div(n_dense, 64 * VEC);
+  const int64_t col_tiles = ceil_div(n_dense, (int64_t)(64 / G) * VEC);
   const int64_t blocks = ceil_div(n_tiles, 4);
   if (blocks > 0x7fffffffLL || col_tiles > 65535) return fail(FS_E_INVALID, "fs_spmm_csr: grid too large");
   dim3 g((unsigned)blocks, (unsigned)col_tiles);
@@ -270,7 +315,7 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
     using I = std::conditional_t<decltype(icode)::value, int64_t, int32_t>;
     using P = std::conditional_t<decltype(pcode)::value, int64_t, int32_t>;
     auto launch = [&](auto uc) {
-      hipLaunchKernelGGL((spmm_merge_kernel<V, VEC, decltype(uc)::value, I, P>), g, dim3(256), 0, stream,
+      hipLaunchKernelGGL((spmm_merge_kernel<V, VEC, decltype(uc)::value, G, I, P>), g, dim3(256), 0, stream,
                          static_cast<const V*>(vals), static_cast<const I*>(cols), static_cast<const P*>(indptr),
                          static_cast<const V*>(B), ldb, static_cast<V*>(C), ldc, n_dense, part, head, tail,
                          plan->n_rows, plan->nnz, n_tiles);
@@ -294,19 +339,28 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   return FS_OK;
 }
 
+template <class V, int VEC>
+int launch_spmm_g(const fs_csr_plan* plan, int groups, const void* vals, const void* cols, const void* indptr,
+                  const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense, const int64_t* part,
+                  int64_t n_tiles, void* ws, hipStream_t s) {
+  if (groups == 2)
+    return launch_spmm_vec<V, VEC, 2>(plan, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
+  return launch_spmm_vec<V, VEC, 1>(plan, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
+}
+
 template <class V>
-int launch_spmm(const fs_csr_plan* plan, int vec, const void* vals, const void* cols, const void* indptr,
-                const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense, const int64_t* part,
-                int64_t n_tiles, void* ws, hipStream_t s) {
+int launch_spmm(const fs_csr_plan* plan, int vec, int groups, const void* vals, const void* cols,
+                const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense,
+                const int64_t* part, int64_t n_tiles, void* ws, hipStream_t s) {
   switch (vec) {
-    case 1: return launch_spmm_vec<V, 1>(plan, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
+    case 1: return launch_spmm_g<V, 1>(plan, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
     case 2:
       if constexpr (sizeof(V) <= 8)
-        return launch_spmm_vec<V, 2>(plan, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
+        return launch_spmm_g<V, 2>(plan, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
       break;
     case 4:
       if constexpr (sizeof(V) == 4)
-        return launch_spmm_vec<V, 4>(plan, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
+        return launch_spmm_g<V, 4>(plan, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, s);
       break;
   }
   return fail(FS_E_INVALID, "fs_spmm_csr: unsupported vector width");
@@ -344,21 +398,27 @@ extern "C" int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void
     return fail(FS_E_INVALID, "fs_spmm_csr: null pointer");
   if (ws_bytes < fs_spmm_workspace_bytes(plan->val_t, n_tiles, n_dense) || (!ws && n_tiles > 0))
     return fail(FS_E_WORKSPACE, "fs_spmm_csr: workspace too small");
+  const size_t vsz[] = {4, 8, 8, 16};
+  const size_t esz = vsz[plan->val_t];
   int vec = spmm_vec_for(plan->val_t, n_dense);
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_VEC")) {
     const int v = std::atoi(e);
-    if (v == 1 || v == 2 || v == 4) vec = std::min(vec, v);
+    if ((v == 1 || v == 2 || v == 4) && (size_t)v * esz <= 16) vec = v;
   }
   // Vector loads need every lane's B/C slice aligned to the vector width.
-  const size_t vsz[] = {4, 8, 8, 16};
-  const size_t esz = vsz[plan->val_t];
   while (vec > 1 && ((ldb % vec) || (ldc % vec) || ((uintptr_t)B % (esz * vec)) || ((uintptr_t)C % (esz * vec))))
     vec >>= 1;
+  // Narrow B: two 32-lane groups per wave, each gathering its own B row.
+  int groups = n_dense <= 32 * vec ? 2 : 1;
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_G")) {
+    const int gv = std::atoi(e);
+    if (gv == 1 || gv == 2) groups = gv;
+  }
   const int64_t* part = static_cast<const int64_t*>(part_dev);
   switch (plan->val_t) {
-    case FS_F32: return launch_spmm<float>(plan, vec, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
-    case FS_F64: return launch_spmm<double>(plan, vec, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
-    case FS_C64: return launch_spmm<c32>(plan, vec, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
-    default: return launch_spmm<c64>(plan, vec, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
+    case FS_F32: return launch_spmm<float>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
+    case FS_F64: return launch_spmm<double>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
+    case FS_C64: return launch_spmm<c32>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
+    default: return launch_spmm<c64>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
   }
 }

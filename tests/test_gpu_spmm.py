@@ -28,11 +28,24 @@ def _check(data, indices, indptr, shape, B, op, **kw):
     return C
 
 
+@pytest.fixture(params=["auto", "G1", "G2", "VEC2-G2", "VEC4-G1"])
+def lane_layout(request, monkeypatch):
+    """SpMM lane layout under test: lane groups per wave (G) and columns per lane (VEC)."""
+    monkeypatch.delenv("FLAGSPARSE_SPMM_G", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SPMM_VEC", raising=False)
+    for part in request.param.split("-"):
+        if part.startswith("G"):
+            monkeypatch.setenv("FLAGSPARSE_SPMM_G", part[1:])
+        elif part.startswith("VEC"):
+            monkeypatch.setenv("FLAGSPARSE_SPMM_VEC", part[3:])
+    return request.param
+
+
 @pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
 @pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
 @pytest.mark.parametrize("op", OPS)
 @pytest.mark.parametrize("n_dense", [1, 4, 33, 64, 96, 130, 256, 300])
-def test_spmm_matches_oracle(device, dtype, index_dtype, op, n_dense):
+def test_spmm_matches_oracle(lane_layout, device, dtype, index_dtype, op, n_dense):
     m, k = 611, 333
     d, i, p, sh = S.random_csr(m, k, 0.03, dtype, index_dtype, device, seed=n_dense, empty_row_every=9,
                                long_rows=((300, 330),))
@@ -69,7 +82,7 @@ def test_spmm_matches_dense_reference(device, M, N, K, dtype, index_dtype, op):
     assert torch.allclose(out, ref, rtol=tol, atol=tol)
 
 
-def test_spmm_long_rows_and_empty_rows(device):
+def test_spmm_long_rows_and_empty_rows(lane_layout, device):
     # rows far longer than a tile (split across tiles, fixed up in order)
     d, i, p, sh = S.random_csr(40, 20000, 0.0, torch.float32, torch.int32, device, seed=1,
                                long_rows=((3, 12000), (4, 7000), (30, 19999)))
