@@ -6,7 +6,9 @@ A step is one pass of the hot path over one synthetic input: one SpMV
 y = A x (or one SpMM C = A B) through the public operator API with the
 matrix prepared once (analysis / transpose outside the timed region, as
 the reference's prepare_* APIs do).  Inputs are generated on the GPU from
-a fixed seed and resident in HBM before timing starts.
+a fixed seed and resident in HBM before timing starts.  Before the W
+warm-up steps the step runs back to back, untimed, for 0.2 s so that the
+timed steps do not see the GPU's clock ramp from idle.
 
 Default workload: BASELINE config 2 (27-point stencil SpMV, 128^3 grid,
 fp64 / int32).  The line reports effective algorithmic HBM GB/s (bytes =
@@ -27,6 +29,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+SETTLE_S = 0.2  # untimed back-to-back steps before the warm-up (clock ramp)
 METRIC = "effective HBM GB/s (% of peak) + GFLOP/s for CSR SpMV/SpMM, 1 MI355X"
 
 CONFIGS = {
@@ -47,7 +50,14 @@ DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 # counts are in profiles/<kernel>_<workload>.md).  Reported as
 # roofline.traffic; configs not profiled with the current kernels report null.
 MEASURED_TRAFFIC = {
-    "c2_spmv_stencil128_f64_i32": 776.6e6,
+    "c1_spmv_uniform4096_f32_i32": 0.747e6,
+    "c2_spmv_stencil128_f64_i32": 776.8e6,
+    "c3_spmv_powerlaw4M_f32_i32": 2440.2e6,
+    "c3_spmv_powerlaw4M_f32_i64": 3127.1e6,
+    "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
+    "c4_spmm_uniform1M_f32_i32_n64_trans": 9184.5e6,
+    "c5_spmm_rmat21_f32_i64_n256_non": 30747.6e6,
+    "c5_spmm_rmat21_c64_i64_n32_conj": 7198.9e6,
 }
 
 
@@ -235,7 +245,15 @@ def run(args):
             full()
             extra["ms_with_transpose"] = round(time_loop(full, max(2, args.steps // 10), stream), 4)
 
-    # warm-up, then the timed steps
+    # Untimed clock settle (at least SETTLE_S of back-to-back steps: a step
+    # is ~0.15 ms, so a handful of warm-up steps ends before the GPU leaves
+    # its idle clocks), then the W warm-up steps, then exactly K timed steps.
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     ms_per_step = time_loop(step, args.steps, stream)

@@ -100,6 +100,19 @@ struct VT<c64> {
 __device__ inline double add(double a, double b) { return a + b; }
 __device__ inline c64 add(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
 
+// Streaming (non-temporal) store of one output element: results written
+// once and not re-read by the kernel skip L2 allocation priority.
+__device__ inline void store_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ inline void store_stream(double* p, double v) { __builtin_nontemporal_store(v, p); }
+__device__ inline void store_stream(c32* p, c32 v) {
+  __builtin_nontemporal_store(v.re, &p->re);
+  __builtin_nontemporal_store(v.im, &p->im);
+}
+__device__ inline void store_stream(c64* p, c64 v) {
+  __builtin_nontemporal_store(v.re, &p->re);
+  __builtin_nontemporal_store(v.im, &p->im);
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane moves.  DPP for distances inside a 16-lane row, ds_swizzle for
 // the 16-lane xor inside each 32-lane half, readlane across halves.
