@@ -43,6 +43,8 @@ from .spmm_csr import (
     resolve_spmm_csr_algorithm,
 )
 from .spmv_csr import PreparedCsrSpmv, flagsparse_spmv_csr, prepare_spmv_csr
+from .spmv_coo import PreparedCoo, flagsparse_spmv_coo, prepare_spmv_coo
+from .spmm_coo import flagsparse_spmm_coo
 
 __all__ = [
     "SUPPORTED_VALUE_DTYPES",
@@ -74,4 +76,8 @@ __all__ = [
     "coo_to_csr_for_spmv",
     "prepare_spmv_coo_tocsr",
     "flagsparse_spmv_coo_tocsr",
+    "PreparedCoo",
+    "prepare_spmv_coo",
+    "flagsparse_spmv_coo",
+    "flagsparse_spmm_coo",
 ]

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
     const V* __restrict__ B, int64_t ldb, V* __restrict__ C, int64_t ldc, int64_t n_dense,
     const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
-    typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+    typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz, int64_t n_tiles, int xcd_cols) {
   static_assert(G == 1 || G == 2, "one or two lane groups per wave");
   using T = VT<V>;
   using A = typename T::acc;
@@ -101,9 +101,16 @@ __global__ __launch_bounds__(256) void spmm_merge_kernel(
   const int lane = threadIdx.x & 63;
   const int grp = G == 1 ? 0 : lane / LG;
   const int gl = lane % LG;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // Column tile and tile block.  With xcd_cols > 0 the grid is 1-D and
+  // column tile = workgroup id % xcd_cols: workgroups go to the 8 XCDs
+  // round-robin, so (for xcd_cols a power of two up to 8) each XCD always
+  // works on the same slice of B's columns and its L2 keeps the hot rows of
+  // that slice.
+  const int64_t ctile = xcd_cols > 0 ? (int64_t)(blockIdx.x % (unsigned)xcd_cols) : (int64_t)blockIdx.y;
+  const int64_t tblk = xcd_cols > 0 ? (int64_t)(blockIdx.x / (unsigned)xcd_cols) : (int64_t)blockIdx.x;
+  const int64_t t = tblk * 4 + (threadIdx.x >> 6);
   if (t >= n_tiles) return;  // wave-uniform, no barriers below
-  const int64_t col0 = (int64_t)blockIdx.y * LG * VEC + (int64_t)gl * VEC;
+  const int64_t col0 = ctile * LG * VEC + (int64_t)gl * VEC;
   const int64_t vrem = n_dense - col0;
   const int valid = vrem <= 0 ? 0 : (vrem >= VEC ? VEC : (int)vrem);
 
@@ -308,7 +315,10 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   const int64_t col_tiles = ceil_div(n_dense, (int64_t)(64 / G) * VEC);
   const int64_t blocks = ceil_div(n_tiles, 4);
   if (blocks > 0x7fffffffLL || col_tiles > 65535) return fail(FS_E_INVALID, "fs_spmm_csr: grid too large");
-  dim3 g((unsigned)blocks, (unsigned)col_tiles);
+  int xcd_cols = 0;
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_XCD")) xcd_cols = std::atoi(e) != 0 ? (int)col_tiles : 0;
+  if (xcd_cols > 0 && blocks * col_tiles > 0x7fffffffLL) xcd_cols = 0;
+  dim3 g = xcd_cols > 0 ? dim3((unsigned)(blocks * col_tiles)) : dim3((unsigned)blocks, (unsigned)col_tiles);
   int u = spmm_batch<V, VEC>();
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_U")) u = std::atoi(e);
   auto go = [&](auto icode, auto pcode) {
@@ -318,7 +328,7 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
       hipLaunchKernelGGL((spmm_merge_kernel<V, VEC, decltype(uc)::value, G, I, P>), g, dim3(256), 0, stream,
                          static_cast<const V*>(vals), static_cast<const I*>(cols), static_cast<const P*>(indptr),
                          static_cast<const V*>(B), ldb, static_cast<V*>(C), ldc, n_dense, part, head, tail,
-                         plan->n_rows, plan->nnz, n_tiles);
+                         plan->n_rows, plan->nnz, n_tiles, xcd_cols);
     };
     if (u <= 4) launch(std::integral_constant<int, 4>{});
     else launch(std::integral_constant<int, 8>{});

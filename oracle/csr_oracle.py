@@ -18,6 +18,9 @@ It restates the reference algorithm in numpy:
                            complex128, the more accurate of the two)
   SpMM numerics            spmm_csr.py:2684-2789 (same dtype policy)
   empty cases              spmm_csr.py:2706-2710 (zeros)
+  COO -> CSR               spmv_csr.py:926-950 (key row * n_cols + col)
+  COO SpMV / SpMM          spmv_coo.py:425-644, spmm_coo.py:101-142, 696-723
+                           (duplicates summed; trans / conj swap row and col)
 
 Pinning (tests/test_oracle.py): every function is checked against dense
 brute force on small inputs, scipy's independent CSR->CSC conversion and
@@ -197,6 +200,30 @@ def coo_to_csr(data, row, col, shape):
     order = np.argsort(key, kind="stable")
     indptr[1:] = np.cumsum(np.bincount(row[order], minlength=n_rows))
     return data[order], col[order].astype(np.int32), indptr
+
+
+def spmv_coo(data, row, col, x, shape, op=None):
+    """COO SpMV y = op(A) x in the wide accumulator type (spmv_coo.py:425-644).
+
+    A is the COO with duplicate (row, col) entries summed; op=trans / conj
+    work on (col, row) with the data conjugated for conj (spmv_coo.py:525-554).
+    Restated as: sort to CSR (coo_to_csr), then spmv_csr_wide."""
+    code = normalize_op(op)
+    n_rows, n_cols = int(shape[0]), int(shape[1])
+    data = np.asarray(data)
+    if code != 0:
+        if code == 2 and np.iscomplexobj(data):
+            data = np.conj(data)
+        row, col, n_rows, n_cols = col, row, n_cols, n_rows
+    d, c, p = coo_to_csr(data, row, col, (n_rows, n_cols))
+    return spmv_csr_wide(d, c, p, x, (n_rows, n_cols))
+
+
+def spmm_coo(data, row, col, B, shape):
+    """COO SpMM C = A B in the wide accumulator type (spmm_coo.py:101-142,
+    696-723: duplicates coalesced by summation, then the row-run product)."""
+    d, c, p = coo_to_csr(data, row, col, shape)
+    return spmm_csr_wide(d, c, p, B, shape)
 
 
 def load_mtx_reference(file_path):

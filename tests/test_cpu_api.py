@@ -41,7 +41,8 @@ def test_public_surface():
         "prepare_spmm_csr_opt_alg2", "prepare_spmm_csr_opt_alg2_preprocess", "flagsparse_spmm_csr_opt",
         "flagsparse_spmm_csr_opt_alg1", "flagsparse_spmm_csr_opt_alg1_preprocess", "flagsparse_spmm_csr_opt_alg2",
         "flagsparse_spmm_csr_opt_alg2_preprocess", "coo_to_csr_for_spmv", "prepare_spmv_coo_tocsr",
-        "flagsparse_spmv_coo_tocsr",
+        "flagsparse_spmv_coo_tocsr", "PreparedCoo", "prepare_spmv_coo", "flagsparse_spmv_coo",
+        "flagsparse_spmm_coo",
     }
     assert expected <= set(dir(fs)) and expected <= set(fs.__all__)
 
@@ -194,3 +195,80 @@ def test_error_metrics():
     m = spmm_mod._spmm_validation_metrics(cand, ref)
     assert m["max_relative_error"] == pytest.approx(0.125)
     assert m["relative_threshold"] == 1e-12 and m["matches_threshold"] is False
+
+
+def test_coo_validation_before_launch_on_cpu_tensors():
+    """spmv_coo.py:390-422, 726-790 and spmm_coo.py:335-368, 651-668: checks
+    that fire before any device work, with the reference's messages."""
+    from flagsparse_amd import spmv_coo as coo_mod
+
+    d = torch.ones(3)
+    i = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(TypeError, match="data, row, col must all be torch.Tensor"):
+        fs.prepare_spmv_coo([1.0], i, i, (2, 2))
+    with pytest.raises(ValueError, match="data, row, col must be 1D"):
+        fs.prepare_spmv_coo(d.view(3, 1), i, i, (2, 2))
+    with pytest.raises(ValueError, match="data, row, col must be CUDA tensors"):
+        fs.prepare_spmv_coo(d, i, i, (2, 2))
+    with pytest.raises(ValueError, match="data, row, col, x, shape required when prepared is None"):
+        fs.flagsparse_spmv_coo(d, i, i, None, (2, 2))
+    with pytest.raises(ValueError, match="transpose conflicts with op"):
+        fs.flagsparse_spmv_coo(d, i, i, d, (2, 2), op="non", transpose=True)
+    with pytest.raises(ValueError, match="transpose=True conflicts with op=non"):
+        fs.prepare_spmv_coo(d, i, i, (2, 2), transpose=True, op="non")
+    with pytest.raises(ValueError, match="index_fallback_policy must be 'auto' or 'strict'"):
+        fs.prepare_spmv_coo(d, i, i, (2, 2), index_fallback_policy="maybe")
+    with pytest.raises(ValueError, match="op must be one of: 0=non, 1=trans, 2=conj"):
+        fs.flagsparse_spmv_coo(d, i, i, d, (2, 2), op="hermitian")
+    assert coo_mod._normalize_spmv_coo_op(None, transpose=True) == 1
+    assert coo_mod._normalize_spmv_coo_op(2) == 2 and coo_mod._spmv_coo_op_to_name("TRANS") == "trans"
+
+    B = torch.ones(2, 4)
+    with pytest.raises(ValueError, match="shape must be a 2-tuple"):
+        fs.flagsparse_spmm_coo(d, i, i, B, (2, 2, 2))
+    with pytest.raises(ValueError, match="data, row, and col must be 1D tensors"):
+        fs.flagsparse_spmm_coo(d.view(3, 1), i, i, B, (2, 2))
+    with pytest.raises(ValueError, match="B must be a 2D dense tensor"):
+        fs.flagsparse_spmm_coo(d, i, i, B.view(-1), (2, 2))
+    with pytest.raises(ValueError, match="shape dimensions must be non-negative"):
+        fs.flagsparse_spmm_coo(d, i, i, B, (-1, 2))
+    with pytest.raises(ValueError, match="same length"):
+        fs.flagsparse_spmm_coo(d[:2], i, i, B, (2, 2))
+    with pytest.raises(ValueError, match=r"B.shape\[0\] must be n_cols=3, got 2"):
+        fs.flagsparse_spmm_coo(d, i, i, B, (2, 3))
+    with pytest.raises(ValueError, match="data, row, col, and B must be CUDA tensors"):
+        fs.flagsparse_spmm_coo(d, i, i, B, (2, 2))
+    with pytest.raises(ValueError, match="block_n must be positive when provided"):
+        fs.flagsparse_spmm_coo(d, i, i, B, (2, 2), block_n=0)
+    with pytest.raises(TypeError, match="unexpected keyword argument 'op'"):
+        fs.flagsparse_spmm_coo(d, i, i, B, (2, 2), op="trans")
+
+
+def test_coo_int32_fallback_with_injected_launcher(monkeypatch):
+    """spmv_coo.py:701-723 with an injected failing launch (CPU tensors, no
+    device work): auto retries on int32 indices, strict re-raises, and an
+    unsafe narrowing raises the reference's RuntimeError."""
+    from flagsparse_amd import spmv_coo as coo_mod
+
+    srt = coo_mod._SortedCoo(torch.ones(3), torch.tensor([0, 0, 1]), torch.tensor([0, 1, 1]),
+                             torch.tensor([0, 2, 3]), torch.tensor([0, 2, 3]), (2, 2))
+    launch = coo_mod._PreparedCooLaunch(srt, srt.data, srt.row, srt.col, (2, 2), seg_starts=srt.seg_starts)
+    calls = []
+
+    def fake(lau, x, block_size, num_warps, block_inner):
+        calls.append(lau.row.dtype)
+        if lau.row.dtype == torch.int64:
+            raise RuntimeError("forced int64 launch failure")
+        return torch.zeros(lau.n_rows)
+
+    monkeypatch.setattr(coo_mod, "_hip_spmv_coo_kernel", fake)
+    y = coo_mod._run_spmv_coo_prepared_with_fallback(launch, torch.ones(2), 256, 4, 128)
+    assert calls == [torch.int64, torch.int32] and y.shape == (2,)
+    strict = coo_mod._PreparedCooLaunch(srt, srt.data, srt.row, srt.col, (2, 2), seg_starts=srt.seg_starts,
+                                        index_fallback_policy="strict")
+    with pytest.raises(RuntimeError, match="forced int64 launch failure"):
+        coo_mod._run_spmv_coo_prepared_with_fallback(strict, torch.ones(2), 256, 4, 128)
+    big = torch.tensor([0, 2**31, 1])
+    unsafe = coo_mod._PreparedCooLaunch(srt, srt.data, big, srt.col, (2**31 + 1, 2), seg_starts=srt.seg_starts)
+    with pytest.raises(RuntimeError, match="native int64 COO SpMV failed and int32 fallback is unsafe: row index range"):
+        coo_mod._run_spmv_coo_prepared_with_fallback(unsafe, torch.ones(2), 256, 4, 128)

@@ -207,3 +207,60 @@ def test_coo_to_csr_vs_scipy_and_stability():
     assert np.array_equal(d, [20.0, 40.0, 10.0, 30.0]) and np.array_equal(c, [3, 0, 2, 2]) and np.array_equal(p, [0, 1, 4])
     d2, c2, p2 = O.coo_to_csr(d, np.array([0, 1, 1, 1]), c, (2, 4))
     assert np.array_equal(d2, d) and np.array_equal(c2, c)
+
+
+def _dense_from_coo(data, row, col, shape):
+    D = np.zeros(shape, dtype=np.result_type(data.dtype, np.float64))
+    np.add.at(D, (row, col), data)  # duplicates summed
+    return D
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.complex64, np.complex128])
+@pytest.mark.parametrize("op", ["non", "trans", "conj"])
+def test_spmv_coo_vs_dense_with_duplicates(dtype, op):
+    rng = np.random.default_rng(11)
+    m, n, nnz = 23, 17, 150  # dense enough that duplicates occur
+    row = rng.integers(0, m, nnz)
+    col = rng.integers(0, n, nnz)
+    data = rng.uniform(-1, 1, nnz)
+    if np.dtype(dtype).kind == "c":
+        data = data + 1j * rng.uniform(-1, 1, nnz)
+    data = data.astype(dtype)
+    D = _dense_from_coo(data, row, col, (m, n))
+    A = {"non": D, "trans": D.T, "conj": D.conj().T}[op]
+    x = rng.uniform(-1, 1, A.shape[1]).astype(dtype)
+    y = O.spmv_coo(data, row, col, x, (m, n), op=op)
+    assert y.shape == (A.shape[0],)
+    assert O.relative_error(y, A @ x.astype(A.dtype)) < 1e-12
+    if np.dtype(dtype).kind == "c" and op != "non":
+        # trans and conj differ on complex data: a dropped conjugation fails here
+        other = O.spmv_coo(data, row, col, x, (m, n), op="trans" if op == "conj" else "conj")
+        assert O.relative_error(other, y) > 1e-3
+
+
+def test_spmv_coo_hand_example():
+    # A = [[1, 0, 2], [0, 0, 0]] with the (0, 2) entry given as 0.5 + 1.5 (a duplicate)
+    data = np.array([0.5, 1.0, 1.5]); row = np.array([0, 0, 0]); col = np.array([2, 0, 2])
+    x = np.array([10.0, 20.0, 30.0])
+    assert np.array_equal(O.spmv_coo(data, row, col, x, (2, 3)), [70.0, 0.0])
+    assert np.array_equal(O.spmv_coo(data, row, col, np.array([3.0, 5.0]), (2, 3), op="trans"), [3.0, 0.0, 6.0])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.complex64, np.complex128])
+def test_spmm_coo_vs_dense_with_duplicates(dtype):
+    rng = np.random.default_rng(12)
+    m, k, n, nnz = 19, 13, 7, 120
+    row = rng.integers(0, m, nnz)
+    col = rng.integers(0, k, nnz)
+    data = rng.uniform(-1, 1, nnz)
+    B = rng.uniform(-1, 1, (k, n))
+    if np.dtype(dtype).kind == "c":
+        data = data + 1j * rng.uniform(-1, 1, nnz)
+        B = B + 1j * rng.uniform(-1, 1, (k, n))
+    data, B = data.astype(dtype), B.astype(dtype)
+    D = _dense_from_coo(data, row, col, (m, k))
+    C = O.spmm_coo(data, row, col, B, (m, k))
+    assert C.shape == (m, n)
+    assert O.relative_error(C, D @ B.astype(D.dtype)) < 1e-12
+    # homogeneity in B (scaling by 2 is exact in binary floating point)
+    assert O.relative_error(O.spmm_coo(data, row, col, 2 * B, (m, k)), 2 * C) < 1e-15
