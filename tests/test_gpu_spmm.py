@@ -101,6 +101,26 @@ def test_spmm_deterministic(device):
     assert torch.equal(C1, C2)
 
 
+@pytest.mark.parametrize("lanes", [("1", "1"), ("2", "1"), ("1", "2")], ids=["VEC1-G1", "VEC2-G1", "VEC1-G2"])
+def test_spmm_xcd_column_tiles_bit_identical(device, monkeypatch, lanes):
+    """The XCD-affine mapping of column tiles (1-D grid, tile = id % tiles)
+    changes only which XCD runs a tile: results are bit-identical to the
+    2-D grid, for 2, 4 and 8 column tiles and for other counts."""
+    vec, g = lanes
+    monkeypatch.setenv("FLAGSPARSE_SPMM_VEC", vec)
+    monkeypatch.setenv("FLAGSPARSE_SPMM_G", g)
+    d, i, p, sh = S.powerlaw(1 << 13, torch.float32, torch.int64, device, seed=4)
+    for n_dense in (64, 128, 200, 256, 512):
+        B = S.dense(sh[1], n_dense, torch.float32, device, seed=n_dense)
+        monkeypatch.setenv("FLAGSPARSE_SPMM_XCD", "1")
+        C_xcd = fs.flagsparse_spmm_csr(d, i, p, B, sh)
+        monkeypatch.setenv("FLAGSPARSE_SPMM_XCD", "0")
+        C_2d = fs.flagsparse_spmm_csr(d, i, p, B, sh)
+        assert torch.equal(C_xcd, C_2d), n_dense
+    monkeypatch.delenv("FLAGSPARSE_SPMM_XCD")
+    _check(d, i, p, sh, S.dense(sh[1], 256, torch.float32, device, seed=9), "non")
+
+
 def test_spmm_api_contract(device):
     """Negative / positive API checks of tests/test_spmm.py:766-898."""
     data = torch.tensor([1.0, 2.0, 3.0], dtype=torch.float32, device=device)
