@@ -252,6 +252,13 @@ class PanelledCsr:
             "fs_csr_panelize",
         )
         del ws
+        # The stacked copy is this build's own format: store it with int32
+        # column indices / row pointer whenever they fit, so int64 inputs
+        # stream 4 bytes less per entry (the caller's tensors keep their type).
+        if self.indices.dtype == torch.int64 and n_cols - 1 <= _INDEX_LIMIT_INT32:
+            self.indices = self.indices.to(torch.int32)
+        if self.indptr.dtype == torch.int64 and nnz <= _INDEX_LIMIT_INT32:
+            self.indptr = self.indptr.to(torch.int32)
         self.plan = analyze_csr(
             self.data, self.indices, self.indptr, self.n_panels * n_rows, n_cols, force_kernel=_lib.FS_KERNEL_MERGE
         )

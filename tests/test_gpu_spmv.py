@@ -251,15 +251,19 @@ def test_spmv_full_size_configs(device, config):
     _sampled_rows_check(data, indices, indptr, sh, x1, y1, rows, REL_TOL[data.dtype])
 
 
-def test_spmv_panels_match_unpanelled(device, monkeypatch):
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64], ids=["int32", "int64"])
+def test_spmv_panels_match_unpanelled(device, monkeypatch, index_dtype):
     """Power-law matrix at the BASELINE size: the column-panel path (chosen by
     default there) agrees with the single-pass merge path and the oracle on
-    sampled rows, and is deterministic."""
+    sampled rows, and is deterministic.  int64 input is stacked with int32
+    indices (the stacked copy is internal; the caller's tensors keep int64)."""
     monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
     monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
-    data, indices, indptr, sh = S.powerlaw(4194304, torch.float32, torch.int32, device, seed=3)
+    data, indices, indptr, sh = S.powerlaw(4194304, torch.float32, index_dtype, device, seed=3)
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
     assert prep.kernel_name == "panel"
+    assert prep._panels.indices.dtype == torch.int32 and prep._panels.indptr.dtype == torch.int32
+    assert prep.kernel_indices.dtype == index_dtype
     x = S.vector(sh[1], data.dtype, device, seed=23)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=prep))
