@@ -7,25 +7,27 @@
 // row ids, and build the new indptr with bincount + cumsum; conj is applied
 // to the data first (spmv_csr.py:615-618, spmm_csr.py:341-349).
 //
-// Here: an LSD radix sort over the column index, 8 bits per pass.  Each
-// wave owns a contiguous sub-tile of kSub entries and walks it in 64-entry
-// chunks.  Lanes holding equal digits find each other with eight ballots
-// ("peer masks"), so the per-digit counts and the stable rank of every
-// entry come from popcounts: no atomics, and equal keys keep their input
-// order, which is what makes the result identical to the reference's
-// stable argsort.  Per pass: count -> exclusive scan over
-// [digit][sub-tile] -> stable scatter.  The new indptr is read off the
-// sorted keys (colptr[c] = first position whose key >= c).
+// Here: an LSD radix sort over the column index, 8 bits per pass, over wave
+// sub-tiles of kSub entries held in registers.  Lanes holding equal digits
+// find each other with eight ballots ("peer masks"), so per-digit counts and
+// the stable rank of every entry come from popcounts: no atomics, and equal
+// keys keep their input order, which is what makes the result identical to
+// the reference's stable argsort.  Per pass: count -> exclusive scan over
+// [digit][sub-tile] -> scatter, which sorts each sub-tile by digit in LDS
+// first so that every digit's entries leave as one contiguous run.  The new
+// indptr is read off the sorted keys (colptr[c] = first position whose
+// key >= c).
 #include "fs_common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstring>
 
 namespace fs {
 
 constexpr int kRadixBits = 8;
 constexpr int kDigits = 1 << kRadixBits;
-constexpr int kChunks = 64;                 // 64-entry chunks per wave sub-tile
+constexpr int kChunks = 32;                 // 64-entry chunks per wave sub-tile
 constexpr int64_t kSub = 64 * kChunks;      // entries per wave sub-tile
 constexpr int kWavesPerBlock = 4;
 constexpr int kScanItems = 16;              // per-thread items in the scan kernels
@@ -63,6 +65,19 @@ __device__ inline K load_key(const void* src, int kind, int64_t e) {
   return static_cast<const K*>(src)[e];
 }
 
+// A wave's sub-tile lives in registers: lane l holds entries l, l + 64, ...
+// (chunk c = entries [64c, 64c + 64) of the sub-tile), loaded with all loads
+// in flight before any is used.
+template <class K>
+__device__ inline void load_tile_keys(const void* keys, int kind, int64_t base, int64_t n, int lane,
+                                      K (&key)[kChunks]) {
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int64_t e = base + (int64_t)ch * 64 + lane;
+    key[ch] = e < n ? load_key<K>(keys, kind, e) : (K)0;
+  }
+}
+
 template <class K>
 __global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict__ keys, int kind, int64_t n,
                                                           int shift, int64_t n_sub,
@@ -74,15 +89,16 @@ __global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict
   if (sub >= n_sub) return;  // wave-local work only
   unsigned* hist = s_hist[w];
   for (int d = lane; d < kDigits; d += 64) hist[d] = 0;
-  wave_sync_t();
   const int64_t base = sub * kSub;
+  K key[kChunks];
+  load_tile_keys<K>(keys, kind, base, n, lane, key);
+  wave_sync_t();
+#pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
-    const int64_t e = base + (int64_t)ch * 64 + lane;
-    const bool valid = e < n;
+    const bool valid = base + (int64_t)ch * 64 + lane < n;
     const uint64_t active = __ballot(valid);
     if (active == 0) break;
-    const K key = valid ? load_key<K>(keys, kind, e) : (K)0;
-    const unsigned digit = (unsigned)(key >> shift) & (kDigits - 1);
+    const unsigned digit = (unsigned)(key[ch] >> shift) & (kDigits - 1);
     const uint64_t peers = peer_mask(digit, active);
     if (valid && count_below_t(peers) == 0) hist[digit] += (unsigned)__popcll(peers);
     wave_sync_t();
@@ -90,39 +106,105 @@ __global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict
   for (int d = lane; d < kDigits; d += 64) counts[(int64_t)d * n_sub + sub] = hist[d];
 }
 
+// Exclusive scan of 256 per-digit counts held 4 per lane (digits 4l..4l+3);
+// writes the starts to out[256].
+__device__ inline void wave_digit_scan(const unsigned (&c)[4], int lane, unsigned* out) {
+  const unsigned lane_sum = c[0] + c[1] + c[2] + c[3];
+  unsigned incl = lane_sum;
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned y = (unsigned)__builtin_amdgcn_ds_bpermute((lane - off) << 2, (int)incl);
+    if (lane >= off) incl += y;
+  }
+  unsigned run = incl - lane_sum;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    out[4 * lane + k] = run;
+    run += c[k];
+  }
+}
+
+// Stable scatter of one pass.  One wave per sub-tile (kSub entries):
+//  1. keys / positions into registers (all loads in flight);
+//  2. the tile's digit counts (ballot peer masks) and their exclusive scan;
+//  3. every entry to its digit-sorted slot of an LDS copy of the tile, in
+//     input order within a digit (rank = lanes of the same digit below it,
+//     plus the digit's cursor), which keeps the sort stable;
+//  4. the LDS copy written out in order: entry i of digit d goes to
+//     offsets[d][sub] + (i - start[d]), so a digit's entries leave as one
+//     contiguous run instead of single scattered stores.
 template <class K, class Pos>
-__global__ __launch_bounds__(256) void radix_scatter_kernel(const void* __restrict__ keys_in, int kind,
-                                                            const Pos* __restrict__ pos_in, int64_t n, int shift,
-                                                            int64_t n_sub, const int64_t* __restrict__ offsets,
-                                                            K* __restrict__ keys_out, Pos* __restrict__ pos_out) {
-  __shared__ int64_t s_off[kWavesPerBlock][kDigits];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int64_t sub = (int64_t)blockIdx.x * kWavesPerBlock + w;
+__global__ __launch_bounds__(64) void radix_scatter_kernel(const void* __restrict__ keys_in, int kind,
+                                                           const Pos* __restrict__ pos_in, int64_t n, int shift,
+                                                           int64_t n_sub, const int64_t* __restrict__ offsets,
+                                                           K* __restrict__ keys_out, Pos* __restrict__ pos_out) {
+  __shared__ K s_key[kSub];
+  __shared__ Pos s_pos[kSub];
+  __shared__ unsigned s_start[kDigits];
+  __shared__ unsigned s_cur[kDigits];
+  __shared__ int64_t s_glob[kDigits];
+  const int lane = threadIdx.x;
+  const int64_t sub = blockIdx.x;
   if (sub >= n_sub) return;
-  int64_t* off = s_off[w];
-  for (int d = lane; d < kDigits; d += 64) off[d] = offsets[(int64_t)d * n_sub + sub];
-  wave_sync_t();
   const int64_t base = sub * kSub;
+  const int cnt = n - base < kSub ? (int)(n - base) : (int)kSub;
+  K key[kChunks];
+  Pos pos[kChunks];
+  load_tile_keys<K>(keys_in, kind, base, n, lane, key);
+#pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
     const int64_t e = base + (int64_t)ch * 64 + lane;
-    const bool valid = e < n;
+    pos[ch] = e < n ? (pos_in ? pos_in[e] : (Pos)e) : (Pos)0;
+  }
+  for (int d = lane; d < kDigits; d += 64) {
+    s_cur[d] = 0;
+    s_glob[d] = offsets[(int64_t)d * n_sub + sub];
+  }
+  wave_sync_t();
+  // 2. per-digit counts of the tile
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const bool valid = ch * 64 + lane < cnt;
     const uint64_t active = __ballot(valid);
     if (active == 0) break;
-    const K key = valid ? load_key<K>(keys_in, kind, e) : (K)0;
-    const Pos p = valid ? (pos_in ? pos_in[e] : (Pos)e) : (Pos)0;
-    const unsigned digit = (unsigned)(key >> shift) & (kDigits - 1);
+    const unsigned digit = (unsigned)(key[ch] >> shift) & (kDigits - 1);
+    const uint64_t peers = peer_mask(digit, active);
+    if (valid && count_below_t(peers) == 0) s_cur[digit] += (unsigned)__popcll(peers);
+    wave_sync_t();
+  }
+  unsigned c4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) c4[k] = s_cur[4 * lane + k];
+  wave_sync_t();
+  wave_digit_scan(c4, lane, s_start);
+  wave_sync_t();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s_cur[4 * lane + k] = s_start[4 * lane + k];
+  wave_sync_t();
+  // 3. stable placement into the digit-sorted LDS copy
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const bool valid = ch * 64 + lane < cnt;
+    const uint64_t active = __ballot(valid);
+    if (active == 0) break;
+    const unsigned digit = (unsigned)(key[ch] >> shift) & (kDigits - 1);
     const uint64_t peers = peer_mask(digit, active);
     const int rank = count_below_t(peers);
-    int64_t dst = 0;
-    if (valid) dst = off[digit] + rank;
-    wave_sync_t();
     if (valid) {
-      keys_out[dst] = key;
-      pos_out[dst] = p;
-      if (rank == 0) off[digit] = dst + __popcll(peers);
+      const unsigned slot = s_cur[digit] + (unsigned)rank;
+      s_key[slot] = key[ch];
+      s_pos[slot] = pos[ch];
     }
     wave_sync_t();
+    if (valid && rank == 0) s_cur[digit] += (unsigned)__popcll(peers);
+    wave_sync_t();
+  }
+  // 4. runs out
+  for (int i = lane; i < cnt; i += 64) {
+    const K k = s_key[i];
+    const unsigned digit = (unsigned)(k >> shift) & (kDigits - 1);
+    const int64_t dst = s_glob[digit] + (int64_t)(i - (int)s_start[digit]);
+    keys_out[dst] = k;
+    pos_out[dst] = s_pos[i];
   }
 }
 
@@ -195,13 +277,40 @@ __global__ __launch_bounds__(256) void scan_downsweep_kernel(int64_t* __restrict
 // ---- row ids, gather, column pointer ----
 constexpr int kExpandItems = 16;
 
-template <class P, class OI>
-__global__ __launch_bounds__(256) void expand_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz,
-                                                          OI* __restrict__ rowid) {
-  const int64_t e0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kExpandItems;
+// Row id of every entry.  A workgroup covers kExpandTile entries; thread t
+// walks entries [16t, 16t + 16) of the tile (one binary search for the first,
+// then the row pointer), staging the ids in LDS (index padded by one per 16,
+// so the stride-16 walk is free of bank conflicts); the tile then leaves with
+// coalesced stores.
+constexpr int kExpandTile = 256 * kExpandItems;
+__device__ inline int expand_slot(int j) { return j + (j >> 4); }
+
+// First row r in [lo, hi] whose end pointer exceeds e (rowptr[r + 1] > e).
+template <class P>
+__device__ inline int64_t row_of_entry(const P* __restrict__ rowptr, int64_t lo, int64_t hi, int64_t e) {
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)rowptr[mid + 1] <= e)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// Call with all 256 threads (contains a barrier).
+template <class P, class RT>
+__device__ inline void expand_tile_rows(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz, int64_t base,
+                                        RT* s_row) {
+  // rows of the tile's first and last entries bound every thread's search
+  __shared__ int64_t s_bounds[2];
+  const int64_t last = (base + kExpandTile < nnz ? base + kExpandTile : nnz) - 1;
+  if (threadIdx.x == 0) s_bounds[0] = row_of_entry<P>(rowptr, 0, n_rows - 1, base);
+  if (threadIdx.x == 64) s_bounds[1] = row_of_entry<P>(rowptr, 0, n_rows - 1, last);
+  __syncthreads();
+  const int64_t e0 = base + (int64_t)threadIdx.x * kExpandItems;
   if (e0 >= nnz) return;
-  // first row whose end exceeds e0
-  int64_t lo = 0, hi = n_rows - 1;
+  int64_t lo = s_bounds[0], hi = s_bounds[1];  // first row whose end exceeds e0
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
     if ((int64_t)rowptr[mid + 1] <= e0)
@@ -218,7 +327,21 @@ __global__ __launch_bounds__(256) void expand_rows_kernel(const P* __restrict__ 
       ++row;
       rend = (int64_t)rowptr[row + 1];
     }
-    rowid[e] = (OI)row;
+    s_row[expand_slot((int)threadIdx.x * kExpandItems + k)] = (RT)row;
+  }
+}
+
+template <class P, class OI>
+__global__ __launch_bounds__(256) void expand_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz,
+                                                          OI* __restrict__ rowid) {
+  using RT = std::conditional_t<sizeof(OI) == 8, uint64_t, uint32_t>;  // LDS word as wide as the output index
+  __shared__ RT s_row[kExpandTile + kExpandTile / 16];
+  const int64_t base = (int64_t)blockIdx.x * kExpandTile;
+  expand_tile_rows<P, RT>(rowptr, n_rows, nnz, base, s_row);
+  __syncthreads();
+  for (int j = threadIdx.x; j < kExpandTile; j += 256) {
+    const int64_t e = base + j;
+    if (e < nnz) rowid[e] = (OI)s_row[expand_slot(j)];
   }
 }
 
@@ -233,6 +356,42 @@ __global__ __launch_bounds__(256) void transpose_gather_kernel(const V* __restri
   if (conj) v = VT<V>::conj(v);
   t_vals[k] = v;
   t_cols[k] = rowid[p];
+}
+
+// 4-byte values with 4-byte output indices: each entry's (value, row) packed
+// into one 8-byte word, so the permutation gather below is one random 8-byte
+// read per entry instead of two random 4-byte reads.  Values are read and
+// words written coalesced, through the same LDS tile as expand_rows_kernel.
+template <class P, class V, class OI>
+__global__ __launch_bounds__(256) void expand_pack_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz,
+                                                          const V* __restrict__ vals, uint2* __restrict__ packed) {
+  static_assert(sizeof(V) == 4 && sizeof(OI) == 4, "packs a 4-byte value with a 4-byte row index");
+  __shared__ unsigned s_row[kExpandTile + kExpandTile / 16];
+  __shared__ unsigned s_val[kExpandTile + kExpandTile / 16];
+  const int64_t base = (int64_t)blockIdx.x * kExpandTile;
+  for (int j = threadIdx.x; j < kExpandTile; j += 256) {
+    const int64_t e = base + j;
+    if (e < nnz) __builtin_memcpy(&s_val[expand_slot(j)], &vals[e], 4);
+  }
+  expand_tile_rows<P, unsigned>(rowptr, n_rows, nnz, base, s_row);
+  __syncthreads();
+  for (int j = threadIdx.x; j < kExpandTile; j += 256) {
+    const int64_t e = base + j;
+    if (e < nnz) packed[e] = make_uint2(s_val[expand_slot(j)], s_row[expand_slot(j)]);
+  }
+}
+
+template <class V, class OI, class Pos>
+__global__ __launch_bounds__(256) void transpose_gather_packed_kernel(const uint2* __restrict__ packed,
+                                                                      const Pos* __restrict__ perm, int64_t nnz,
+                                                                      V* __restrict__ t_vals, OI* __restrict__ t_cols) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= nnz) return;
+  const uint2 w = packed[(int64_t)perm[k]];
+  V v;
+  __builtin_memcpy(&v, &w.x, 4);
+  t_vals[k] = v;  // real 4-byte values only: conj is the identity
+  t_cols[k] = (OI)w.y;
 }
 
 template <class K, class OP>
@@ -338,8 +497,8 @@ int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, i
     FS_CHECK_LAUNCH("radix_count_kernel");
     int rc = device_exclusive_scan(counts, L.n_counts, partial, s);
     if (rc != FS_OK) return rc;
-    hipLaunchKernelGGL((radix_scatter_kernel<K, Pos>), dim3(blocks), dim3(256), 0, s, kin, kind, pin, nnz, shift,
-                       L.n_sub, counts, kout, pout);
+    hipLaunchKernelGGL((radix_scatter_kernel<K, Pos>), dim3((unsigned)L.n_sub), dim3(64), 0, s, kin, kind, pin, nnz,
+                       shift, L.n_sub, counts, kout, pout);
     FS_CHECK_LAUNCH("radix_scatter_kernel");
     kin = kout;
     kind = 2;
@@ -372,14 +531,27 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
     FS_CHECK_LAUNCH("iota_kernel");
     perm = pa;
   }
-  OI* rowid = reinterpret_cast<OI*>(ws + L.off_rowid);
-  hipLaunchKernelGGL((expand_rows_kernel<P, OI>), dim3((unsigned)ceil_div(ceil_div(nnz, kExpandItems), 256)),
-                     dim3(256), 0, s, static_cast<const P*>(indptr), n_rows, nnz, rowid);
-  FS_CHECK_LAUNCH("expand_rows_kernel");
-  hipLaunchKernelGGL((transpose_gather_kernel<V, OI, Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s,
-                     static_cast<const V*>(vals), rowid, perm, nnz, conj, static_cast<V*>(t_vals),
-                     static_cast<OI*>(t_cols));
-  FS_CHECK_LAUNCH("transpose_gather_kernel");
+  const unsigned expand_blocks = (unsigned)ceil_div(nnz, kExpandTile);
+  if constexpr (sizeof(V) == 4 && sizeof(OI) == 4) {
+    // the rowid slot holds 8 bytes per entry: room for the packed words
+    uint2* packed = reinterpret_cast<uint2*>(ws + L.off_rowid);
+    hipLaunchKernelGGL((expand_pack_kernel<P, V, OI>), dim3(expand_blocks), dim3(256), 0, s,
+                       static_cast<const P*>(indptr), n_rows, nnz, static_cast<const V*>(vals), packed);
+    FS_CHECK_LAUNCH("expand_pack_kernel");
+    hipLaunchKernelGGL((transpose_gather_packed_kernel<V, OI, Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0,
+                       s, packed, perm, nnz, static_cast<V*>(t_vals), static_cast<OI*>(t_cols));
+    FS_CHECK_LAUNCH("transpose_gather_packed_kernel");
+    (void)conj;
+  } else {
+    OI* rowid = reinterpret_cast<OI*>(ws + L.off_rowid);
+    hipLaunchKernelGGL((expand_rows_kernel<P, OI>), dim3(expand_blocks), dim3(256), 0, s,
+                       static_cast<const P*>(indptr), n_rows, nnz, rowid);
+    FS_CHECK_LAUNCH("expand_rows_kernel");
+    hipLaunchKernelGGL((transpose_gather_kernel<V, OI, Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s,
+                       static_cast<const V*>(vals), rowid, perm, nnz, conj, static_cast<V*>(t_vals),
+                       static_cast<OI*>(t_cols));
+    FS_CHECK_LAUNCH("transpose_gather_kernel");
+  }
   hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
                      n_cols, static_cast<OP*>(t_indptr));
   FS_CHECK_LAUNCH("colptr_kernel");
