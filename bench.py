@@ -139,6 +139,16 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz):
     frac = nnz_s / max(1, full_nnz)
     value = full_bytes * frac / secs / 1e9
     info = CB.host_info()
+    # the other CPU path the reference compares against: torch.sparse.mm on a
+    # CPU CSR tensor, all torch threads, same sample (5 s budget)
+    t_secs, t_reps, t_threads = CB.time_torch_cpu(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R,
+                                                  min_seconds=5.0)
+    torch_leg = {
+        "value": round(full_bytes * frac / t_secs / 1e9, 3),
+        "unit": "GB/s",
+        "cores": int(t_threads),
+        "sample": f"torch.sparse.mm(CPU CSR, dense) on the same rows, median of {t_reps} runs ({t_secs * 1e3:.2f} ms each)",
+    }
     return {
         "value": round(value, 3),
         "unit": "GB/s",
@@ -150,6 +160,7 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz):
             f"({secs * 1e3:.2f} ms each); value = full algorithmic bytes x sampled nnz fraction / time; "
             f"host {info['model']}, {info['affinity']} cores visible"
         ),
+        "torch_sparse_mm": torch_leg,
     }
 
 
