@@ -45,6 +45,23 @@ from .spmm_csr import (
 from .spmv_csr import PreparedCsrSpmv, flagsparse_spmv_csr, prepare_spmv_csr
 from .spmv_coo import PreparedCoo, flagsparse_spmv_coo, prepare_spmv_coo
 from .spmm_coo import flagsparse_spmm_coo
+from .alpha_spmm import (
+    PreparedAlphaSpmmAlg1,
+    alpha_spmm_alg1_tle_opt2_unavailable_reason,
+    alpha_spmm_alg1_tle_opt_unavailable_reason,
+    alpha_spmm_alg1_tle_unavailable_reason,
+    flagsparse_alpha_spmm_alg1,
+    flagsparse_alpha_spmm_alg1_tle,
+    flagsparse_alpha_spmm_alg1_tle_opt,
+    flagsparse_alpha_spmm_alg1_tle_opt2,
+    is_alpha_spmm_alg1_tle_available,
+    is_alpha_spmm_alg1_tle_opt2_available,
+    is_alpha_spmm_alg1_tle_opt_available,
+    prepare_alpha_spmm_alg1,
+    prepare_alpha_spmm_alg1_tle,
+    prepare_alpha_spmm_alg1_tle_opt,
+    prepare_alpha_spmm_alg1_tle_opt2,
+)
 
 __all__ = [
     "SUPPORTED_VALUE_DTYPES",
@@ -80,4 +97,19 @@ __all__ = [
     "prepare_spmv_coo",
     "flagsparse_spmv_coo",
     "flagsparse_spmm_coo",
+    "PreparedAlphaSpmmAlg1",
+    "prepare_alpha_spmm_alg1",
+    "prepare_alpha_spmm_alg1_tle",
+    "prepare_alpha_spmm_alg1_tle_opt",
+    "prepare_alpha_spmm_alg1_tle_opt2",
+    "flagsparse_alpha_spmm_alg1",
+    "flagsparse_alpha_spmm_alg1_tle",
+    "flagsparse_alpha_spmm_alg1_tle_opt",
+    "flagsparse_alpha_spmm_alg1_tle_opt2",
+    "is_alpha_spmm_alg1_tle_available",
+    "is_alpha_spmm_alg1_tle_opt_available",
+    "is_alpha_spmm_alg1_tle_opt2_available",
+    "alpha_spmm_alg1_tle_unavailable_reason",
+    "alpha_spmm_alg1_tle_opt_unavailable_reason",
+    "alpha_spmm_alg1_tle_opt2_unavailable_reason",
 ]

@@ -42,7 +42,9 @@ def test_public_surface():
         "flagsparse_spmm_csr_opt_alg1", "flagsparse_spmm_csr_opt_alg1_preprocess", "flagsparse_spmm_csr_opt_alg2",
         "flagsparse_spmm_csr_opt_alg2_preprocess", "coo_to_csr_for_spmv", "prepare_spmv_coo_tocsr",
         "flagsparse_spmv_coo_tocsr", "PreparedCoo", "prepare_spmv_coo", "flagsparse_spmv_coo",
-        "flagsparse_spmm_coo",
+        "flagsparse_spmm_coo", "PreparedAlphaSpmmAlg1", "prepare_alpha_spmm_alg1", "flagsparse_alpha_spmm_alg1",
+        "flagsparse_alpha_spmm_alg1_tle", "flagsparse_alpha_spmm_alg1_tle_opt", "flagsparse_alpha_spmm_alg1_tle_opt2",
+        "is_alpha_spmm_alg1_tle_available", "alpha_spmm_alg1_tle_unavailable_reason",
     }
     assert expected <= set(dir(fs)) and expected <= set(fs.__all__)
 
@@ -272,3 +274,20 @@ def test_coo_int32_fallback_with_injected_launcher(monkeypatch):
     unsafe = coo_mod._PreparedCooLaunch(srt, srt.data, big, srt.col, (2**31 + 1, 2), seg_starts=srt.seg_starts)
     with pytest.raises(RuntimeError, match="native int64 COO SpMV failed and int32 fallback is unsafe: row index range"):
         coo_mod._run_spmv_coo_prepared_with_fallback(unsafe, torch.ones(2), 256, 4, 128)
+
+
+def test_alpha_spmm_alg1_surface_and_validation_on_cpu():
+    """alpha_spmm_alg1.py:39-150, 866-889, 1037-1182: TLE routes report
+    unavailable; argument checks fire before any device work."""
+    assert fs.is_alpha_spmm_alg1_tle_available() is False
+    assert fs.is_alpha_spmm_alg1_tle_opt_available() is False and fs.is_alpha_spmm_alg1_tle_opt2_available() is False
+    assert "FlagTree" in fs.alpha_spmm_alg1_tle_unavailable_reason()
+    d = torch.ones(2)
+    i = torch.zeros(2, dtype=torch.int32)
+    p = torch.tensor([0, 2], dtype=torch.int32)
+    with pytest.raises(TypeError, match="prepared must be a PreparedAlphaSpmmAlg1 instance"):
+        fs.flagsparse_alpha_spmm_alg1(B=torch.ones(2, 2), prepared=object())
+    with pytest.raises(ValueError, match="data, indices, indptr, and shape are required"):
+        fs.flagsparse_alpha_spmm_alg1(d, i, None, torch.ones(2, 2), (1, 2))
+    with pytest.raises(ValueError, match="must be CUDA tensors|CUDA"):
+        fs.prepare_alpha_spmm_alg1(d, i, p, (1, 2))
