@@ -100,6 +100,16 @@ struct VT<c64> {
 __device__ inline double add(double a, double b) { return a + b; }
 __device__ inline c64 add(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
 
+// Streaming (non-temporal) load of one element.
+__device__ inline float load_stream(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ inline double load_stream(const double* p) { return __builtin_nontemporal_load(p); }
+__device__ inline c32 load_stream(const c32* p) {
+  return c32{__builtin_nontemporal_load(&p->re), __builtin_nontemporal_load(&p->im)};
+}
+__device__ inline c64 load_stream(const c64* p) {
+  return c64{__builtin_nontemporal_load(&p->re), __builtin_nontemporal_load(&p->im)};
+}
+
 // Streaming (non-temporal) store of one output element: results written
 // once and not re-read by the kernel skip L2 allocation priority.
 __device__ inline void store_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }

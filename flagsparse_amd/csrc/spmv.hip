@@ -531,8 +531,8 @@ __device__ inline void merge_tile(const V* __restrict__ vals, const I* __restric
     const int j = k * 64 + lane;
     cv[k] = 0;
     if (j < Nz) {
-      av[k] = vals[n0 + j];
-      cv[k] = cols[n0 + j];
+      av[k] = load_stream(vals + n0 + j);  // A is read once: keep x in L2 (power-law 0.608 -> 0.591 ms)
+      cv[k] = __builtin_nontemporal_load(cols + n0 + j);
     }
   }
   // 2. row-end mask (one ds_or per row end).
