@@ -108,8 +108,12 @@ def time_loop(fn, steps, stream):
     return start.elapsed_time(end) / steps
 
 
-def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz):
-    """Reference CPU path (scipy CSR product, 1 thread) on a bounded sample."""
+def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz, gpu_out):
+    """Reference CPU path (scipy CSR product, 1 thread) on a bounded sample.
+
+    Returns (baseline, accuracy): accuracy is max|out - y64| / max|y64| of
+    the GPU output `gpu_out` on the sampled rows against the fp64 oracle
+    (the reference's normwise metric, spmm_csr.py:95-103)."""
     import numpy as np
 
     from oracle import cpu_baseline as CB
@@ -161,6 +165,23 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz):
             f"host {info['model']}, {info['affinity']} cores visible"
         ),
         "torch_sparse_mm": torch_leg,
+    }, _accuracy(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R, gpu_out[:rows])
+
+
+def _accuracy(d, i, p, shape, R, out_rows):
+    """Normwise relative error of the GPU rows against the fp64 oracle."""
+    from oracle import csr_oracle as O
+
+    wide = O.spmv_csr_wide if R.ndim == 1 else O.spmm_csr_wide
+    ref = wide(d, i, p, R, shape, op="non")
+    err = O.relative_error(out_rows.cpu().numpy(), ref)
+    tol = 1e-12 if d.dtype in ("float64", "complex128") else 1e-5
+    return {
+        "max_rel_err": float(f"{err:.3e}"),
+        "tolerance": tol,
+        "pass": bool(err <= tol),
+        "rows": int(shape[0]),
+        "reference": "fp64 oracle (oracle/csr_oracle.py) on the cpu_baseline row sample",
     }
 
 
@@ -315,7 +336,10 @@ def run(args):
         "extra": dict(extra, generate_s=round(gen_s, 2)),
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cfg, data, indices, indptr, shape, rhs, bytes_alg, nnz)
+        out = step()
+        torch.cuda.synchronize()
+        line["cpu_baseline"], line["accuracy"] = cpu_baseline(cfg, data, indices, indptr, shape, rhs, bytes_alg, nnz,
+                                                              out)
     return line
 
 
