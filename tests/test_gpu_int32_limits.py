@@ -124,3 +124,4 @@ def test_spmm_nnz_above_int32(big):
     assert C.shape == (N, 2)
     assert torch.equal(C[:, 0].double(), big["y_non"])
     assert torch.equal(C[:, 1].double(), -2 * big["y_non"])
+
