@@ -174,12 +174,22 @@ def _accuracy(d, i, p, shape, R, out_rows):
 
     wide = O.spmv_csr_wide if R.ndim == 1 else O.spmm_csr_wide
     ref = wide(d, i, p, R, shape, op="non")
-    err = O.relative_error(out_rows.cpu().numpy(), ref)
+    import numpy as np
+    import torch
+
+    from flagsparse_amd._common import _tolerance_for_dtype
+
+    out = out_rows.cpu().numpy()
+    err = O.relative_error(out, ref)
     tol = 1e-12 if d.dtype in ("float64", "complex128") else 1e-5
+    atol, rtol = _tolerance_for_dtype(torch.from_numpy(np.empty(0, dtype=d.dtype)).dtype)
     return {
         "max_rel_err": float(f"{err:.3e}"),
         "tolerance": tol,
         "pass": bool(err <= tol),
+        # the reference suite's elementwise check, reported as information
+        "allclose": bool(np.allclose(out, ref.astype(out.dtype), rtol=rtol, atol=atol)),
+        "allclose_rtol_atol": [rtol, atol],
         "rows": int(shape[0]),
         "reference": "fp64 oracle (oracle/csr_oracle.py) on the cpu_baseline row sample",
     }

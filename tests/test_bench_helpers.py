@@ -21,6 +21,7 @@ def test_accuracy_exact_output_passes():
     out = torch.tensor([5.0, 0.0, 18.0])
     acc = bench._accuracy(d, i, p, sh, x, out)
     assert acc["max_rel_err"] == 0.0 and acc["pass"] and acc["tolerance"] == 1e-5 and acc["rows"] == 3
+    assert acc["allclose"] and acc["allclose_rtol_atol"] == [1e-5, 1e-6]
 
 
 def test_accuracy_detects_a_wrong_row():
@@ -29,6 +30,7 @@ def test_accuracy_detects_a_wrong_row():
     out = torch.tensor([5.0, 0.0, 18.5])  # |0.5| / max|y| = 0.5 / 18
     acc = bench._accuracy(d, i, p, sh, x, out)
     assert acc["max_rel_err"] == pytest.approx(0.5 / 18, rel=1e-3) and not acc["pass"]
+    assert not acc["allclose"]
 
 
 def test_accuracy_spmm_and_f64_tolerance():
