@@ -27,7 +27,7 @@ import torch
 
 from ._common import _INDEX_LIMIT_INT32, SUPPORTED_INDEX_DTYPES
 from .coo import coo_to_csr_for_spmv
-from .spmv_csr import _hip_spmv_csr_impl_prepared, prepare_spmv_csr
+from .spmv_csr import _hip_spmv_csr_impl_prepared, _prepare_spmv
 
 SUPPORTED_SPMV_COO_VALUE_DTYPES = (
     torch.float32,
@@ -88,7 +88,7 @@ class _SortedCoo:
     """One orientation of the matrix, sorted by (row, col): the reference's
     (data, row, col, seg_starts) plus the row pointer the kernels walk."""
 
-    __slots__ = ("data", "row", "col", "seg_starts", "indptr", "shape", "_csr", "_conj_csr")
+    __slots__ = ("data", "row", "col", "seg_starts", "indptr", "shape", "one_shot", "_csr", "_conj_csr")
 
     def __init__(self, data, row, col, seg_starts, indptr, shape):
         self.data = data
@@ -97,6 +97,7 @@ class _SortedCoo:
         self.seg_starts = seg_starts
         self.indptr = indptr
         self.shape = shape
+        self.one_shot = False  # True for a single unprepared call: no column-panel copy
         self._csr = None
         self._conj_csr = None
 
@@ -105,11 +106,15 @@ class _SortedCoo:
         if conj:
             if self._conj_csr is None:
                 data = self.data.conj().resolve_conj().contiguous()
-                self._conj_csr = prepare_spmv_csr(data, self.col, self.indptr, self.shape)
+                self._conj_csr = self._prepare(data)
             return self._conj_csr
         if self._csr is None:
-            self._csr = prepare_spmv_csr(self.data, self.col, self.indptr, self.shape)
+            self._csr = self._prepare(self.data)
         return self._csr
+
+    def _prepare(self, data):
+        return _prepare_spmv(data, self.col, self.indptr, self.shape, 256, None, False, None, "auto",
+                             one_shot=self.one_shot)
 
 
 def _seg_starts_from_indptr(indptr, nnz, index_dtype):
@@ -411,6 +416,9 @@ def flagsparse_spmv_coo(
             raise ValueError("data, row, col, x, shape required when prepared is None")
         prepared = prepare_spmv_coo(data, row, col, shape, sort_by_row=sort_by_row, transpose=transpose_flag, op=op,
                                     index_fallback_policy=index_fallback_policy)
+        for srt in (prepared._sorted_non, prepared._sorted_trans):
+            if srt is not None:
+                srt.one_shot = True
     else:
         if x is None:
             raise TypeError("x is required when prepared is set")

@@ -107,6 +107,7 @@ class PreparedCsrSpmv:
         "_part",
         "_carry",
         "_panels",
+        "_one_shot",
     )
 
     def __init__(
@@ -156,6 +157,7 @@ class PreparedCsrSpmv:
         self._part = None
         self._carry = None
         self._panels = None
+        self._one_shot = False  # built for a single call: no column-panel copy
 
     # -- HIP plan (built lazily on first run, then cached) ------------------
     def hip_plan(self):
@@ -166,7 +168,7 @@ class PreparedCsrSpmv:
             )
             p = self._plan.plan
             if p.kernel == _lib.FS_KERNEL_MERGE:
-                n_panels = _spmv_panel_count(p, data.dtype)
+                n_panels = _spmv_panel_count(p, data.dtype, self._one_shot)
                 if n_panels > 1:
                     self._panels = PanelledCsr(
                         data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols, n_panels
@@ -209,13 +211,19 @@ _PANEL_X_BYTES = 6 << 20
 _PANEL_SLICE_BYTES = 9 << 19
 
 
-def _spmv_panel_count(plan, dtype):
+def _spmv_panel_count(plan, dtype, one_shot=False):
     """Column panels for a merge-path matrix (0 = none).  FLAGSPARSE_SPMV_PANELS=N
     forces N (0/1 off); otherwise the fewest of 2, 4, 8 whose x slice is at most
-    ~4.5 MiB, for x above 6 MiB and rows averaging at least 2 entries per panel."""
+    ~4.5 MiB, for x above 6 MiB and rows averaging at least 2 entries per panel.
+
+    A one-shot call (no prepared object kept) gets none: building the panel
+    copy costs several launches of the unpanelled kernel (C3: 2.7 ms to save
+    0.4 ms)."""
     env = os.environ.get("FLAGSPARSE_SPMV_PANELS")
     if env is not None:
         return max(0, int(env))
+    if one_shot:
+        return 0
     n_rows, n_cols, nnz = int(plan.n_rows), int(plan.n_cols), int(plan.nnz)
     x_bytes = n_cols * torch.empty(0, dtype=dtype).element_size()
     if n_rows == 0 or x_bytes <= _PANEL_X_BYTES:
@@ -400,6 +408,12 @@ def prepare_spmv_csr(
     read them back; the HIP kernels do not iterate fixed segments, so they
     do not limit which rows can be processed.
     """
+    return _prepare_spmv(data, indices, indptr, shape, block_nnz, max_segments, transpose, op, index_fallback_policy)
+
+
+def _prepare_spmv(
+    data, indices, indptr, shape, block_nnz, max_segments, transpose, op, index_fallback_policy, one_shot=False
+):
     index_fallback_policy = _normalize_spmv_index_fallback_policy(index_fallback_policy)
     op_code = _normalize_spmv_op(op, transpose=transpose)
     if op is not None and bool(transpose) and op_code == SPMV_OP_NON:
@@ -432,6 +446,7 @@ def prepare_spmv_csr(
         op=op_code,
         index_fallback_policy=index_fallback_policy,
     )
+    prepared._one_shot = bool(one_shot)
     if n_rows > 0:
         plan = prepared.hip_plan()
         max_row = plan.max_row_nnz
@@ -584,15 +599,17 @@ def flagsparse_spmv_csr(
     if prepared is None:
         if any(arg is None for arg in (data, indices, indptr, shape)):
             raise ValueError("data, indices, indptr, and shape are required when prepared is not provided")
-        prepared = prepare_spmv_csr(
+        prepared = _prepare_spmv(
             data,
             indices,
             indptr,
             shape,
-            block_nnz=block_nnz,
-            max_segments=max_segments,
-            op=op_code,
-            index_fallback_policy=index_fallback_policy,
+            block_nnz,
+            max_segments,
+            False,
+            op_code,
+            index_fallback_policy,
+            one_shot=True,
         )
     else:
         if op_explicit and op_code != prepared.op:

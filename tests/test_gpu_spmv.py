@@ -274,6 +274,12 @@ def test_spmv_panels_match_unpanelled(device, monkeypatch, index_dtype):
     # both are f64 sums rounded once to f32: at most one ulp apart
     diff = (y.double() - y0.double()).abs()
     assert bool((diff <= y0.double().abs() * 2.0**-23 + 1e-30).all())
+    # a one-shot call (no prepared object) skips the panel copy: same kernel
+    # and bits as the unpanelled prepared path
+    monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS")
+    y1, meta = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh, return_meta=True)
+    assert meta["kernel"] == "merge"
+    assert torch.equal(y1, y0)
     gen = np.random.default_rng(1)
     rows = sorted(set(gen.integers(0, sh[0], 3000).tolist()) | {0, sh[0] - 1})
     _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[data.dtype])
