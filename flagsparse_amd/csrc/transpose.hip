@@ -231,13 +231,18 @@ __device__ inline int64_t block_exclusive_scan(int64_t v, int64_t* s_wave, int64
   return wave_base + x - v;
 }
 
+// Tile total: integer sums do not depend on order, so the loads are
+// coalesced (item k * 256 + t of the tile to thread t).
 __global__ __launch_bounds__(256) void scan_reduce_kernel(const int64_t* __restrict__ in, int64_t n,
                                                           int64_t* __restrict__ partial) {
   __shared__ int64_t s_wave[4];
-  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + threadIdx.x;
+  int64_t v[kScanItems];
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) v[k] = base + k * 256 < n ? in[base + k * 256] : 0;
   int64_t s = 0;
-  for (int k = 0; k < kScanItems; ++k)
-    if (base + k < n) s += in[base + k];
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) s += v[k];
   int64_t total;
   block_exclusive_scan(s, s_wave, total);
   if (threadIdx.x == 0) partial[blockIdx.x] = total;
@@ -256,21 +261,42 @@ __global__ __launch_bounds__(256) void scan_partials_kernel(int64_t* __restrict_
   }
 }
 
+// Tile scan: coalesced loads into LDS, each thread scans 16 consecutive
+// items there (slot i + i / 16 keeps that stride-16 walk free of bank
+// conflicts), then coalesced stores.
+__device__ inline int scan_slot(int i) { return i + (i >> 4); }
+
 __global__ __launch_bounds__(256) void scan_downsweep_kernel(int64_t* __restrict__ data, int64_t n,
                                                              const int64_t* __restrict__ partial) {
   __shared__ int64_t s_wave[4];
-  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  __shared__ int64_t s_tile[kScanTile + kScanTile / 16];
+  const int t = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    const int i = k * 256 + t;
+    s_tile[scan_slot(i)] = base + i < n ? data[base + i] : 0;
+  }
+  __syncthreads();
   int64_t v[kScanItems];
   int64_t s = 0;
+#pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
-    v[k] = base + k < n ? data[base + k] : 0;
+    v[k] = s_tile[scan_slot(t * kScanItems + k)];
     s += v[k];
   }
   int64_t total;
   int64_t run = partial[blockIdx.x] + block_exclusive_scan(s, s_wave, total);
+#pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
-    if (base + k < n) data[base + k] = run;
+    s_tile[scan_slot(t * kScanItems + k)] = run;
     run += v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    const int i = k * 256 + t;
+    if (base + i < n) data[base + i] = s_tile[scan_slot(i)];
   }
 }
 
