@@ -27,7 +27,10 @@ namespace fs {
 
 constexpr int kRadixBits = 8;
 constexpr int kDigits = 1 << kRadixBits;
-constexpr int kChunks = 32;                 // 64-entry chunks per wave sub-tile
+#ifndef FS_RADIX_CHUNKS
+#define FS_RADIX_CHUNKS 32
+#endif
+constexpr int kChunks = FS_RADIX_CHUNKS;    // 64-entry chunks per wave sub-tile
 constexpr int64_t kSub = 64 * kChunks;      // entries per wave sub-tile
 constexpr int kWavesPerBlock = 4;
 constexpr int kScanItems = 16;              // per-thread items in the scan kernels
