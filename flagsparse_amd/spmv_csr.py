@@ -320,8 +320,9 @@ def _check_structure(data, indices, indptr, n_cols, messages):
     else:
         probes.append(torch.zeros(1, dtype=torch.int64, device=indptr.device))
     if nnz > 0:
-        probes.append(indices.min().reshape(1).to(torch.int64))
-        probes.append(indices.max().reshape(1).to(torch.int64))
+        lo, hi = torch.aminmax(indices)  # one pass over the indices for both bounds
+        probes.append(lo.reshape(1).to(torch.int64))
+        probes.append(hi.reshape(1).to(torch.int64))
     vals = torch.cat(probes).cpu().tolist()
     if int(vals[0]) != 0:
         raise ValueError(messages["start"])
