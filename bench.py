@@ -51,7 +51,7 @@ DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 # roofline.traffic; configs not profiled with the current kernels report null.
 MEASURED_TRAFFIC = {
     "c1_spmv_uniform4096_f32_i32": 0.747e6,
-    "c2_spmv_stencil128_f64_i32": 776.7e6,
+    "c2_spmv_stencil128_f64_i32": 733.3e6,
     "c3_spmv_powerlaw4M_f32_i32": 2440.0e6,
     "c3_spmv_powerlaw4M_f32_i64": 2440.4e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
@@ -234,6 +234,16 @@ def run(args):
             _lib.stream_handle(device),
         )
         kernel_call = lambda: lib.fs_spmv_csr(*args_abi)  # noqa: E731
+        sell = prep._sell
+        if sell is not None:
+            # SELL-64 copy of a short-row matrix with column locality (the stencil)
+            args_abi = (
+                _lib.value_code(sell.vals.dtype), _lib.index_code(sell.cols.dtype), _lib.index_code(sell.indptr.dtype),
+                sell.n_rows, _lib.ptr(sell.vals), _lib.ptr(sell.cols), _lib.ptr(sell.slice_ptr), _lib.ptr(sell.indptr),
+                _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(device),
+            )
+            kernel_call = lambda: lib.fs_spmv_sell(*args_abi)  # noqa: E731
+            extra["sell_stored_slots"] = sell.padded
         pan = prep._panels
         if pan is not None:
             # column panels: the timed call is the whole panel sequence
@@ -248,7 +258,8 @@ def run(args):
         bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
         flops = S.flops_spmv(nnz, complex_values)
         kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
-                       "panel": "spmv_panel_merge_kernel", "nnzblock": "spmv_nnzblock_kernel"}[prep.kernel_name]
+                       "panel": "spmv_panel_merge_kernel", "nnzblock": "spmv_nnzblock_kernel",
+                       "sell": "spmv_sell_kernel"}[prep.kernel_name]
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:

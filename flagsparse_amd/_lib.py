@@ -55,6 +55,9 @@ EXPORTED_SYMBOLS = (
     "fs_csr_panelize",
     "fs_spmv_panels_workspace_bytes",
     "fs_spmv_csr_panels",
+    "fs_sell_slots",
+    "fs_csr_to_sell",
+    "fs_spmv_sell",
 )
 
 
@@ -136,6 +139,12 @@ def _declare(lib):
     lib.fs_spmv_csr_panels.restype = _i32
     lib.fs_spmv_csr_panels.argtypes = [ctypes.POINTER(FsCsrPlan), _i32, ctypes.POINTER(_i64), _vp, _vp, _vp, _vp, _vp,
                                        _vp, _vp, _sz, _vp]
+    lib.fs_sell_slots.restype = _i32
+    lib.fs_sell_slots.argtypes = [_i32, _i64, _vp, _vp, _vp]
+    lib.fs_csr_to_sell.restype = _i32
+    lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.fs_spmv_sell.restype = _i32
+    lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
 
 
 def load_library(path=None):

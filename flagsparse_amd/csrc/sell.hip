@@ -1,0 +1,252 @@
+// sell.hip — sliced-ELL (SELL-64) copy of a CSR matrix and its SpMV, gfx950.
+//
+// A prepared matrix whose rows are short and of similar length (stencils,
+// FEM meshes) is copied once into SELL-64: rows are cut into slices of 64
+// consecutive rows, one slice per wave; slot j of the slice holds entry j of
+// each of its 64 rows, stored contiguously (slot-major), so the slot's loads
+// are one coalesced 64-lane access. Slice s starts at slice_ptr[s] and has
+// (slice_ptr[s+1] - slice_ptr[s]) / 64 slots = its longest row. Rows keep
+// their CSR entry order, and each lane sums its own row sequentially in the
+// accumulator type (f64 for f32 data), so no cross-lane reduction and no LDS
+// are needed.
+//
+// What it buys over the row-block stream kernel: on matrices whose
+// neighbouring rows have neighbouring columns (a stencil's slot j of rows
+// r..r+63 gathers x[r + offset_j .. r + 63 + offset_j]) the x gather becomes
+// as coalesced as the A stream, which takes most of the per-CU address work
+// off the gather.  Slots past a row's length are padding: never loaded,
+// never multiplied (an inf / nan in x cannot leak in through 0 * x).
+//
+// Reference path replaced: the per-row SpMV kernels behind
+// _triton_spmv_csr_impl_prepared (spmv_csr.py:166-227, 679-723); the format
+// is this build's own prepared copy, like the fp64 value copy the
+// reference's prepare caches (spmv_csr.py:124-130).
+#include "fs_common.hpp"
+
+#include <cstdlib>
+#include <type_traits>
+
+namespace fs {
+
+__device__ inline int64_t ceil_div_d(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <class T>
+struct type_tag {
+  using type = T;
+};
+
+constexpr int kSellRows = 64;  // rows per slice = wave width
+constexpr int kXcdsSell = 8;   // MI355X: workgroup w runs on XCD w % 8
+
+// slots[s] = longest row of slice s.
+template <class P>
+__global__ __launch_bounds__(256) void sell_slots_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                                         int64_t n_slices, int64_t* __restrict__ slots) {
+  const int lane = threadIdx.x & 63;
+  const int64_t slice = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (slice >= n_slices) return;  // whole wave
+  const int64_t r = slice * kSellRows + lane;
+  int64_t len = r < n_rows ? (int64_t)rowptr[r + 1] - (int64_t)rowptr[r] : 0;
+  for (int off = 32; off > 0; off >>= 1) {
+    const int64_t o = (int64_t)__shfl_xor((long long)len, off);
+    len = o > len ? o : len;
+  }
+  if (lane == 0) slots[slice] = len;
+}
+
+// One thread per row: entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64
+// (lanes of a wave write the same slot: coalesced stores).
+template <class V, class I, class P, class SI>
+__global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
+                                                        const P* __restrict__ rowptr, int64_t n_rows,
+                                                        const int64_t* __restrict__ slice_ptr,
+                                                        V* __restrict__ sell_vals, SI* __restrict__ sell_cols) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  const int64_t s = (int64_t)rowptr[r];
+  const int64_t e = (int64_t)rowptr[r + 1];
+  const int64_t dst = slice_ptr[r / kSellRows] + (r % kSellRows);
+  for (int64_t k = 0; k < e - s; ++k) {
+    sell_vals[dst + k * kSellRows] = vals[s + k];
+    sell_cols[dst + k * kSellRows] = (SI)cols[s + k];
+  }
+}
+
+// One wave per slice, lane = row.  Row lengths come from the CSR row
+// pointer; the loop runs to the slice's slot count with every slot past a
+// lane's own length masked off.
+// U slots are loaded before any is used.  With remap, XCD k takes the k-th
+// eighth of the slices in order (workgroup w -> XCD w % 8), so the rows one
+// XCD works on are contiguous and share their x window in its L2.
+template <class V, class I, class P, int U>
+__global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ sell_vals,
+                                                        const I* __restrict__ sell_cols,
+                                                        const int64_t* __restrict__ slice_ptr,
+                                                        const P* __restrict__ rowptr, const V* __restrict__ x,
+                                                        V* __restrict__ y, int64_t n_rows, int64_t n_slices,
+                                                        int remap) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  const int lane = threadIdx.x & 63;
+  int64_t blk = blockIdx.x;
+  if (remap) {
+    const int64_t per = (ceil_div_d(n_slices, 4) + kXcdsSell - 1) / kXcdsSell;
+    blk = (int64_t)(blockIdx.x % kXcdsSell) * per + blockIdx.x / kXcdsSell;
+  }
+  const int64_t slice = blk * 4 + (threadIdx.x >> 6);
+  if (slice >= n_slices) return;  // whole wave
+  const int64_t r = slice * kSellRows + lane;
+  const int len = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
+  const int64_t base = slice_ptr[slice];
+  const int slots = (int)((slice_ptr[slice + 1] - base) / kSellRows);
+  const V* pv = sell_vals + base + lane;
+  const I* pc = sell_cols + base + lane;
+  A acc = T::zero();
+  for (int j = 0; j < slots; j += U) {
+    V v[U];
+    I c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      c[u] = 0;
+      if (j + u < len) {
+        v[u] = load_stream(pv + (int64_t)(j + u) * kSellRows);
+        c[u] = __builtin_nontemporal_load(pc + (int64_t)(j + u) * kSellRows);
+      }
+    }
+    V xv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j + u < len) xv[u] = x[c[u]];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j + u < len) acc = T::fma(v[u], xv[u], acc);
+  }
+  if (r < n_rows) store_stream(y + r, T::out(acc));
+}
+
+template <class P>
+int sell_slots_p(const void* indptr, int64_t n_rows, int64_t* slots, hipStream_t s) {
+  const int64_t n_slices = ceil_div(n_rows, kSellRows);
+  hipLaunchKernelGGL((sell_slots_kernel<P>), dim3((unsigned)ceil_div(n_slices, 4)), dim3(256), 0, s,
+                     static_cast<const P*>(indptr), n_rows, n_slices, slots);
+  FS_CHECK_LAUNCH("sell_slots_kernel");
+  return FS_OK;
+}
+
+template <class V, class I, class P>
+int sell_fill_t(int sidx_t, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
+                const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) {
+  const dim3 g((unsigned)ceil_div(n_rows, 256));
+  if (sidx_t == FS_I32)
+    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int32_t>), g, dim3(256), 0, s, static_cast<const V*>(vals),
+                       static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
+                       static_cast<V*>(sv), static_cast<int32_t*>(sc));
+  else
+    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int64_t>), g, dim3(256), 0, s, static_cast<const V*>(vals),
+                       static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
+                       static_cast<V*>(sv), static_cast<int64_t*>(sc));
+  FS_CHECK_LAUNCH("sell_fill_kernel");
+  return FS_OK;
+}
+
+inline int env_int(const char* name, int dflt) {
+  if (const char* e = std::getenv(name)) return std::atoi(e);
+  return dflt;
+}
+
+template <class V, class I, class P>
+int spmv_sell_t(int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr, const void* indptr,
+                const void* x, void* y, hipStream_t s) {
+  const int64_t n_slices = ceil_div(n_rows, kSellRows);
+  const int64_t blocks = ceil_div(n_slices, 4);
+  const int remap = env_int("FLAGSPARSE_SELL_REMAP", 0) != 0;
+  const int64_t grid = remap ? ceil_div(blocks, kXcdsSell) * kXcdsSell : blocks;
+  // 16 slots in flight for 4-byte values (stencil f32: 0.086 against 0.090 ms
+  // with 8), 8 for 8-byte ones (f64: equal to 4, 16 is 8% slower), 4 for
+  // 16-byte complex values (register budget)
+  const int u = env_int("FLAGSPARSE_SELL_U", sizeof(V) <= 4 ? 16 : (sizeof(V) <= 8 ? 8 : 4));
+  auto go = [&](auto uc) {
+    hipLaunchKernelGGL((spmv_sell_kernel<V, I, P, decltype(uc)::value>), dim3((unsigned)grid), dim3(256), 0, s,
+                       static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
+                       static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y), n_rows,
+                       n_slices, remap);
+  };
+  if (u <= 4) go(std::integral_constant<int, 4>{});
+  else if (u <= 8) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, 16>{});
+  FS_CHECK_LAUNCH("spmv_sell_kernel");
+  return FS_OK;
+}
+
+// Type dispatch: F is a functor template taking <V, I, P>.
+template <template <class, class, class> class F, class... Args>
+int dispatch_vip(int val_t, int idx_t, int ptr_t, Args... args) {
+  auto by_ptr = [&](auto vtag, auto itag) -> int {
+    using V = typename decltype(vtag)::type;
+    using I = typename decltype(itag)::type;
+    if (ptr_t == FS_I32) return F<V, I, int32_t>()(args...);
+    return F<V, I, int64_t>()(args...);
+  };
+  auto by_idx = [&](auto vtag) -> int {
+    if (idx_t == FS_I32) return by_ptr(vtag, type_tag<int32_t>{});
+    return by_ptr(vtag, type_tag<int64_t>{});
+  };
+  switch (val_t) {
+    case FS_F32: return by_idx(type_tag<float>{});
+    case FS_F64: return by_idx(type_tag<double>{});
+    case FS_C64: return by_idx(type_tag<c32>{});
+    default: return by_idx(type_tag<c64>{});
+  }
+}
+
+template <class V, class I, class P>
+struct FillF {
+  int operator()(int sidx_t, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
+                 const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) const {
+    return sell_fill_t<V, I, P>(sidx_t, n_rows, vals, cols, indptr, slice_ptr, sv, sc, s);
+  }
+};
+
+template <class V, class I, class P>
+struct SpmvF {
+  int operator()(int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr, const void* indptr,
+                 const void* x, void* y, hipStream_t s) const {
+    return spmv_sell_t<V, I, P>(n_rows, sv, sc, slice_ptr, indptr, x, y, s);
+  }
+};
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" int fs_sell_slots(int ptr_t, int64_t n_rows, const void* indptr, int64_t* slots_dev, hipStream_t stream) {
+  if (!(ptr_t == FS_I32 || ptr_t == FS_I64)) return fail(FS_E_INVALID, "fs_sell_slots: bad type code");
+  if (n_rows < 0) return fail(FS_E_INVALID, "fs_sell_slots: negative size");
+  if (n_rows == 0) return FS_OK;
+  if (!indptr || !slots_dev) return fail(FS_E_INVALID, "fs_sell_slots: null pointer");
+  if (ptr_t == FS_I32) return sell_slots_p<int32_t>(indptr, n_rows, slots_dev, stream);
+  return sell_slots_p<int64_t>(indptr, n_rows, slots_dev, stream);
+}
+
+extern "C" int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t, int64_t n_rows, const void* vals,
+                              const void* cols, const void* indptr, const int64_t* slice_ptr, void* sell_vals,
+                              void* sell_cols, hipStream_t stream) {
+  if (!valid_types(val_t, idx_t, ptr_t) || !(sell_idx_t == FS_I32 || sell_idx_t == FS_I64))
+    return fail(FS_E_INVALID, "fs_csr_to_sell: bad type code");
+  if (n_rows < 0) return fail(FS_E_INVALID, "fs_csr_to_sell: negative size");
+  if (n_rows == 0) return FS_OK;
+  if (!indptr || !slice_ptr) return fail(FS_E_INVALID, "fs_csr_to_sell: null pointer");
+  return dispatch_vip<FillF>(val_t, idx_t, ptr_t, sell_idx_t, n_rows, vals, cols, indptr, slice_ptr, sell_vals,
+                             sell_cols, stream);
+}
+
+extern "C" int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int64_t n_rows, const void* sell_vals,
+                            const void* sell_cols, const int64_t* slice_ptr, const void* indptr, const void* x,
+                            void* y, hipStream_t stream) {
+  if (!valid_types(val_t, sell_idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_spmv_sell: bad type code");
+  if (n_rows < 0) return fail(FS_E_INVALID, "fs_spmv_sell: negative size");
+  if (n_rows == 0) return FS_OK;
+  if (!indptr || !slice_ptr || !y) return fail(FS_E_INVALID, "fs_spmv_sell: null pointer");
+  return dispatch_vip<SpmvF>(val_t, sell_idx_t, ptr_t, n_rows, sell_vals, sell_cols, slice_ptr, indptr, x, y,
+                             stream);
+}

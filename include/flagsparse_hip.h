@@ -218,6 +218,39 @@ int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
                        void* y, const void* part_dev, void* ws,
                        size_t ws_bytes, hipStream_t stream);
 
+/* ---- Sliced-ELL copy (SELL-64) of a prepared CSR matrix ------------------
+ * No counterpart call in the reference: like the column panels it is a
+ * per-matrix copy that prepare_spmv_csr (spmv_csr.py:591-676) may build,
+ * and fs_spmv_sell then replaces _triton_spmv_csr_impl_prepared
+ * (spmv_csr.py:679-723) for that prepared matrix, with the same result up
+ * to the order of the floating-point additions (each row is summed in its
+ * CSR order).
+ *
+ * Layout: rows are cut into slices of 64 consecutive rows; slice s holds
+ * slots[s] = its longest row slots of 64 entries each, slot-major: entry k
+ * of row r sits at slice_ptr[r / 64] + 64 * k + r % 64.  slice_ptr (device,
+ * int64, n_slices + 1 with n_slices = ceil(n_rows / 64)) is the exclusive
+ * prefix sum of 64 * slots.  Padding slots are never read by fs_spmv_sell.
+ *
+ * fs_sell_slots writes slots[s] (device, int64, n_slices).
+ * fs_csr_to_sell writes the values and the column indices (as sell_idx_t,
+ * which the caller picks wide enough for n_cols - 1) into buffers of
+ * slice_ptr[n_slices] entries.
+ * fs_spmv_sell computes y = A x from the copy; row lengths come from the
+ * CSR indptr (ptr_t).  Rows may hold up to 2^31 - 1 entries.
+ * None of the three synchronises `stream`.
+ */
+int fs_sell_slots(int ptr_t, int64_t n_rows, const void* indptr,
+                  int64_t* slots_dev, hipStream_t stream);
+int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t,
+                   int64_t n_rows, const void* vals, const void* cols,
+                   const void* indptr, const int64_t* slice_ptr,
+                   void* sell_vals, void* sell_cols, hipStream_t stream);
+int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int64_t n_rows,
+                 const void* sell_vals, const void* sell_cols,
+                 const int64_t* slice_ptr, const void* indptr,
+                 const void* x, void* y, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

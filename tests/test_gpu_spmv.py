@@ -31,11 +31,17 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge", "stream", "nnzblock", "panel2", "panel3", "panel8", "panel16"])
+@pytest.fixture(params=["auto", "vector", "merge", "stream", "nnzblock", "sell", "panel2", "panel3", "panel8",
+                        "panel16"])
 def kernel_choice(request, monkeypatch):
-    """Kernel variant under test; panelN = merge path over N column panels."""
+    """Kernel variant under test; panelN = merge path over N column panels;
+    sell = the SELL-64 copy, forced for every matrix."""
     monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
-    if request.param.startswith("panel"):
+    monkeypatch.delenv("FLAGSPARSE_SPMV_SELL", raising=False)
+    if request.param == "sell":
+        monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
+        monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    elif request.param.startswith("panel"):
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
         monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", request.param[len("panel"):])
     elif request.param != "auto":
@@ -47,9 +53,9 @@ def kernel_choice(request, monkeypatch):
 
 def _check_spmv(data, indices, indptr, shape, x, op, kernel=None):
     y = fs.flagsparse_spmv_csr(data, indices, indptr, x, shape, op=op)
-    if kernel is not None and kernel.startswith("panel") and shape[0] > 0:
+    if kernel is not None and (kernel.startswith("panel") or kernel == "sell") and shape[0] > 0:
         prep = fs.prepare_spmv_csr(data, indices, indptr, shape, op=op)
-        assert prep.kernel_name == "panel"
+        assert prep.kernel_name == ("sell" if kernel == "sell" else "panel")
     ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), shape, op=op)
     assert y.dtype == data.dtype
     assert tuple(y.shape) == (ref.shape[0],)
@@ -309,3 +315,86 @@ def test_csr_panelize_layout(device, n_panels):
     assert np.array_equal(np_(pc.indices).astype(np.int64), np.concatenate(exp_c))
     assert np.array_equal(np_(pc.data), np.concatenate(exp_d))
     assert pc.indptr.dtype == indptr.dtype and pc.indices.dtype == indices.dtype
+
+
+def _dropped(data, indices, indptr, shape, frac, seed):
+    """The matrix with a random share `frac` of its entries removed."""
+    g = torch.Generator(device=data.device)
+    g.manual_seed(seed)
+    keep = torch.rand(data.numel(), generator=g, device=data.device) >= frac
+    rows = torch.repeat_interleave(torch.arange(shape[0], device=data.device), indptr[1:] - indptr[:-1])
+    counts = torch.bincount(rows[keep], minlength=shape[0])
+    p = torch.zeros(shape[0] + 1, dtype=indptr.dtype, device=data.device)
+    p[1:] = torch.cumsum(counts, 0)
+    return data[keep].contiguous(), indices[keep].contiguous(), p, shape
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
+def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype):
+    """A prepared 27-point stencil (64^3, 262,144 rows) gets the SELL-64 copy
+    by itself and matches the oracle on sampled rows and the row-block stream
+    kernel to within rounding; one-shot calls keep the CSR kernels."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS"):
+        monkeypatch.delenv(k, raising=False)
+    data, indices, indptr, sh = S.stencil27(64, torch.float64, torch.int32, device, seed=5)
+    if dtype == torch.complex64:
+        imag = S.vector(data.numel(), torch.float64, device, seed=6)
+        data = torch.complex(data, imag).to(torch.complex64)
+    else:
+        data = data.to(dtype)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep.kernel_name == "sell"
+    assert prep._sell.padded <= 1.03 * data.numel()
+    x = S.vector(sh[1], dtype, device, seed=7)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=prep))  # deterministic
+    _, meta = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh, return_meta=True)
+    assert meta["kernel"] != "sell"
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "0")
+    prep0 = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep0.kernel_name != "sell"
+    y0 = fs.flagsparse_spmv_csr(x=x, prepared=prep0)
+    # the same per-row sums in two orders, each rounded once from the wide type
+    tol = REL_TOL[dtype]
+    assert rel_err(np_(y), np_(y0)) <= tol
+    gen = np.random.default_rng(2)
+    rows = sorted(set(gen.integers(0, sh[0], 3000).tolist()) | {0, sh[0] - 1})
+    _sampled_rows_check(data, indices, indptr, sh, x, y, rows, tol)
+
+
+def test_spmv_sell_not_chosen_without_locality_or_with_padding(device, monkeypatch):
+    """Uniformly random columns (no locality) and uneven rows (a stencil with
+    30% of its entries dropped: ~28% padding) keep the CSR kernels."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS"):
+        monkeypatch.delenv(k, raising=False)
+    d, i, p, sh = S.uniform_rows(1 << 18, 1 << 18, 16, torch.float32, torch.int32, device, seed=8)
+    assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell"
+    d, i, p, sh = _dropped(*S.stencil27(64, torch.float64, torch.int32, device, seed=5), 0.3, 9)
+    prep = fs.prepare_spmv_csr(d, i, p, sh)
+    assert prep.kernel_name != "sell"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
+def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype):
+    """Rows of one slice with different lengths: the padding slots of the short
+    rows hold column 0, where x is infinite; only row 0 references column 0,
+    so every other row must stay finite (padding is never loaded)."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    n = 256
+    lengths = torch.tensor([(r % 7) + 1 for r in range(n)], dtype=torch.int64, device=device)
+    lengths[0] = 3
+    indptr = torch.zeros(n + 1, dtype=torch.int32, device=device)
+    indptr[1:] = torch.cumsum(lengths, 0)
+    cols = []
+    for r in range(n):
+        start = 0 if r == 0 else 1 + (r * 13) % (n - 8)
+        cols.extend(range(start, start + int(lengths[r])))
+    indices = torch.tensor(cols, dtype=torch.int32, device=device)
+    data = torch.ones(indices.numel(), dtype=dtype, device=device)
+    x = torch.ones(n, dtype=dtype, device=device)
+    x[0] = float("inf")
+    prep = fs.prepare_spmv_csr(data, indices, indptr, (n, n))
+    assert prep.kernel_name == "sell" and prep._sell.padded > data.numel()
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert torch.isinf(y[0])
+    assert torch.equal(y[1:], lengths[1:].to(dtype))
