@@ -56,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "fs_spmv_panels_workspace_bytes",
     "fs_spmv_csr_panels",
     "fs_sell_slots",
+    "fs_sell_max_offset",
     "fs_csr_to_sell",
     "fs_spmv_sell",
 )
@@ -141,6 +142,8 @@ def _declare(lib):
                                        _vp, _vp, _sz, _vp]
     lib.fs_sell_slots.restype = _i32
     lib.fs_sell_slots.argtypes = [_i32, _i64, _vp, _vp, _vp]
+    lib.fs_sell_max_offset.restype = _i32
+    lib.fs_sell_max_offset.argtypes = [_i32, _i32, _i64, _vp, _vp, _vp, _vp]
     lib.fs_csr_to_sell.restype = _i32
     lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_sell.restype = _i32

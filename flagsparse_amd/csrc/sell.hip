@@ -56,7 +56,9 @@ __global__ __launch_bounds__(256) void sell_slots_kernel(const P* __restrict__ r
 
 // One thread per row: entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64
 // (lanes of a wave write the same slot: coalesced stores).
-template <class V, class I, class P, class SI>
+// With DELTA the column is stored as the 16-bit offset c - r from the row
+// (the caller has checked |c - r| <= 32767 with fs_sell_max_offset).
+template <class V, class I, class P, class SI, bool DELTA>
 __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
                                                         const P* __restrict__ rowptr, int64_t n_rows,
                                                         const int64_t* __restrict__ slice_ptr,
@@ -68,8 +70,29 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
   const int64_t dst = slice_ptr[r / kSellRows] + (r % kSellRows);
   for (int64_t k = 0; k < e - s; ++k) {
     sell_vals[dst + k * kSellRows] = vals[s + k];
-    sell_cols[dst + k * kSellRows] = (SI)cols[s + k];
+    sell_cols[dst + k * kSellRows] = DELTA ? (SI)((int64_t)cols[s + k] - r) : (SI)cols[s + k];
   }
+}
+
+// max over entries of |c - r| (one integer atomic per wave: order independent).
+template <class I, class P>
+__global__ __launch_bounds__(256) void sell_max_offset_kernel(const I* __restrict__ cols, const P* __restrict__ rowptr,
+                                                              int64_t n_rows, unsigned long long* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long m = 0;
+  if (r < n_rows) {
+    const int64_t e = (int64_t)rowptr[r + 1];
+    for (int64_t k = (int64_t)rowptr[r]; k < e; ++k) {
+      const int64_t d = (int64_t)cols[k] - r;
+      const unsigned long long a = (unsigned long long)(d < 0 ? -d : d);
+      m = a > m ? a : m;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(m, off);
+    m = o > m ? o : m;
+  }
+  if ((threadIdx.x & 63) == 0 && m > 0) atomicMax(out, m);
 }
 
 // One wave per slice, lane = row.  Row lengths come from the CSR row
@@ -78,7 +101,7 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
 // U slots are loaded before any is used.  With remap, XCD k takes the k-th
 // eighth of the slices in order (workgroup w -> XCD w % 8), so the rows one
 // XCD works on are contiguous and share their x window in its L2.
-template <class V, class I, class P, int U>
+template <class V, class I, class P, int U, bool DELTA>
 __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ sell_vals,
                                                         const I* __restrict__ sell_cols,
                                                         const int64_t* __restrict__ slice_ptr,
@@ -116,7 +139,7 @@ __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ se
     V xv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (j + u < len) xv[u] = x[c[u]];
+      if (j + u < len) xv[u] = DELTA ? x[r + (int64_t)c[u]] : x[c[u]];
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (j + u < len) acc = T::fma(v[u], xv[u], acc);
@@ -137,12 +160,16 @@ template <class V, class I, class P>
 int sell_fill_t(int sidx_t, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
                 const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) {
   const dim3 g((unsigned)ceil_div(n_rows, 256));
-  if (sidx_t == FS_I32)
-    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int32_t>), g, dim3(256), 0, s, static_cast<const V*>(vals),
+  if (sidx_t == FS_SELL_D16)
+    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int16_t, true>), g, dim3(256), 0, s, static_cast<const V*>(vals),
+                       static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
+                       static_cast<V*>(sv), static_cast<int16_t*>(sc));
+  else if (sidx_t == FS_SELL_I32)
+    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int32_t, false>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
                        static_cast<V*>(sv), static_cast<int32_t*>(sc));
   else
-    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int64_t>), g, dim3(256), 0, s, static_cast<const V*>(vals),
+    hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int64_t, false>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
                        static_cast<V*>(sv), static_cast<int64_t*>(sc));
   FS_CHECK_LAUNCH("sell_fill_kernel");
@@ -154,19 +181,19 @@ inline int env_int(const char* name, int dflt) {
   return dflt;
 }
 
-template <class V, class I, class P>
+template <class V, class I, class P, bool DELTA>
 int spmv_sell_t(int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr, const void* indptr,
                 const void* x, void* y, hipStream_t s) {
   const int64_t n_slices = ceil_div(n_rows, kSellRows);
   const int64_t blocks = ceil_div(n_slices, 4);
   const int remap = env_int("FLAGSPARSE_SELL_REMAP", 0) != 0;
   const int64_t grid = remap ? ceil_div(blocks, kXcdsSell) * kXcdsSell : blocks;
-  // 16 slots in flight for 4-byte values (stencil f32: 0.086 against 0.090 ms
-  // with 8), 8 for 8-byte ones (f64: equal to 4, 16 is 8% slower), 4 for
-  // 16-byte complex values (register budget)
-  const int u = env_int("FLAGSPARSE_SELL_U", sizeof(V) <= 4 ? 16 : (sizeof(V) <= 8 ? 8 : 4));
+  // Slots in flight: 16 for 4-byte values (27-point stencil f32: 0.0858 ms,
+  // against 0.0877 with 8 and 0.0925 with 4), 4 for wider ones (f64 with
+  // 16-bit column offsets: 0.1138 ms, against 0.1164 with 8 and 0.1446 with 16)
+  const int u = env_int("FLAGSPARSE_SELL_U", sizeof(V) <= 4 ? 16 : 4);
   auto go = [&](auto uc) {
-    hipLaunchKernelGGL((spmv_sell_kernel<V, I, P, decltype(uc)::value>), dim3((unsigned)grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((spmv_sell_kernel<V, I, P, decltype(uc)::value, DELTA>), dim3((unsigned)grid), dim3(256), 0, s,
                        static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
                        static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y), n_rows,
                        n_slices, remap);
@@ -188,6 +215,7 @@ int dispatch_vip(int val_t, int idx_t, int ptr_t, Args... args) {
     return F<V, I, int64_t>()(args...);
   };
   auto by_idx = [&](auto vtag) -> int {
+    if (idx_t == FS_SELL_D16) return by_ptr(vtag, type_tag<int16_t>{});
     if (idx_t == FS_I32) return by_ptr(vtag, type_tag<int32_t>{});
     return by_ptr(vtag, type_tag<int64_t>{});
   };
@@ -211,7 +239,7 @@ template <class V, class I, class P>
 struct SpmvF {
   int operator()(int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr, const void* indptr,
                  const void* x, void* y, hipStream_t s) const {
-    return spmv_sell_t<V, I, P>(n_rows, sv, sc, slice_ptr, indptr, x, y, s);
+    return spmv_sell_t<V, I, P, std::is_same<I, int16_t>::value>(n_rows, sv, sc, slice_ptr, indptr, x, y, s);
   }
 };
 
@@ -228,10 +256,34 @@ extern "C" int fs_sell_slots(int ptr_t, int64_t n_rows, const void* indptr, int6
   return sell_slots_p<int64_t>(indptr, n_rows, slots_dev, stream);
 }
 
+extern "C" int fs_sell_max_offset(int idx_t, int ptr_t, int64_t n_rows, const void* cols, const void* indptr,
+                                  unsigned long long* max_dev, hipStream_t stream) {
+  if (!valid_types(FS_F32, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_sell_max_offset: bad type code");
+  if (n_rows < 0) return fail(FS_E_INVALID, "fs_sell_max_offset: negative size");
+  if (n_rows == 0) return FS_OK;
+  if (!cols || !indptr || !max_dev) return fail(FS_E_INVALID, "fs_sell_max_offset: null pointer");
+  const dim3 g((unsigned)ceil_div(n_rows, 256));
+  if (idx_t == FS_I32 && ptr_t == FS_I32)
+    hipLaunchKernelGGL((sell_max_offset_kernel<int32_t, int32_t>), g, dim3(256), 0, stream,
+                       static_cast<const int32_t*>(cols), static_cast<const int32_t*>(indptr), n_rows, max_dev);
+  else if (idx_t == FS_I32)
+    hipLaunchKernelGGL((sell_max_offset_kernel<int32_t, int64_t>), g, dim3(256), 0, stream,
+                       static_cast<const int32_t*>(cols), static_cast<const int64_t*>(indptr), n_rows, max_dev);
+  else if (ptr_t == FS_I32)
+    hipLaunchKernelGGL((sell_max_offset_kernel<int64_t, int32_t>), g, dim3(256), 0, stream,
+                       static_cast<const int64_t*>(cols), static_cast<const int32_t*>(indptr), n_rows, max_dev);
+  else
+    hipLaunchKernelGGL((sell_max_offset_kernel<int64_t, int64_t>), g, dim3(256), 0, stream,
+                       static_cast<const int64_t*>(cols), static_cast<const int64_t*>(indptr), n_rows, max_dev);
+  FS_CHECK_LAUNCH("sell_max_offset_kernel");
+  return FS_OK;
+}
+
 extern "C" int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t, int64_t n_rows, const void* vals,
                               const void* cols, const void* indptr, const int64_t* slice_ptr, void* sell_vals,
                               void* sell_cols, hipStream_t stream) {
-  if (!valid_types(val_t, idx_t, ptr_t) || !(sell_idx_t == FS_I32 || sell_idx_t == FS_I64))
+  if (!valid_types(val_t, idx_t, ptr_t) ||
+      !(sell_idx_t == FS_SELL_I32 || sell_idx_t == FS_SELL_I64 || sell_idx_t == FS_SELL_D16))
     return fail(FS_E_INVALID, "fs_csr_to_sell: bad type code");
   if (n_rows < 0) return fail(FS_E_INVALID, "fs_csr_to_sell: negative size");
   if (n_rows == 0) return FS_OK;
@@ -243,7 +295,8 @@ extern "C" int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t, i
 extern "C" int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int64_t n_rows, const void* sell_vals,
                             const void* sell_cols, const int64_t* slice_ptr, const void* indptr, const void* x,
                             void* y, hipStream_t stream) {
-  if (!valid_types(val_t, sell_idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_spmv_sell: bad type code");
+  if (!valid_types(val_t, sell_idx_t == FS_SELL_D16 ? FS_I32 : sell_idx_t, ptr_t))
+    return fail(FS_E_INVALID, "fs_spmv_sell: bad type code");
   if (n_rows < 0) return fail(FS_E_INVALID, "fs_spmv_sell: negative size");
   if (n_rows == 0) return FS_OK;
   if (!indptr || !slice_ptr || !y) return fail(FS_E_INVALID, "fs_spmv_sell: null pointer");

@@ -369,13 +369,33 @@ def _sell_slice_ptr(indptr, n_rows):
     return slice_ptr
 
 
+_SELL_I32, _SELL_I64, _SELL_D16 = 0, 1, 2  # enum fs_sell_index
+
+
+def _sell_max_offset(indices, indptr, n_rows):
+    """max |c - r| over the entries (one device->host sync)."""
+    if indices.numel() == 0:
+        return 0
+    out = torch.zeros(1, dtype=torch.int64, device=indices.device)
+    _lib.check(
+        _lib.lib().fs_sell_max_offset(
+            _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype), n_rows, _lib.ptr(indices),
+            _lib.ptr(indptr), _lib.ptr(out), _lib.stream_handle(indices.device),
+        ),
+        "fs_sell_max_offset",
+    )
+    return int(out.item())
+
+
 class SellCsr:
     """A as SELL-64: slices of 64 consecutive rows, slot-major, built once per
-    prepared matrix (fs_sell_slots, fs_csr_to_sell).  Column indices are
-    stored as int32 whenever n_cols - 1 fits; the CSR row pointer of the
-    prepared matrix still supplies the row lengths."""
+    prepared matrix (fs_sell_slots, fs_csr_to_sell).  Columns are stored as
+    the int16 offset c - r from the row when every |c - r| <= 32767 (banded
+    matrices such as stencils: 2 bytes per entry instead of 4; off with
+    FLAGSPARSE_SELL_DELTA=0), else as int32 when n_cols - 1 fits, else int64.
+    The CSR row pointer of the prepared matrix supplies the row lengths."""
 
-    __slots__ = ("vals", "cols", "slice_ptr", "indptr", "n_rows", "padded")
+    __slots__ = ("vals", "cols", "col_code", "slice_ptr", "indptr", "n_rows", "padded")
 
     def __init__(self, data, indices, indptr, n_cols, slice_ptr):
         device = data.device
@@ -387,12 +407,17 @@ class SellCsr:
         self.indptr = indptr
         self.n_rows = n_rows
         self.vals = torch.zeros(self.padded, dtype=data.dtype, device=device)
-        col_dtype = torch.int32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else torch.int64
+        if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0" and _sell_max_offset(indices, indptr, n_rows) <= 32767:
+            col_dtype, self.col_code = torch.int16, _SELL_D16
+        elif n_cols - 1 <= _INDEX_LIMIT_INT32:
+            col_dtype, self.col_code = torch.int32, _SELL_I32
+        else:
+            col_dtype, self.col_code = torch.int64, _SELL_I64
         self.cols = torch.zeros(self.padded, dtype=col_dtype, device=device)
         _lib.check(
             lib.fs_csr_to_sell(
                 _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype),
-                _lib.index_code(col_dtype), n_rows, _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr),
+                self.col_code, n_rows, _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr),
                 _lib.ptr(self.slice_ptr), _lib.ptr(self.vals), _lib.ptr(self.cols), stream,
             ),
             "fs_csr_to_sell",
@@ -401,7 +426,7 @@ class SellCsr:
     def spmv(self, x, y):
         _lib.check(
             _lib.lib().fs_spmv_sell(
-                _lib.value_code(self.vals.dtype), _lib.index_code(self.cols.dtype), _lib.index_code(self.indptr.dtype),
+                _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype),
                 self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols), _lib.ptr(self.slice_ptr), _lib.ptr(self.indptr),
                 _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(self.vals.device),
             ),

@@ -37,6 +37,9 @@ extern "C" {
 enum fs_value_type { FS_F32 = 0, FS_F64 = 1, FS_C64 = 2, FS_C128 = 3 };
 /* Index types: SUPPORTED_INDEX_DTYPES (_common.py:29). */
 enum fs_index_type { FS_I32 = 0, FS_I64 = 1 };
+/* Column storage of a SELL-64 copy: absolute int32 / int64, or the int16
+ * offset c - r from the entry's row (banded matrices, |c - r| <= 32767). */
+enum fs_sell_index { FS_SELL_I32 = 0, FS_SELL_I64 = 1, FS_SELL_D16 = 2 };
 
 enum fs_status {
   FS_OK = 0,
@@ -233,15 +236,21 @@ int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
  * prefix sum of 64 * slots.  Padding slots are never read by fs_spmv_sell.
  *
  * fs_sell_slots writes slots[s] (device, int64, n_slices).
- * fs_csr_to_sell writes the values and the column indices (as sell_idx_t,
- * which the caller picks wide enough for n_cols - 1) into buffers of
- * slice_ptr[n_slices] entries.
+ * fs_sell_max_offset raises *max_dev (device, caller-initialised to 0) to
+ * the largest |c - r| over the entries (c = column, r = row).
+ * fs_csr_to_sell writes the values and the columns into buffers of
+ * slice_ptr[n_slices] entries, as sell_idx_t: FS_SELL_I32 / FS_SELL_I64
+ * (absolute, wide enough for n_cols - 1) or FS_SELL_D16 (int16 c - r; the
+ * caller has checked fs_sell_max_offset <= 32767).
  * fs_spmv_sell computes y = A x from the copy; row lengths come from the
  * CSR indptr (ptr_t).  Rows may hold up to 2^31 - 1 entries.
  * None of the three synchronises `stream`.
  */
 int fs_sell_slots(int ptr_t, int64_t n_rows, const void* indptr,
                   int64_t* slots_dev, hipStream_t stream);
+int fs_sell_max_offset(int idx_t, int ptr_t, int64_t n_rows, const void* cols,
+                       const void* indptr, unsigned long long* max_dev,
+                       hipStream_t stream);
 int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t,
                    int64_t n_rows, const void* vals, const void* cols,
                    const void* indptr, const int64_t* slice_ptr,

@@ -329,13 +329,15 @@ def _dropped(data, indices, indptr, shape, frac, seed):
     return data[keep].contiguous(), indices[keep].contiguous(), p, shape
 
 
+@pytest.mark.parametrize("delta", ["1", "0"], ids=["int16-offsets", "int32-columns"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
-def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype):
+def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, delta):
     """A prepared 27-point stencil (64^3, 262,144 rows) gets the SELL-64 copy
     by itself and matches the oracle on sampled rows and the row-block stream
     kernel to within rounding; one-shot calls keep the CSR kernels."""
     for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS"):
         monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("FLAGSPARSE_SELL_DELTA", delta)
     data, indices, indptr, sh = S.stencil27(64, torch.float64, torch.int32, device, seed=5)
     if dtype == torch.complex64:
         imag = S.vector(data.numel(), torch.float64, device, seed=6)
@@ -345,6 +347,7 @@ def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype):
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
     assert prep.kernel_name == "sell"
     assert prep._sell.padded <= 1.03 * data.numel()
+    assert prep._sell.cols.dtype == (torch.int16 if delta == "1" else torch.int32)
     x = S.vector(sh[1], dtype, device, seed=7)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=prep))  # deterministic
@@ -398,3 +401,25 @@ def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype):
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert torch.isinf(y[0])
     assert torch.equal(y[1:], lengths[1:].to(dtype))
+
+
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64], ids=["int32", "int64"])
+def test_spmv_sell_wide_offsets_keep_absolute_columns(device, monkeypatch, index_dtype):
+    """Forced SELL on a matrix with an entry 70,000 columns from its row: the
+    int16 offset would overflow, so the copy stores absolute int32 columns
+    and still matches the oracle."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    monkeypatch.delenv("FLAGSPARSE_SELL_DELTA", raising=False)
+    n_rows, n_cols = 1000, 80000
+    data, indices, indptr, sh = S.random_csr(n_rows, n_cols, 8.0 / n_cols, torch.float64, index_dtype, device,
+                                             seed=12)
+    # make row 0's last entry column 70,000 (row 0 is non-empty with high probability; force it)
+    assert int(indptr[1]) > 0
+    indices = indices.clone()
+    indices[int(indptr[1]) - 1] = 70000
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep.kernel_name == "sell" and prep._sell.cols.dtype == torch.int32
+    x = S.vector(n_cols, torch.float64, device, seed=13)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
+    assert rel_err(np_(y), ref) <= REL_TOL[torch.float64]
