@@ -169,20 +169,30 @@ class PreparedCsrSpmv:
                 data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols
             )
             p = self._plan.plan
+            # The SELL and panel copies are optional: when device memory cannot
+            # hold one next to the caller's matrix, the CSR kernels run instead.
             if _spmv_use_sell(p, self.kernel_indices, self.kernel_indptr, self._one_shot):
-                slice_ptr = _sell_slice_ptr(self.kernel_indptr, self.n_rows)
-                padded = int(slice_ptr[-1])
-                if padded <= _SELL_MAX_PADDING * max(1, int(p.nnz)) or _sell_forced():
-                    self._sell = SellCsr(data, self.kernel_indices, self.kernel_indptr, self.n_cols, slice_ptr)
+                try:
+                    slice_ptr = _sell_slice_ptr(self.kernel_indptr, self.n_rows)
+                    padded = int(slice_ptr[-1])
+                    if padded <= _SELL_MAX_PADDING * max(1, int(p.nnz)) or _sell_forced():
+                        self._sell = SellCsr(data, self.kernel_indices, self.kernel_indptr, self.n_cols, slice_ptr)
+                except torch.OutOfMemoryError:
+                    self._sell = None
+                    torch.cuda.empty_cache()
             if self._sell is not None:
                 return self._plan  # the copy needs no partition or carry
             if p.kernel == _lib.FS_KERNEL_MERGE:
                 n_panels = _spmv_panel_count(p, data.dtype, self._one_shot)
                 if n_panels > 1:
-                    self._panels = PanelledCsr(
-                        data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols, n_panels
-                    )
-                else:
+                    try:
+                        self._panels = PanelledCsr(
+                            data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols, n_panels
+                        )
+                    except torch.OutOfMemoryError:
+                        self._panels = None
+                        torch.cuda.empty_cache()
+                if self._panels is None:
                     self._part = self._plan.partition(self.kernel_indptr, int(p.tile_items))
                     self._carry = _lib.workspace(p.carry_bytes, data.device)
             elif p.kernel == _lib.FS_KERNEL_NNZBLOCK:

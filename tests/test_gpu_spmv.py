@@ -423,3 +423,30 @@ def test_spmv_sell_wide_offsets_keep_absolute_columns(device, monkeypatch, index
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
     assert rel_err(np_(y), ref) <= REL_TOL[torch.float64]
+
+
+@pytest.mark.parametrize("copy", ["sell", "panel"])
+def test_spmv_copy_out_of_memory_falls_back_to_csr(device, monkeypatch, copy):
+    """When the optional SELL / panel copy cannot be allocated, prepare keeps
+    the CSR kernels and the result is still correct."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS"):
+        monkeypatch.delenv(k, raising=False)
+
+    def no_memory(*args, **kwargs):
+        raise torch.OutOfMemoryError("injected")
+
+    if copy == "sell":
+        monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+        monkeypatch.setattr(spmv_mod.SellCsr, "__init__", no_memory)
+        data, indices, indptr, sh = S.stencil27(16, torch.float64, torch.int32, device, seed=3)
+    else:
+        monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
+        monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", "4")
+        monkeypatch.setattr(spmv_mod.PanelledCsr, "__init__", no_memory)
+        data, indices, indptr, sh = S.random_csr(500, 700, 0.02, torch.float64, torch.int32, device, seed=3)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep.kernel_name not in ("sell", "panel")
+    x = S.vector(sh[1], torch.float64, device, seed=4)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
+    assert rel_err(np_(y), ref) <= REL_TOL[torch.float64]
