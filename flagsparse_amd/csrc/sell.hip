@@ -54,8 +54,35 @@ __global__ __launch_bounds__(256) void sell_slots_kernel(const P* __restrict__ r
   if (lane == 0) slots[slice] = len;
 }
 
-// One thread per row: entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64
-// (lanes of a wave write the same slot: coalesced stores).
+// Entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64.
+// Build kernels: one wave per slice.  A slice's entries are contiguous in
+// the CSR arrays, so the wave reads them with unit stride; each entry's row
+// inside the slice comes from a binary search over the slice's 65 row
+// pointers in LDS.  Writes stay inside the slice's region of the copy.
+__device__ inline int sell_local_row(const int64_t* ptr, int64_t e) {
+  int lo = 0, hi = kSellRows - 1;  // last local row whose start <= e
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (ptr[mid] <= e)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// Loads the 65 row pointers of slice `slice` (rows past n_rows repeat the end).
+template <class P>
+__device__ inline void sell_load_ptr(const P* __restrict__ rowptr, int64_t n_rows, int64_t slice, int lane,
+                                     int64_t* ptr) {
+  const int64_t r = slice * kSellRows + lane;
+  ptr[lane] = (int64_t)rowptr[r < n_rows ? r : n_rows];
+  if (lane == 0) {
+    const int64_t r_end = slice * kSellRows + kSellRows;
+    ptr[kSellRows] = (int64_t)rowptr[r_end < n_rows ? r_end : n_rows];
+  }
+}
+
 // With DELTA the column is stored as the 16-bit offset c - r from the row
 // (the caller has checked |c - r| <= 32767 with fs_sell_max_offset).
 template <class V, class I, class P, class SI, bool DELTA>
@@ -63,14 +90,25 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
                                                         const P* __restrict__ rowptr, int64_t n_rows,
                                                         const int64_t* __restrict__ slice_ptr,
                                                         V* __restrict__ sell_vals, SI* __restrict__ sell_cols) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= n_rows) return;
-  const int64_t s = (int64_t)rowptr[r];
-  const int64_t e = (int64_t)rowptr[r + 1];
-  const int64_t dst = slice_ptr[r / kSellRows] + (r % kSellRows);
-  for (int64_t k = 0; k < e - s; ++k) {
-    sell_vals[dst + k * kSellRows] = vals[s + k];
-    sell_cols[dst + k * kSellRows] = DELTA ? (SI)((int64_t)cols[s + k] - r) : (SI)cols[s + k];
+  __shared__ int64_t s_ptr[4][kSellRows + 1];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t n_slices = (n_rows + kSellRows - 1) / kSellRows;
+  const int64_t slice = (int64_t)blockIdx.x * 4 + w;
+  if (slice >= n_slices) return;  // whole wave; no block barrier below
+  int64_t* ptr = s_ptr[w];
+  sell_load_ptr(rowptr, n_rows, slice, lane, ptr);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int64_t base = slice_ptr[slice];
+  const int64_t row0 = slice * kSellRows;
+  for (int64_t e = ptr[0] + lane; e < ptr[kSellRows]; e += kSellRows) {
+    const int lr = sell_local_row(ptr, e);
+    const int64_t dst = base + (e - ptr[lr]) * kSellRows + lr;
+    sell_vals[dst] = vals[e];
+    const I c = cols[e];
+    sell_cols[dst] = DELTA ? (SI)((int64_t)c - (row0 + lr)) : (SI)c;
   }
 }
 
@@ -78,21 +116,29 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
 template <class I, class P>
 __global__ __launch_bounds__(256) void sell_max_offset_kernel(const I* __restrict__ cols, const P* __restrict__ rowptr,
                                                               int64_t n_rows, unsigned long long* __restrict__ out) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ int64_t s_ptr[4][kSellRows + 1];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t n_slices = (n_rows + kSellRows - 1) / kSellRows;
+  const int64_t slice = (int64_t)blockIdx.x * 4 + w;
+  if (slice >= n_slices) return;  // whole wave
+  int64_t* ptr = s_ptr[w];
+  sell_load_ptr(rowptr, n_rows, slice, lane, ptr);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int64_t row0 = slice * kSellRows;
   unsigned long long m = 0;
-  if (r < n_rows) {
-    const int64_t e = (int64_t)rowptr[r + 1];
-    for (int64_t k = (int64_t)rowptr[r]; k < e; ++k) {
-      const int64_t d = (int64_t)cols[k] - r;
-      const unsigned long long a = (unsigned long long)(d < 0 ? -d : d);
-      m = a > m ? a : m;
-    }
+  for (int64_t e = ptr[0] + lane; e < ptr[kSellRows]; e += kSellRows) {
+    const int64_t d = (int64_t)cols[e] - (row0 + sell_local_row(ptr, e));
+    const unsigned long long a = (unsigned long long)(d < 0 ? -d : d);
+    m = a > m ? a : m;
   }
   for (int off = 32; off > 0; off >>= 1) {
     const unsigned long long o = __shfl_xor(m, off);
     m = o > m ? o : m;
   }
-  if ((threadIdx.x & 63) == 0 && m > 0) atomicMax(out, m);
+  if (lane == 0 && m > 0) atomicMax(out, m);
 }
 
 // One wave per slice, lane = row.  Row lengths come from the CSR row
@@ -159,7 +205,7 @@ int sell_slots_p(const void* indptr, int64_t n_rows, int64_t* slots, hipStream_t
 template <class V, class I, class P>
 int sell_fill_t(int sidx_t, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
                 const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) {
-  const dim3 g((unsigned)ceil_div(n_rows, 256));
+  const dim3 g((unsigned)ceil_div(ceil_div(n_rows, kSellRows), 4));
   if (sidx_t == FS_SELL_D16)
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int16_t, true>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
@@ -262,7 +308,7 @@ extern "C" int fs_sell_max_offset(int idx_t, int ptr_t, int64_t n_rows, const vo
   if (n_rows < 0) return fail(FS_E_INVALID, "fs_sell_max_offset: negative size");
   if (n_rows == 0) return FS_OK;
   if (!cols || !indptr || !max_dev) return fail(FS_E_INVALID, "fs_sell_max_offset: null pointer");
-  const dim3 g((unsigned)ceil_div(n_rows, 256));
+  const dim3 g((unsigned)ceil_div(ceil_div(n_rows, kSellRows), 4));
   if (idx_t == FS_I32 && ptr_t == FS_I32)
     hipLaunchKernelGGL((sell_max_offset_kernel<int32_t, int32_t>), g, dim3(256), 0, stream,
                        static_cast<const int32_t*>(cols), static_cast<const int32_t*>(indptr), n_rows, max_dev);
