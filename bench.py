@@ -55,7 +55,7 @@ MEASURED_TRAFFIC = {
     "c3_spmv_powerlaw4M_f32_i32": 2440.0e6,
     "c3_spmv_powerlaw4M_f32_i64": 2440.4e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
-    "c4_spmm_uniform1M_f32_i32_n64_trans": 9184.5e6,
+    "c4_spmm_uniform1M_f32_i32_n64_trans": 9184.6e6,
     "c5_spmm_rmat21_f32_i64_n256_non": 30702.7e6,
     "c5_spmm_rmat21_c64_i64_n32_conj": 7198.5e6,
 }

@@ -88,8 +88,21 @@ constexpr int spmm_batch() {
 // wave-uniform: a row end between the two nnz of a pair is handled between
 // the two predicated accumulations, and a row's sum is the sum of the two
 // halves' accumulators (one cross-half permute per row).
+// Minimum waves per SIMD asked of the register allocator.  4-byte values
+// and column indices, one column per lane, one lane group and 4 gathers per
+// batch fit in 64 VGPRs without spilling, i.e. 8 waves instead of 7
+// (1M x 1M, 32 per row, N = 64: 1.439 -> 1.342 ms).  Elsewhere the
+// allocator keeps its choice: 64 VGPRs would spill there (int64 indices,
+// two lane groups, 8 gathers per batch), and wider lanes lose more to L2
+// thrashing than they gain (R-MAT N = 256 at 6 / 8 waves: 5.65 -> 5.89 /
+// 8.06 ms; complex64 N = 32: 2.04 -> 3.33 / 6.15 ms).
+template <class V, int VEC, int U, int G, class I>
+constexpr int spmm_min_waves() {
+  return (sizeof(V) == 4 && sizeof(I) == 4 && VEC == 1 && U == 4 && G == 1) ? 8 : 1;
+}
+
 template <class V, int VEC, int U, int G, class I, class P>
-__global__ __launch_bounds__(256) void spmm_merge_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(spmm_min_waves<V, VEC, U, G, I>()))) void spmm_merge_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
     const V* __restrict__ B, int64_t ldb, V* __restrict__ C, int64_t ldc, int64_t n_dense,
     const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
