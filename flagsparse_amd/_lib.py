@@ -76,7 +76,7 @@ class FsCsrPlan(ctypes.Structure):
         ("vec_width", ctypes.c_int32),
         ("tile_items", ctypes.c_int32),
         ("rows_per_block", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("spmm_wg_cap", ctypes.c_int32),
         ("n_tiles", ctypes.c_int64),
         ("max_row", ctypes.c_int64),
         ("min_row", ctypes.c_int64),

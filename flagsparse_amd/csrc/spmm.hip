@@ -318,6 +318,20 @@ int spmm_vec_for(int val_t, int64_t n_dense) {
   return vec;
 }
 
+// LDS bytes per CU of the current device (cached per device id).
+inline size_t lds_per_cu() {
+  static size_t cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 163840;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || n <= 0)
+      n = 163840;
+    cached[dev] = (size_t)n;
+  }
+  return cached[dev];
+}
+
 template <class V, int VEC, int G>
 int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
                     const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense,
@@ -334,13 +348,26 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_XCD")) xcd_cols = std::atoi(e) != 0 ? (int)col_tiles : 0;
   if (xcd_cols > 0 && blocks * col_tiles > 0x7fffffffLL) xcd_cols = 0;
   dim3 g = xcd_cols > 0 ? dim3((unsigned)(blocks * col_tiles)) : dim3((unsigned)blocks, (unsigned)col_tiles);
+  // Residency cap for the two-columns-per-lane kernel: dynamic LDS of
+  // (LDS per CU) / cap bytes per workgroup leaves room for `cap` workgroups
+  // per CU.  On matrices with skewed columns (R-MAT) fewer concurrent waves
+  // keep more hot B rows in L2: 4 per CU instead of 5, N = 256: 5.69 ->
+  // 5.43 ms, N = 128: 2.86 -> 2.73 ms.  On uniform columns it costs 7-13%, so
+  // the caller sets plan->spmm_wg_cap only for skewed matrices.
+  size_t lds_pad = 0;
+  int cap = plan->spmm_wg_cap;
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_WG_CAP")) cap = std::atoi(e);
+  if (VEC == 2 && cap > 0) {
+    const size_t per_cu = lds_per_cu();
+    lds_pad = std::min<size_t>(per_cu / (size_t)cap, 65536);
+  }
   int u = spmm_batch<V, VEC>();
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_U")) u = std::atoi(e);
   auto go = [&](auto icode, auto pcode) {
     using I = std::conditional_t<decltype(icode)::value, int64_t, int32_t>;
     using P = std::conditional_t<decltype(pcode)::value, int64_t, int32_t>;
     auto launch = [&](auto uc) {
-      hipLaunchKernelGGL((spmm_merge_kernel<V, VEC, decltype(uc)::value, G, I, P>), g, dim3(256), 0, stream,
+      hipLaunchKernelGGL((spmm_merge_kernel<V, VEC, decltype(uc)::value, G, I, P>), g, dim3(256), lds_pad, stream,
                          static_cast<const V*>(vals), static_cast<const I*>(cols), static_cast<const P*>(indptr),
                          static_cast<const V*>(B), ldb, static_cast<V*>(C), ldc, n_dense, part, head, tail,
                          plan->n_rows, plan->nnz, n_tiles, xcd_cols);

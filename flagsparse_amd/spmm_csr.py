@@ -199,6 +199,21 @@ def _check_segment_override(max_row_nnz, block_nnz, max_segments):
         )
 
 
+# Skewed columns (a few columns hold much of the matrix, as in R-MAT / power-law
+# graphs): the two-columns-per-lane SpMM kernel then runs with at most
+# _SPMM_SKEW_WG_CAP workgroups per CU, which keeps more hot B rows in L2.
+_SPMM_SKEW_MIN_NNZ = 1 << 20
+_SPMM_SKEW_SHARE = 0.2   # share of nnz in the top 1% of columns (uniform columns: ~1%)
+_SPMM_SKEW_WG_CAP = 4
+
+
+def _column_skew(indices, n_cols):
+    """Share of the entries that fall in the 1% most frequent columns (one sync)."""
+    counts = torch.bincount(indices, minlength=n_cols)
+    top = torch.topk(counts, max(1, n_cols // 100), sorted=False).values
+    return float(top.sum().item()) / float(max(1, indices.numel()))
+
+
 class _SpmmPlan:
     """Analysis + partition + workspace for one (matrix, N) SpMM."""
 
@@ -209,6 +224,8 @@ class _SpmmPlan:
         self.tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(_compute_dtype(data.dtype)), 0))
         self.n_tiles = self.csr.n_tiles(self.tile_items)
         self.part = self.csr.partition(indptr, self.tile_items)
+        if indices.numel() >= _SPMM_SKEW_MIN_NNZ and _column_skew(indices, n_cols) >= _SPMM_SKEW_SHARE:
+            self.csr.plan.spmm_wg_cap = _SPMM_SKEW_WG_CAP
 
 
 def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):

@@ -62,7 +62,9 @@ typedef struct fs_csr_plan {
   int32_t tile_items;    /* merge-path items (rows + nnz) per tile; entries
                             per block for FS_KERNEL_NNZBLOCK */
   int32_t rows_per_block; /* rows per workgroup for FS_KERNEL_STREAM */
-  int32_t reserved;
+  int32_t spmm_wg_cap;   /* fs_spmm_csr: workgroups per CU for the two-columns-
+                            per-lane kernel (0 = as many as resources allow).
+                            fs_csr_analyze writes 0; the caller may set it. */
   int64_t n_tiles;       /* merge-path tiles / entry blocks */
   int64_t max_row, min_row;
   int64_t hist[FS_HIST_BINS];

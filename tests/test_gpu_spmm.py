@@ -265,3 +265,22 @@ def test_spmm_full_size_configs(device, config):
     gen = np.random.default_rng(1)
     rows = sorted(set(gen.integers(0, sh[0], 1500).tolist()) | {0, sh[0] - 1, longest})
     _sampled_rows(d, i, p, B, C, rows, REL_TOL[d.dtype])
+
+
+def test_spmm_skewed_columns_cap_residency_bit_identical(device, monkeypatch):
+    """An R-MAT matrix (skewed columns) gets a residency cap for the
+    two-columns-per-lane kernel; uniform columns do not.  The cap changes
+    only how many workgroups share a CU, so results are bit-identical."""
+    for k in ("FLAGSPARSE_SPMM_WG_CAP", "FLAGSPARSE_SPMM_VEC", "FLAGSPARSE_SPMM_G", "FLAGSPARSE_SPMM_XCD"):
+        monkeypatch.delenv(k, raising=False)
+    d, i, p, sh = S.rmat(17, dtype=torch.float32, index_dtype=torch.int64, device=device, seed=3)
+    route = fs.prepare_spmm_csr_route(d, i, p, sh)
+    assert route.hip_plan().csr.plan.spmm_wg_cap == 4
+    B = S.dense(sh[1], 256, torch.float32, device, seed=5, dist="normal")
+    C_cap = fs.flagsparse_spmm_csr_run(route, B)
+    monkeypatch.setenv("FLAGSPARSE_SPMM_WG_CAP", "0")
+    C_free = fs.flagsparse_spmm_csr_run(route, B)
+    assert torch.equal(C_cap, C_free)
+    _check(d, i, p, sh, S.dense(sh[1], 64, torch.float32, device, seed=6), "non")
+    d, i, p, sh = S.uniform_rows(1 << 16, 1 << 16, 32, torch.float32, torch.int32, device, seed=7)
+    assert fs.prepare_spmm_csr_route(d, i, p, sh).hip_plan().csr.plan.spmm_wg_cap == 0
