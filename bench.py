@@ -52,8 +52,8 @@ DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 MEASURED_TRAFFIC = {
     "c1_spmv_uniform4096_f32_i32": 0.747e6,
     "c2_spmv_stencil128_f64_i32": 621.2e6,
-    "c3_spmv_powerlaw4M_f32_i32": 2440.0e6,
-    "c3_spmv_powerlaw4M_f32_i64": 2440.4e6,
+    "c3_spmv_powerlaw4M_f32_i32": 1762.1e6,
+    "c3_spmv_powerlaw4M_f32_i64": 1761.1e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
     "c4_spmm_uniform1M_f32_i32_n64_trans": 9184.6e6,
     "c5_spmm_rmat21_f32_i64_n256_non": 30702.7e6,

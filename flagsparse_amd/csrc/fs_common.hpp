@@ -9,6 +9,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 #include <string>
 
 #include "../../include/flagsparse_hip.h"
@@ -199,6 +201,29 @@ int fail(int code, const std::string& msg);
 int check_hip(hipError_t e, const char* what);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// LDS bytes per CU of the current device (cached per device id).
+inline size_t lds_per_cu() {
+  static size_t cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 163840;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || n <= 0)
+      n = 163840;
+    cached[dev] = (size_t)n;
+  }
+  return cached[dev];
+}
+
+// Dynamic LDS bytes that leave room for at most `wg_per_cu` workgroups per
+// CU of a kernel using `static_lds` bytes of LDS per workgroup (0 when the
+// cap is off or already implied).
+inline size_t lds_pad_for_cap(int wg_per_cu, size_t static_lds) {
+  if (wg_per_cu <= 0) return 0;
+  const size_t share = lds_per_cu() / (size_t)wg_per_cu;
+  return share > static_lds ? std::min<size_t>(share - static_lds, 65536 - static_lds) : 0;
+}
 
 // Type-code validation shared by every entry point.
 bool valid_types(int val_t, int idx_t, int ptr_t);

@@ -318,20 +318,6 @@ int spmm_vec_for(int val_t, int64_t n_dense) {
   return vec;
 }
 
-// LDS bytes per CU of the current device (cached per device id).
-inline size_t lds_per_cu() {
-  static size_t cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 163840;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || n <= 0)
-      n = 163840;
-    cached[dev] = (size_t)n;
-  }
-  return cached[dev];
-}
-
 template <class V, int VEC, int G>
 int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
                     const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense,
@@ -357,10 +343,7 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   size_t lds_pad = 0;
   int cap = plan->spmm_wg_cap;
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_WG_CAP")) cap = std::atoi(e);
-  if (VEC == 2 && cap > 0) {
-    const size_t per_cu = lds_per_cu();
-    lds_pad = std::min<size_t>(per_cu / (size_t)cap, 65536);
-  }
+  if (VEC == 2) lds_pad = lds_pad_for_cap(cap, 0);  // the kernel has no static LDS
   int u = spmm_batch<V, VEC>();
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_U")) u = std::atoi(e);
   auto go = [&](auto icode, auto pcode) {

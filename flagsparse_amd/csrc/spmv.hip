@@ -634,6 +634,7 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
 // (panel-major); panel_reduce_kernel sums them per row in panel order.
 // ---------------------------------------------------------------------------
 constexpr int kMaxPanels = 64;
+constexpr int kPanelWgPerCu = 6;
 struct PanelTable {
   int64_t first[kMaxPanels + 1];  // first merge block of each panel; [n_panels] = number of blocks
 };
@@ -881,7 +882,17 @@ int launch_spmv_panels(const fs_csr_plan* plan, int n_panels, const int64_t* pan
     }
   }
   if (per_xcd * kXcds > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr_panels: grid too large");
-  hipLaunchKernelGGL((spmv_panel_merge_kernel<V, I, P>), dim3((unsigned)(per_xcd * kXcds)), dim3(256), 0, stream,
+  // At most 6 workgroups per CU instead of the 8 that LDS allows: fewer
+  // concurrent tiles contend for the L2 request queues that the random x
+  // gathers saturate (power-law 4M, 4 panels: 0.593 -> 0.577 ms; 5 per CU
+  // the same, 4 per CU 0.615, 2 per CU 0.846).  FLAGSPARSE_PANEL_WG_CAP=N
+  // overrides (0 = no cap).
+  int cap = kPanelWgPerCu;
+  if (const char* e = std::getenv("FLAGSPARSE_PANEL_WG_CAP")) cap = std::atoi(e);
+  const size_t static_lds = sizeof(unsigned) * kMergeWaves * (kMergeTile / 32) +
+                            sizeof(typename VT<V>::acc) * kMergeWaves * (kMergeTile + kMergeTile / 8);
+  const size_t lds_pad = lds_pad_for_cap(cap, static_lds);
+  hipLaunchKernelGGL((spmv_panel_merge_kernel<V, I, P>), dim3((unsigned)(per_xcd * kXcds)), dim3(256), lds_pad, stream,
                      static_cast<const V*>(vals), static_cast<const I*>(cols), p, static_cast<const V*>(x), partial,
                      static_cast<const int64_t*>(part), head, tail, tab, n_panels, plan->n_rows, plan->nnz, n_tiles);
   FS_CHECK_LAUNCH("spmv_panel_merge_kernel");
