@@ -280,6 +280,7 @@ def run(args):
         rhs = B
         step = lambda: fs.flagsparse_spmm_csr_run(route, B)  # noqa: E731
         plan = route.hip_plan()
+        plan.set_residency(route.kernel_indices, k, n_dense, route.data.dtype)  # as the public call does
         C = torch.empty((m, n_dense), dtype=data.dtype, device=device)
         lib = _lib.lib()
         ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(data.dtype), plan.n_tiles, n_dense), device)

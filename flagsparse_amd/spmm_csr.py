@@ -205,26 +205,46 @@ def _check_segment_override(max_row_nnz, block_nnz, max_segments):
 _SPMM_SKEW_MIN_NNZ = 1 << 20
 _SPMM_SKEW_SHARE = 0.2   # share of nnz in the top 1% of columns (uniform columns: ~1%)
 _SPMM_SKEW_WG_CAP = 4
+_SPMM_SKEW_MAX_COLS = 1 << 27  # wider: no per-column count array (1 GB of int64), no cap
+
+
+_SPMM_SKEW_SAMPLE = 1 << 22  # entries sampled (evenly strided) for the column counts
 
 
 def _column_skew(indices, n_cols):
-    """Share of the entries that fall in the 1% most frequent columns (one sync)."""
-    counts = torch.bincount(indices, minlength=n_cols)
+    """Share of the sampled entries that fall in the 1% most frequent columns
+    (one sync)."""
+    step = max(1, indices.numel() // _SPMM_SKEW_SAMPLE)
+    sample = indices[::step]
+    counts = torch.bincount(sample, minlength=n_cols)
     top = torch.topk(counts, max(1, n_cols // 100), sorted=False).values
-    return float(top.sum().item()) / float(max(1, indices.numel()))
+    return float(top.sum().item()) / float(max(1, sample.numel()))
 
 
 class _SpmmPlan:
     """Analysis + partition + workspace for one (matrix, N) SpMM."""
 
-    __slots__ = ("csr", "part", "tile_items", "n_tiles")
+    __slots__ = ("csr", "part", "tile_items", "n_tiles", "_skew_checked")
 
     def __init__(self, data, indices, indptr, n_rows, n_cols):
         self.csr = analyze_csr(data, indices, indptr, n_rows, n_cols)
         self.tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(_compute_dtype(data.dtype)), 0))
         self.n_tiles = self.csr.n_tiles(self.tile_items)
         self.part = self.csr.partition(indptr, self.tile_items)
-        if indices.numel() >= _SPMM_SKEW_MIN_NNZ and _column_skew(indices, n_cols) >= _SPMM_SKEW_SHARE:
+        self._skew_checked = False
+
+    def set_residency(self, indices, n_cols, n_dense, value_dtype):
+        """Sets plan.spmm_wg_cap once, when a launch will use the two-columns-
+        per-lane kernel (N > 64, values of at most 8 bytes): only that kernel
+        reads the cap, so other launches skip the column count."""
+        if self._skew_checked or n_dense <= 64 or torch.empty(0, dtype=value_dtype).element_size() > 8:
+            return
+        self._skew_checked = True
+        if (
+            indices.numel() >= _SPMM_SKEW_MIN_NNZ
+            and n_cols <= _SPMM_SKEW_MAX_COLS
+            and _column_skew(indices, n_cols) >= _SPMM_SKEW_SHARE
+        ):
             self.csr.plan.spmm_wg_cap = _SPMM_SKEW_WG_CAP
 
 
@@ -246,6 +266,7 @@ def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
     if data.numel() == 0:
         C_k.zero_()
     else:
+        plan.set_residency(indices, int(plan.csr.plan.n_cols), n_dense, cdt)
         lib = _lib.lib()
         ws = _lib.workspace(
             lib.fs_spmm_workspace_bytes(_lib.value_code(cdt), plan.n_tiles, n_dense), device

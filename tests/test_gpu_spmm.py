@@ -275,12 +275,16 @@ def test_spmm_skewed_columns_cap_residency_bit_identical(device, monkeypatch):
         monkeypatch.delenv(k, raising=False)
     d, i, p, sh = S.rmat(17, dtype=torch.float32, index_dtype=torch.int64, device=device, seed=3)
     route = fs.prepare_spmm_csr_route(d, i, p, sh)
-    assert route.hip_plan().csr.plan.spmm_wg_cap == 4
+    fs.flagsparse_spmm_csr_run(route, S.dense(sh[1], 64, torch.float32, device, seed=4))
+    assert route.hip_plan().csr.plan.spmm_wg_cap == 0  # N = 64: one column per lane, not measured
     B = S.dense(sh[1], 256, torch.float32, device, seed=5, dist="normal")
     C_cap = fs.flagsparse_spmm_csr_run(route, B)
+    assert route.hip_plan().csr.plan.spmm_wg_cap == 4
     monkeypatch.setenv("FLAGSPARSE_SPMM_WG_CAP", "0")
     C_free = fs.flagsparse_spmm_csr_run(route, B)
     assert torch.equal(C_cap, C_free)
     _check(d, i, p, sh, S.dense(sh[1], 64, torch.float32, device, seed=6), "non")
     d, i, p, sh = S.uniform_rows(1 << 16, 1 << 16, 32, torch.float32, torch.int32, device, seed=7)
-    assert fs.prepare_spmm_csr_route(d, i, p, sh).hip_plan().csr.plan.spmm_wg_cap == 0
+    route = fs.prepare_spmm_csr_route(d, i, p, sh)
+    fs.flagsparse_spmm_csr_run(route, S.dense(sh[1], 256, torch.float32, device, seed=8))
+    assert route.hip_plan().csr.plan.spmm_wg_cap == 0
