@@ -179,14 +179,33 @@ def check(rc, what):
 
 
 def ptr(t):
-    """Raw device pointer of a tensor (None for empty tensors)."""
+    """Raw device pointer of a tensor as an int (None for empty tensors); the
+    c_void_p argtypes take it as is."""
     if t is None or t.numel() == 0:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
+
+
+# torch's raw current-stream handle without building a Stream object (the
+# public torch.cuda.current_stream path costs ~4 us per call).
+_raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream_handle(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """hipStream_t of torch's current stream on `device` (an int for ctypes)."""
+    if _raw_current_stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(device, torch.device):
+        index = device.index
+    elif isinstance(device, int):
+        index = device
+    elif device is None:
+        index = None
+    else:
+        index = torch.device(device).index
+    if index is None:
+        index = torch.cuda.current_device()
+    return _raw_current_stream(index)
 
 
 def value_code(dtype):
