@@ -51,7 +51,7 @@ DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 # roofline.traffic; configs not profiled with the current kernels report null.
 MEASURED_TRAFFIC = {
     "c1_spmv_uniform4096_f32_i32": 0.747e6,
-    "c2_spmv_stencil128_f64_i32": 621.2e6,
+    "c2_spmv_stencil128_f64_i32": 641.5e6,
     "c3_spmv_powerlaw4M_f32_i32": 1762.1e6,
     "c3_spmv_powerlaw4M_f32_i64": 1761.1e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
@@ -238,12 +238,13 @@ def run(args):
         if sell is not None:
             # SELL-64 copy of a short-row matrix with column locality (the stencil)
             args_abi = (
-                _lib.value_code(sell.vals.dtype), sell.col_code, _lib.index_code(sell.indptr.dtype),
+                _lib.value_code(sell.vals.dtype), sell.col_code, _lib.index_code(sell.indptr.dtype), sell.layout,
                 sell.n_rows, _lib.ptr(sell.vals), _lib.ptr(sell.cols), _lib.ptr(sell.slice_ptr), _lib.ptr(sell.indptr),
                 _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(device),
             )
             kernel_call = lambda: lib.fs_spmv_sell(*args_abi)  # noqa: E731
             extra["sell_stored_slots"] = sell.padded
+            extra["sell_layout"] = "pair" if sell.layout == 1 else "slot"
             extra["sell_column_storage"] = {0: "int32", 1: "int64", 2: "int16 offset from the row"}[sell.col_code]
         pan = prep._panels
         if pan is not None:
@@ -261,6 +262,8 @@ def run(args):
         kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
                        "panel": "spmv_panel_merge_kernel", "nnzblock": "spmv_nnzblock_kernel",
                        "sell": "spmv_sell_kernel"}[prep.kernel_name]
+        if sell is not None and sell.layout == 1:
+            kernel_name = "spmv_sell_pair_kernel"
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:

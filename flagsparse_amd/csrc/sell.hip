@@ -28,7 +28,6 @@
 
 namespace fs {
 
-__device__ inline int64_t ceil_div_d(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 template <class T>
 struct type_tag {
@@ -36,7 +35,6 @@ struct type_tag {
 };
 
 constexpr int kSellRows = 64;  // rows per slice = wave width
-constexpr int kXcdsSell = 8;   // MI355X: workgroup w runs on XCD w % 8
 
 // slots[s] = longest row of slice s.
 template <class P>
@@ -54,7 +52,9 @@ __global__ __launch_bounds__(256) void sell_slots_kernel(const P* __restrict__ r
   if (lane == 0) slots[slice] = len;
 }
 
-// Entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64.
+// Entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64 (slot
+// layout), or to slice_ptr[r / 64] + (k / 2) * 128 + 2 * (r % 64) + k % 2
+// (pair layout: a row's slots 2i and 2i+1 side by side).
 // Build kernels: one wave per slice.  A slice's entries are contiguous in
 // the CSR arrays, so the wave reads them with unit stride; each entry's row
 // inside the slice comes from a binary search over the slice's 65 row
@@ -88,7 +88,7 @@ __device__ inline void sell_load_ptr(const P* __restrict__ rowptr, int64_t n_row
 template <class V, class I, class P, class SI, bool DELTA>
 __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
                                                         const P* __restrict__ rowptr, int64_t n_rows,
-                                                        const int64_t* __restrict__ slice_ptr,
+                                                        const int64_t* __restrict__ slice_ptr, int pair,
                                                         V* __restrict__ sell_vals, SI* __restrict__ sell_cols) {
   __shared__ int64_t s_ptr[4][kSellRows + 1];
   const int lane = threadIdx.x & 63;
@@ -105,7 +105,8 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
   const int64_t row0 = slice * kSellRows;
   for (int64_t e = ptr[0] + lane; e < ptr[kSellRows]; e += kSellRows) {
     const int lr = sell_local_row(ptr, e);
-    const int64_t dst = base + (e - ptr[lr]) * kSellRows + lr;
+    const int64_t k = e - ptr[lr];
+    const int64_t dst = pair ? base + (k >> 1) * (2 * kSellRows) + 2 * lr + (k & 1) : base + k * kSellRows + lr;
     sell_vals[dst] = vals[e];
     const I c = cols[e];
     sell_cols[dst] = DELTA ? (SI)((int64_t)c - (row0 + lr)) : (SI)c;
@@ -143,26 +144,18 @@ __global__ __launch_bounds__(256) void sell_max_offset_kernel(const I* __restric
 
 // One wave per slice, lane = row.  Row lengths come from the CSR row
 // pointer; the loop runs to the slice's slot count with every slot past a
-// lane's own length masked off.
-// U slots are loaded before any is used.  With remap, XCD k takes the k-th
-// eighth of the slices in order (workgroup w -> XCD w % 8), so the rows one
-// XCD works on are contiguous and share their x window in its L2.
+// lane's own length masked off.  U slots are loaded before any is used.
+// Slot layout (used for complex values).
 template <class V, class I, class P, int U, bool DELTA>
 __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ sell_vals,
                                                         const I* __restrict__ sell_cols,
                                                         const int64_t* __restrict__ slice_ptr,
                                                         const P* __restrict__ rowptr, const V* __restrict__ x,
-                                                        V* __restrict__ y, int64_t n_rows, int64_t n_slices,
-                                                        int remap) {
+                                                        V* __restrict__ y, int64_t n_rows, int64_t n_slices) {
   using T = VT<V>;
   using A = typename T::acc;
   const int lane = threadIdx.x & 63;
-  int64_t blk = blockIdx.x;
-  if (remap) {
-    const int64_t per = (ceil_div_d(n_slices, 4) + kXcdsSell - 1) / kXcdsSell;
-    blk = (int64_t)(blockIdx.x % kXcdsSell) * per + blockIdx.x / kXcdsSell;
-  }
-  const int64_t slice = blk * 4 + (threadIdx.x >> 6);
+  const int64_t slice = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (slice >= n_slices) return;  // whole wave
   const int64_t r = slice * kSellRows + lane;
   const int len = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
@@ -193,6 +186,60 @@ __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ se
   if (r < n_rows) store_stream(y + r, T::out(acc));
 }
 
+// Pair layout (real values): each lane loads two consecutive slots of its
+// row with one 2-element vector load of values and one of columns, which
+// halves the load instructions and doubles the bytes per request
+// (27-point stencil f64 with int16 offsets: 0.1140 -> 0.1075 ms; f32:
+// 0.0858 -> 0.0804 ms).  UP pairs are loaded before any is used.  The
+// second slot of a row's last pair may be padding: it is loaded with its
+// pair but never gathered or multiplied.
+template <class V, class I, class P, int UP, bool DELTA>
+__global__ __launch_bounds__(256) void spmv_sell_pair_kernel(const V* __restrict__ sell_vals,
+                                                             const I* __restrict__ sell_cols,
+                                                             const int64_t* __restrict__ slice_ptr,
+                                                             const P* __restrict__ rowptr, const V* __restrict__ x,
+                                                             V* __restrict__ y, int64_t n_rows, int64_t n_slices) {
+  static_assert(!VT<V>::complex, "pair layout is for real values");
+  using T = VT<V>;
+  using A = typename T::acc;
+  typedef V V2 __attribute__((ext_vector_type(2)));
+  typedef I I2 __attribute__((ext_vector_type(2)));
+  const int lane = threadIdx.x & 63;
+  const int64_t slice = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (slice >= n_slices) return;  // whole wave
+  const int64_t r = slice * kSellRows + lane;
+  const int len = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
+  const int64_t base = slice_ptr[slice];  // a multiple of 128 entries: pairs are aligned
+  const int pairs = (int)((slice_ptr[slice + 1] - base) / (2 * kSellRows));
+  const V2* pv = reinterpret_cast<const V2*>(sell_vals + base) + lane;
+  const I2* pc = reinterpret_cast<const I2*>(sell_cols + base) + lane;
+  A acc = T::zero();
+  for (int j = 0; j < pairs; j += UP) {
+    V2 v[UP];
+    I2 c[UP];
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      c[u] = I2{0, 0};
+      if (2 * (j + u) < len) {
+        v[u] = __builtin_nontemporal_load(pv + (int64_t)(j + u) * kSellRows);
+        c[u] = __builtin_nontemporal_load(pc + (int64_t)(j + u) * kSellRows);
+      }
+    }
+    V x0[UP], x1[UP];
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      if (2 * (j + u) < len) x0[u] = DELTA ? x[r + (int64_t)c[u].x] : x[c[u].x];
+      if (2 * (j + u) + 1 < len) x1[u] = DELTA ? x[r + (int64_t)c[u].y] : x[c[u].y];
+    }
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      if (2 * (j + u) < len) acc = T::fma(v[u].x, x0[u], acc);
+      if (2 * (j + u) + 1 < len) acc = T::fma(v[u].y, x1[u], acc);
+    }
+  }
+  if (r < n_rows) store_stream(y + r, T::out(acc));
+}
+
 template <class P>
 int sell_slots_p(const void* indptr, int64_t n_rows, int64_t* slots, hipStream_t s) {
   const int64_t n_slices = ceil_div(n_rows, kSellRows);
@@ -203,21 +250,22 @@ int sell_slots_p(const void* indptr, int64_t n_rows, int64_t* slots, hipStream_t
 }
 
 template <class V, class I, class P>
-int sell_fill_t(int sidx_t, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
+int sell_fill_t(int sidx_t, int layout, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
                 const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) {
+  const int pair = layout == FS_SELL_PAIR;
   const dim3 g((unsigned)ceil_div(ceil_div(n_rows, kSellRows), 4));
   if (sidx_t == FS_SELL_D16)
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int16_t, true>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
-                       static_cast<V*>(sv), static_cast<int16_t*>(sc));
+                       pair, static_cast<V*>(sv), static_cast<int16_t*>(sc));
   else if (sidx_t == FS_SELL_I32)
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int32_t, false>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
-                       static_cast<V*>(sv), static_cast<int32_t*>(sc));
+                       pair, static_cast<V*>(sv), static_cast<int32_t*>(sc));
   else
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int64_t, false>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
-                       static_cast<V*>(sv), static_cast<int64_t*>(sc));
+                       pair, static_cast<V*>(sv), static_cast<int64_t*>(sc));
   FS_CHECK_LAUNCH("sell_fill_kernel");
   return FS_OK;
 }
@@ -228,21 +276,35 @@ inline int env_int(const char* name, int dflt) {
 }
 
 template <class V, class I, class P, bool DELTA>
-int spmv_sell_t(int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr, const void* indptr,
-                const void* x, void* y, hipStream_t s) {
+int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr,
+                const void* indptr, const void* x, void* y, hipStream_t s) {
   const int64_t n_slices = ceil_div(n_rows, kSellRows);
-  const int64_t blocks = ceil_div(n_slices, 4);
-  const int remap = env_int("FLAGSPARSE_SELL_REMAP", 0) != 0;
-  const int64_t grid = remap ? ceil_div(blocks, kXcdsSell) * kXcdsSell : blocks;
-  // Slots in flight: 16 for 4-byte values (27-point stencil f32: 0.0858 ms,
-  // against 0.0877 with 8 and 0.0925 with 4), 4 for wider ones (f64 with
-  // 16-bit column offsets: 0.1138 ms, against 0.1164 with 8 and 0.1446 with 16)
+  const dim3 grid((unsigned)ceil_div(n_slices, 4));
+  if constexpr (!VT<V>::complex) {
+    if (layout == FS_SELL_PAIR) {
+      // 4 pairs in flight (f64 stencil: 0.1107 / 0.1084 / 0.1075 ms with 1 / 2 / 4)
+      const int up = env_int("FLAGSPARSE_SELL_UP", 4);
+      auto go = [&](auto uc) {
+        hipLaunchKernelGGL((spmv_sell_pair_kernel<V, I, P, decltype(uc)::value, DELTA>), grid, dim3(256), 0, s,
+                           static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
+                           static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y), n_rows,
+                           n_slices);
+      };
+      if (up <= 2) go(std::integral_constant<int, 2>{});
+      else if (up <= 4) go(std::integral_constant<int, 4>{});
+      else go(std::integral_constant<int, 8>{});
+      FS_CHECK_LAUNCH("spmv_sell_pair_kernel");
+      return FS_OK;
+    }
+  }
+  if (layout != FS_SELL_SLOT) return fail(FS_E_INVALID, "fs_spmv_sell: the pair layout is for real values");
+  // Slots in flight: 16 for 4-byte values, 4 for wider ones.
   const int u = env_int("FLAGSPARSE_SELL_U", sizeof(V) <= 4 ? 16 : 4);
   auto go = [&](auto uc) {
-    hipLaunchKernelGGL((spmv_sell_kernel<V, I, P, decltype(uc)::value, DELTA>), dim3((unsigned)grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((spmv_sell_kernel<V, I, P, decltype(uc)::value, DELTA>), grid, dim3(256), 0, s,
                        static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
                        static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y), n_rows,
-                       n_slices, remap);
+                       n_slices);
   };
   if (u <= 4) go(std::integral_constant<int, 4>{});
   else if (u <= 8) go(std::integral_constant<int, 8>{});
@@ -275,17 +337,18 @@ int dispatch_vip(int val_t, int idx_t, int ptr_t, Args... args) {
 
 template <class V, class I, class P>
 struct FillF {
-  int operator()(int sidx_t, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
+  int operator()(int sidx_t, int layout, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
                  const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) const {
-    return sell_fill_t<V, I, P>(sidx_t, n_rows, vals, cols, indptr, slice_ptr, sv, sc, s);
+    return sell_fill_t<V, I, P>(sidx_t, layout, n_rows, vals, cols, indptr, slice_ptr, sv, sc, s);
   }
 };
 
 template <class V, class I, class P>
 struct SpmvF {
-  int operator()(int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr, const void* indptr,
-                 const void* x, void* y, hipStream_t s) const {
-    return spmv_sell_t<V, I, P, std::is_same<I, int16_t>::value>(n_rows, sv, sc, slice_ptr, indptr, x, y, s);
+  int operator()(int layout, int64_t n_rows, const void* sv, const void* sc, const int64_t* slice_ptr,
+                 const void* indptr, const void* x, void* y, hipStream_t s) const {
+    return spmv_sell_t<V, I, P, std::is_same<I, int16_t>::value>(layout, n_rows, sv, sc, slice_ptr, indptr, x, y,
+                                                                  s);
   }
 };
 
@@ -325,27 +388,30 @@ extern "C" int fs_sell_max_offset(int idx_t, int ptr_t, int64_t n_rows, const vo
   return FS_OK;
 }
 
-extern "C" int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t, int64_t n_rows, const void* vals,
-                              const void* cols, const void* indptr, const int64_t* slice_ptr, void* sell_vals,
-                              void* sell_cols, hipStream_t stream) {
+extern "C" int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t, int layout, int64_t n_rows,
+                              const void* vals, const void* cols, const void* indptr, const int64_t* slice_ptr,
+                              void* sell_vals, void* sell_cols, hipStream_t stream) {
   if (!valid_types(val_t, idx_t, ptr_t) ||
       !(sell_idx_t == FS_SELL_I32 || sell_idx_t == FS_SELL_I64 || sell_idx_t == FS_SELL_D16))
     return fail(FS_E_INVALID, "fs_csr_to_sell: bad type code");
+  if (!(layout == FS_SELL_SLOT || layout == FS_SELL_PAIR) ||
+      (layout == FS_SELL_PAIR && (val_t == FS_C64 || val_t == FS_C128)))
+    return fail(FS_E_INVALID, "fs_csr_to_sell: bad layout (the pair layout is for real values)");
   if (n_rows < 0) return fail(FS_E_INVALID, "fs_csr_to_sell: negative size");
   if (n_rows == 0) return FS_OK;
   if (!indptr || !slice_ptr) return fail(FS_E_INVALID, "fs_csr_to_sell: null pointer");
-  return dispatch_vip<FillF>(val_t, idx_t, ptr_t, sell_idx_t, n_rows, vals, cols, indptr, slice_ptr, sell_vals,
-                             sell_cols, stream);
+  return dispatch_vip<FillF>(val_t, idx_t, ptr_t, sell_idx_t, layout, n_rows, vals, cols, indptr, slice_ptr,
+                             sell_vals, sell_cols, stream);
 }
 
-extern "C" int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int64_t n_rows, const void* sell_vals,
-                            const void* sell_cols, const int64_t* slice_ptr, const void* indptr, const void* x,
-                            void* y, hipStream_t stream) {
+extern "C" int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
+                            const void* sell_vals, const void* sell_cols, const int64_t* slice_ptr,
+                            const void* indptr, const void* x, void* y, hipStream_t stream) {
   if (!valid_types(val_t, sell_idx_t == FS_SELL_D16 ? FS_I32 : sell_idx_t, ptr_t))
     return fail(FS_E_INVALID, "fs_spmv_sell: bad type code");
   if (n_rows < 0) return fail(FS_E_INVALID, "fs_spmv_sell: negative size");
   if (n_rows == 0) return FS_OK;
   if (!indptr || !slice_ptr || !y) return fail(FS_E_INVALID, "fs_spmv_sell: null pointer");
-  return dispatch_vip<SpmvF>(val_t, sell_idx_t, ptr_t, n_rows, sell_vals, sell_cols, slice_ptr, indptr, x, y,
-                             stream);
+  return dispatch_vip<SpmvF>(val_t, sell_idx_t, ptr_t, layout, n_rows, sell_vals, sell_cols, slice_ptr, indptr, x,
+                             y, stream);
 }

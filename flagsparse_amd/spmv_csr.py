@@ -173,10 +173,16 @@ class PreparedCsrSpmv:
             # hold one next to the caller's matrix, the CSR kernels run instead.
             if _spmv_use_sell(p, self.kernel_indices, self.kernel_indptr, self._one_shot):
                 try:
-                    slice_ptr = _sell_slice_ptr(self.kernel_indptr, self.n_rows)
-                    padded = int(slice_ptr[-1])
-                    if padded <= _SELL_MAX_PADDING * max(1, int(p.nnz)) or _sell_forced():
-                        self._sell = SellCsr(data, self.kernel_indices, self.kernel_indptr, self.n_cols, slice_ptr)
+                    col_code = _sell_column_code(self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols)
+                    # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.080);
+                    # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
+                    pair = col_code == _SELL_D16 and not data.dtype.is_complex
+                    slice_ptr, stored = _sell_slice_ptr(self.kernel_indptr, self.n_rows, pair)
+                    if stored <= _SELL_MAX_PADDING * max(1, int(p.nnz)) or _sell_forced():
+                        self._sell = SellCsr(
+                            data, self.kernel_indices, self.kernel_indptr, slice_ptr, col_code,
+                            _SELL_PAIR if pair else _SELL_SLOT,
+                        )
                 except torch.OutOfMemoryError:
                     self._sell = None
                     torch.cuda.empty_cache()
@@ -362,9 +368,11 @@ def _spmv_use_sell(plan, indices, indptr, one_shot):
     return _sell_locality(indices, indptr, n_rows) >= _SELL_MIN_LOCALITY
 
 
-def _sell_slice_ptr(indptr, n_rows):
+def _sell_slice_ptr(indptr, n_rows, pair):
     """Start of every 64-row slice in the SELL-64 copy (int64, n_slices + 1):
-    the prefix sum of 64 x the slice's longest row."""
+    the prefix sum of 64 x the slice's slot count (its longest row, rounded
+    up to even for the pair layout).  Also returns 64 x the sum of the
+    unrounded counts, which the padding bound is judged on (one sync)."""
     device = indptr.device
     n_slices = -(-n_rows // 64)
     slots = torch.empty(n_slices, dtype=torch.int64, device=device)
@@ -374,12 +382,16 @@ def _sell_slice_ptr(indptr, n_rows):
         ),
         "fs_sell_slots",
     )
+    unrounded = int(slots.sum().item()) * 64
+    if pair:
+        slots = (slots + 1) // 2 * 2
     slice_ptr = torch.zeros(n_slices + 1, dtype=torch.int64, device=device)
     torch.cumsum(slots * 64, 0, out=slice_ptr[1:])
-    return slice_ptr
+    return slice_ptr, unrounded
 
 
 _SELL_I32, _SELL_I64, _SELL_D16 = 0, 1, 2  # enum fs_sell_index
+_SELL_SLOT, _SELL_PAIR = 0, 1  # enum fs_sell_layout
 
 
 def _sell_max_offset(indices, indptr, n_rows):
@@ -397,37 +409,43 @@ def _sell_max_offset(indices, indptr, n_rows):
     return int(out.item())
 
 
+def _sell_column_code(indices, indptr, n_rows, n_cols):
+    """Column storage of the SELL copy: int16 offsets c - r when every
+    |c - r| <= 32767 (off with FLAGSPARSE_SELL_DELTA=0), else int32 when
+    n_cols - 1 fits, else int64."""
+    if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0" and _sell_max_offset(indices, indptr, n_rows) <= 32767:
+        return _SELL_D16
+    return _SELL_I32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else _SELL_I64
+
+
 class SellCsr:
-    """A as SELL-64: slices of 64 consecutive rows, slot-major, built once per
-    prepared matrix (fs_sell_slots, fs_csr_to_sell).  Columns are stored as
-    the int16 offset c - r from the row when every |c - r| <= 32767 (banded
-    matrices such as stencils: 2 bytes per entry instead of 4; off with
-    FLAGSPARSE_SELL_DELTA=0), else as int32 when n_cols - 1 fits, else int64.
-    The CSR row pointer of the prepared matrix supplies the row lengths."""
+    """A as SELL-64: slices of 64 consecutive rows, built once per prepared
+    matrix (fs_sell_slots, fs_csr_to_sell).  Columns are stored as chosen by
+    _sell_column_code; with int16 offsets, real values use the pair layout (a
+    row's consecutive slots side by side, loaded two at a time), otherwise
+    the slot layout.  The CSR row pointer of the prepared matrix supplies the
+    row lengths."""
 
-    __slots__ = ("vals", "cols", "col_code", "slice_ptr", "indptr", "n_rows", "padded")
+    __slots__ = ("vals", "cols", "col_code", "layout", "slice_ptr", "indptr", "n_rows", "padded")
 
-    def __init__(self, data, indices, indptr, n_cols, slice_ptr):
+    def __init__(self, data, indices, indptr, slice_ptr, col_code, layout):
         device = data.device
         lib = _lib.lib()
         stream = _lib.stream_handle(device)
         n_rows = indptr.numel() - 1
         self.slice_ptr = slice_ptr
+        self.layout = layout
         self.padded = int(slice_ptr[-1])
         self.indptr = indptr
         self.n_rows = n_rows
         self.vals = torch.zeros(self.padded, dtype=data.dtype, device=device)
-        if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0" and _sell_max_offset(indices, indptr, n_rows) <= 32767:
-            col_dtype, self.col_code = torch.int16, _SELL_D16
-        elif n_cols - 1 <= _INDEX_LIMIT_INT32:
-            col_dtype, self.col_code = torch.int32, _SELL_I32
-        else:
-            col_dtype, self.col_code = torch.int64, _SELL_I64
+        self.col_code = col_code
+        col_dtype = {_SELL_D16: torch.int16, _SELL_I32: torch.int32, _SELL_I64: torch.int64}[col_code]
         self.cols = torch.zeros(self.padded, dtype=col_dtype, device=device)
         _lib.check(
             lib.fs_csr_to_sell(
                 _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype),
-                self.col_code, n_rows, _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr),
+                self.col_code, layout, n_rows, _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr),
                 _lib.ptr(self.slice_ptr), _lib.ptr(self.vals), _lib.ptr(self.cols), stream,
             ),
             "fs_csr_to_sell",
@@ -436,7 +454,7 @@ class SellCsr:
     def spmv(self, x, y):
         _lib.check(
             _lib.lib().fs_spmv_sell(
-                _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype),
+                _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype), self.layout,
                 self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols), _lib.ptr(self.slice_ptr), _lib.ptr(self.indptr),
                 _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(self.vals.device),
             ),

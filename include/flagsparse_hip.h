@@ -40,6 +40,9 @@ enum fs_index_type { FS_I32 = 0, FS_I64 = 1 };
 /* Column storage of a SELL-64 copy: absolute int32 / int64, or the int16
  * offset c - r from the entry's row (banded matrices, |c - r| <= 32767). */
 enum fs_sell_index { FS_SELL_I32 = 0, FS_SELL_I64 = 1, FS_SELL_D16 = 2 };
+/* Entry order inside a SELL-64 slice: one slot of 64 rows after another, or
+ * pairs of a row's consecutive slots side by side (real values only). */
+enum fs_sell_layout { FS_SELL_SLOT = 0, FS_SELL_PAIR = 1 };
 
 enum fs_status {
   FS_OK = 0,
@@ -232,10 +235,13 @@ int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
  * CSR order).
  *
  * Layout: rows are cut into slices of 64 consecutive rows; slice s holds
- * slots[s] = its longest row slots of 64 entries each, slot-major: entry k
- * of row r sits at slice_ptr[r / 64] + 64 * k + r % 64.  slice_ptr (device,
- * int64, n_slices + 1 with n_slices = ceil(n_rows / 64)) is the exclusive
- * prefix sum of 64 * slots.  Padding slots are never read by fs_spmv_sell.
+ * S_s slots of 64 entries each.  FS_SELL_SLOT: S_s = slots[s] (the slice's
+ * longest row), and entry k of row r sits at slice_ptr[r / 64] + 64 * k +
+ * r % 64.  FS_SELL_PAIR: S_s = slots[s] rounded up to even, and entry k of
+ * row r sits at slice_ptr[r / 64] + 128 * (k / 2) + 2 * (r % 64) + k % 2.
+ * slice_ptr (device, int64, n_slices + 1 with n_slices = ceil(n_rows / 64))
+ * is the exclusive prefix sum of 64 * S_s.  Padding entries are never
+ * gathered or multiplied by fs_spmv_sell.
  *
  * fs_sell_slots writes slots[s] (device, int64, n_slices).
  * fs_sell_max_offset raises *max_dev (device, caller-initialised to 0) to
@@ -254,10 +260,10 @@ int fs_sell_max_offset(int idx_t, int ptr_t, int64_t n_rows, const void* cols,
                        const void* indptr, unsigned long long* max_dev,
                        hipStream_t stream);
 int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t,
-                   int64_t n_rows, const void* vals, const void* cols,
+                   int layout, int64_t n_rows, const void* vals, const void* cols,
                    const void* indptr, const int64_t* slice_ptr,
                    void* sell_vals, void* sell_cols, hipStream_t stream);
-int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int64_t n_rows,
+int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
                  const void* sell_vals, const void* sell_cols,
                  const int64_t* slice_ptr, const void* indptr,
                  const void* x, void* y, hipStream_t stream);

@@ -346,7 +346,11 @@ def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, delta):
         data = data.to(dtype)
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
     assert prep.kernel_name == "sell"
-    assert prep._sell.padded <= 1.03 * data.numel()
+    # 27 entries per interior row: 28 stored slots with pairs (real values with
+    # int16 offsets), 27 with slots
+    pair = delta == "1" and not dtype.is_complex
+    assert prep._sell.layout == (1 if pair else 0)
+    assert prep._sell.padded <= (1.07 if pair else 1.03) * data.numel()
     assert prep._sell.cols.dtype == (torch.int16 if delta == "1" else torch.int32)
     x = S.vector(sh[1], dtype, device, seed=7)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
@@ -377,30 +381,33 @@ def test_spmv_sell_not_chosen_without_locality_or_with_padding(device, monkeypat
     assert prep.kernel_name != "sell"
 
 
+@pytest.mark.parametrize("delta", ["1", "0"], ids=["int16-offsets", "absolute-columns"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
-def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype):
-    """Rows of one slice with different lengths: the padding slots of the short
-    rows hold column 0, where x is infinite; only row 0 references column 0,
-    so every other row must stay finite (padding is never loaded)."""
+def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype, delta):
+    """Rows of one slice with different lengths (1..7 entries, so odd lengths
+    leave half-used pairs too).  Every row references only columns n..2n-1;
+    x is infinite on columns 0..n-1, which is where a padding entry points
+    (column 0, or offset 0 = the row's own index).  A padding entry that was
+    gathered and multiplied would turn its row into nan; no row may."""
     monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    monkeypatch.setenv("FLAGSPARSE_SELL_DELTA", delta)
     n = 256
     lengths = torch.tensor([(r % 7) + 1 for r in range(n)], dtype=torch.int64, device=device)
-    lengths[0] = 3
     indptr = torch.zeros(n + 1, dtype=torch.int32, device=device)
     indptr[1:] = torch.cumsum(lengths, 0)
     cols = []
     for r in range(n):
-        start = 0 if r == 0 else 1 + (r * 13) % (n - 8)
+        start = n + (r * 13) % (n - 8)
         cols.extend(range(start, start + int(lengths[r])))
     indices = torch.tensor(cols, dtype=torch.int32, device=device)
     data = torch.ones(indices.numel(), dtype=dtype, device=device)
-    x = torch.ones(n, dtype=dtype, device=device)
-    x[0] = float("inf")
-    prep = fs.prepare_spmv_csr(data, indices, indptr, (n, n))
+    x = torch.ones(2 * n, dtype=dtype, device=device)
+    x[:n] = float("inf")
+    prep = fs.prepare_spmv_csr(data, indices, indptr, (n, 2 * n))
     assert prep.kernel_name == "sell" and prep._sell.padded > data.numel()
+    assert prep._sell.cols.dtype == (torch.int16 if delta == "1" else torch.int32)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
-    assert torch.isinf(y[0])
-    assert torch.equal(y[1:], lengths[1:].to(dtype))
+    assert torch.equal(y, lengths.to(dtype))
 
 
 @pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64], ids=["int32", "int64"])
