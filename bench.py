@@ -263,7 +263,7 @@ def run(args):
                        "panel": "spmv_panel_merge_kernel", "nnzblock": "spmv_nnzblock_kernel",
                        "sell": "spmv_sell_kernel"}[prep.kernel_name]
         if sell is not None and sell.layout == 1:
-            kernel_name = "spmv_sell_pair_kernel"
+            kernel_name = "spmv_sell_group_kernel"
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:

@@ -52,9 +52,8 @@ __global__ __launch_bounds__(256) void sell_slots_kernel(const P* __restrict__ r
   if (lane == 0) slots[slice] = len;
 }
 
-// Entry k of row r goes to slice_ptr[r / 64] + k * 64 + r % 64 (slot
-// layout), or to slice_ptr[r / 64] + (k / 2) * 128 + 2 * (r % 64) + k % 2
-// (pair layout: a row's slots 2i and 2i+1 side by side).
+// Entry k of row r goes to slice_ptr[r / 64] + (k / G) * 64 G + G (r % 64)
+// + k % G with G slots side by side: 1 (slot layout) or 2 (pair layout).
 // Build kernels: one wave per slice.  A slice's entries are contiguous in
 // the CSR arrays, so the wave reads them with unit stride; each entry's row
 // inside the slice comes from a binary search over the slice's 65 row
@@ -88,7 +87,7 @@ __device__ inline void sell_load_ptr(const P* __restrict__ rowptr, int64_t n_row
 template <class V, class I, class P, class SI, bool DELTA>
 __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
                                                         const P* __restrict__ rowptr, int64_t n_rows,
-                                                        const int64_t* __restrict__ slice_ptr, int pair,
+                                                        const int64_t* __restrict__ slice_ptr, int group,
                                                         V* __restrict__ sell_vals, SI* __restrict__ sell_cols) {
   __shared__ int64_t s_ptr[4][kSellRows + 1];
   const int lane = threadIdx.x & 63;
@@ -106,7 +105,7 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
   for (int64_t e = ptr[0] + lane; e < ptr[kSellRows]; e += kSellRows) {
     const int lr = sell_local_row(ptr, e);
     const int64_t k = e - ptr[lr];
-    const int64_t dst = pair ? base + (k >> 1) * (2 * kSellRows) + 2 * lr + (k & 1) : base + k * kSellRows + lr;
+    const int64_t dst = base + (k / group) * (group * kSellRows) + group * lr + k % group;
     sell_vals[dst] = vals[e];
     const I c = cols[e];
     sell_cols[dst] = DELTA ? (SI)((int64_t)c - (row0 + lr)) : (SI)c;
@@ -186,56 +185,56 @@ __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ se
   if (r < n_rows) store_stream(y + r, T::out(acc));
 }
 
-// Pair layout (real values): each lane loads two consecutive slots of its
+// Pair layout (real values): each lane loads G = 2 consecutive slots of its
 // row with one 2-element vector load of values and one of columns, which
-// halves the load instructions and doubles the bytes per request
-// (27-point stencil f64 with int16 offsets: 0.1140 -> 0.1075 ms; f32:
-// 0.0858 -> 0.0804 ms).  UP pairs are loaded before any is used.  The
-// second slot of a row's last pair may be padding: it is loaded with its
-// pair but never gathered or multiplied.
-template <class V, class I, class P, int UP, bool DELTA>
-__global__ __launch_bounds__(256) void spmv_sell_pair_kernel(const V* __restrict__ sell_vals,
-                                                             const I* __restrict__ sell_cols,
-                                                             const int64_t* __restrict__ slice_ptr,
-                                                             const P* __restrict__ rowptr, const V* __restrict__ x,
-                                                             V* __restrict__ y, int64_t n_rows, int64_t n_slices) {
-  static_assert(!VT<V>::complex, "pair layout is for real values");
+// halves the load instructions and doubles the bytes per request (27-point
+// stencil with int16 offsets, f64: 0.1140 -> 0.1075 ms; f32: 0.0858 ->
+// 0.0756 ms).  Groups of 4 measured no better for f32 (0.0750 ms) and worse
+// for f64 (0.132 ms).  UP groups are loaded before any is used.  The tail of a row's last group may be
+// padding: it is loaded with its group but never gathered or multiplied.
+template <class V, class I, class P, int G, int UP, bool DELTA>
+__global__ __launch_bounds__(256) void spmv_sell_group_kernel(const V* __restrict__ sell_vals,
+                                                              const I* __restrict__ sell_cols,
+                                                              const int64_t* __restrict__ slice_ptr,
+                                                              const P* __restrict__ rowptr, const V* __restrict__ x,
+                                                              V* __restrict__ y, int64_t n_rows, int64_t n_slices) {
+  static_assert(!VT<V>::complex, "grouped layouts are for real values");
   using T = VT<V>;
   using A = typename T::acc;
-  typedef V V2 __attribute__((ext_vector_type(2)));
-  typedef I I2 __attribute__((ext_vector_type(2)));
+  typedef V VG __attribute__((ext_vector_type(G)));
+  typedef I IG __attribute__((ext_vector_type(G)));
   const int lane = threadIdx.x & 63;
   const int64_t slice = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (slice >= n_slices) return;  // whole wave
   const int64_t r = slice * kSellRows + lane;
   const int len = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
-  const int64_t base = slice_ptr[slice];  // a multiple of 128 entries: pairs are aligned
-  const int pairs = (int)((slice_ptr[slice + 1] - base) / (2 * kSellRows));
-  const V2* pv = reinterpret_cast<const V2*>(sell_vals + base) + lane;
-  const I2* pc = reinterpret_cast<const I2*>(sell_cols + base) + lane;
+  const int64_t base = slice_ptr[slice];  // a multiple of 64 * G entries: groups are aligned
+  const int groups = (int)((slice_ptr[slice + 1] - base) / (G * kSellRows));
+  const VG* pv = reinterpret_cast<const VG*>(sell_vals + base) + lane;
+  const IG* pc = reinterpret_cast<const IG*>(sell_cols + base) + lane;
   A acc = T::zero();
-  for (int j = 0; j < pairs; j += UP) {
-    V2 v[UP];
-    I2 c[UP];
+  for (int j = 0; j < groups; j += UP) {
+    VG v[UP];
+    IG c[UP];
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
-      c[u] = I2{0, 0};
-      if (2 * (j + u) < len) {
+      c[u] = IG(0);
+      if (G * (j + u) < len) {
         v[u] = __builtin_nontemporal_load(pv + (int64_t)(j + u) * kSellRows);
         c[u] = __builtin_nontemporal_load(pc + (int64_t)(j + u) * kSellRows);
       }
     }
-    V x0[UP], x1[UP];
+    V xs[UP][G];
 #pragma unroll
-    for (int u = 0; u < UP; ++u) {
-      if (2 * (j + u) < len) x0[u] = DELTA ? x[r + (int64_t)c[u].x] : x[c[u].x];
-      if (2 * (j + u) + 1 < len) x1[u] = DELTA ? x[r + (int64_t)c[u].y] : x[c[u].y];
-    }
+    for (int u = 0; u < UP; ++u)
 #pragma unroll
-    for (int u = 0; u < UP; ++u) {
-      if (2 * (j + u) < len) acc = T::fma(v[u].x, x0[u], acc);
-      if (2 * (j + u) + 1 < len) acc = T::fma(v[u].y, x1[u], acc);
-    }
+      for (int g = 0; g < G; ++g)
+        if (G * (j + u) + g < len) xs[u][g] = DELTA ? x[r + (int64_t)c[u][g]] : x[c[u][g]];
+#pragma unroll
+    for (int u = 0; u < UP; ++u)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (G * (j + u) + g < len) acc = T::fma(v[u][g], xs[u][g], acc);
   }
   if (r < n_rows) store_stream(y + r, T::out(acc));
 }
@@ -252,20 +251,20 @@ int sell_slots_p(const void* indptr, int64_t n_rows, int64_t* slots, hipStream_t
 template <class V, class I, class P>
 int sell_fill_t(int sidx_t, int layout, int64_t n_rows, const void* vals, const void* cols, const void* indptr,
                 const int64_t* slice_ptr, void* sv, void* sc, hipStream_t s) {
-  const int pair = layout == FS_SELL_PAIR;
+  const int group = layout == FS_SELL_PAIR ? 2 : 1;  // slots side by side
   const dim3 g((unsigned)ceil_div(ceil_div(n_rows, kSellRows), 4));
   if (sidx_t == FS_SELL_D16)
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int16_t, true>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
-                       pair, static_cast<V*>(sv), static_cast<int16_t*>(sc));
+                       group, static_cast<V*>(sv), static_cast<int16_t*>(sc));
   else if (sidx_t == FS_SELL_I32)
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int32_t, false>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
-                       pair, static_cast<V*>(sv), static_cast<int32_t*>(sc));
+                       group, static_cast<V*>(sv), static_cast<int32_t*>(sc));
   else
     hipLaunchKernelGGL((sell_fill_kernel<V, I, P, int64_t, false>), g, dim3(256), 0, s, static_cast<const V*>(vals),
                        static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows, slice_ptr,
-                       pair, static_cast<V*>(sv), static_cast<int64_t*>(sc));
+                       group, static_cast<V*>(sv), static_cast<int64_t*>(sc));
   FS_CHECK_LAUNCH("sell_fill_kernel");
   return FS_OK;
 }
@@ -282,18 +281,23 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
   const dim3 grid((unsigned)ceil_div(n_slices, 4));
   if constexpr (!VT<V>::complex) {
     if (layout == FS_SELL_PAIR) {
-      // 4 pairs in flight (f64 stencil: 0.1107 / 0.1084 / 0.1075 ms with 1 / 2 / 4)
-      const int up = env_int("FLAGSPARSE_SELL_UP", 4);
-      auto go = [&](auto uc) {
-        hipLaunchKernelGGL((spmv_sell_pair_kernel<V, I, P, decltype(uc)::value, DELTA>), grid, dim3(256), 0, s,
-                           static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
+      // pairs in flight: 4 for 8-byte values (f64 stencil: 0.1084 / 0.1074 / 0.1178 ms with
+      // 2 / 4 / 8), 8 for 4-byte ones (f32: 0.0852 / 0.0804 / 0.0756 ms)
+      const int up = env_int("FLAGSPARSE_SELL_UP", sizeof(V) <= 4 ? 8 : 4);
+      auto go = [&](auto gc, auto uc) {
+        hipLaunchKernelGGL((spmv_sell_group_kernel<V, I, P, decltype(gc)::value, decltype(uc)::value, DELTA>), grid,
+                           dim3(256), 0, s, static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
                            static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y), n_rows,
                            n_slices);
       };
-      if (up <= 2) go(std::integral_constant<int, 2>{});
-      else if (up <= 4) go(std::integral_constant<int, 4>{});
-      else go(std::integral_constant<int, 8>{});
-      FS_CHECK_LAUNCH("spmv_sell_pair_kernel");
+      auto by_up = [&](auto gc) {
+        if (up <= 1) go(gc, std::integral_constant<int, 1>{});
+        else if (up <= 2) go(gc, std::integral_constant<int, 2>{});
+        else if (up <= 4) go(gc, std::integral_constant<int, 4>{});
+        else go(gc, std::integral_constant<int, 8>{});
+      };
+      by_up(std::integral_constant<int, 2>{});
+      FS_CHECK_LAUNCH("spmv_sell_group_kernel");
       return FS_OK;
     }
   }

@@ -176,12 +176,13 @@ class PreparedCsrSpmv:
                     col_code = _sell_column_code(self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols)
                     # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.080);
                     # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
-                    pair = col_code == _SELL_D16 and not data.dtype.is_complex
-                    slice_ptr, stored = _sell_slice_ptr(self.kernel_indptr, self.n_rows, pair)
+                    layout = _SELL_SLOT
+                    if col_code == _SELL_D16 and not data.dtype.is_complex:
+                        layout = _SELL_PAIR
+                    slice_ptr, stored = _sell_slice_ptr(self.kernel_indptr, self.n_rows, _SELL_GROUP[layout])
                     if stored <= _SELL_MAX_PADDING * max(1, int(p.nnz)) or _sell_forced():
                         self._sell = SellCsr(
-                            data, self.kernel_indices, self.kernel_indptr, slice_ptr, col_code,
-                            _SELL_PAIR if pair else _SELL_SLOT,
+                            data, self.kernel_indices, self.kernel_indptr, slice_ptr, col_code, layout
                         )
                 except torch.OutOfMemoryError:
                     self._sell = None
@@ -368,10 +369,10 @@ def _spmv_use_sell(plan, indices, indptr, one_shot):
     return _sell_locality(indices, indptr, n_rows) >= _SELL_MIN_LOCALITY
 
 
-def _sell_slice_ptr(indptr, n_rows, pair):
+def _sell_slice_ptr(indptr, n_rows, group):
     """Start of every 64-row slice in the SELL-64 copy (int64, n_slices + 1):
     the prefix sum of 64 x the slice's slot count (its longest row, rounded
-    up to even for the pair layout).  Also returns 64 x the sum of the
+    up to a multiple of the layout's group size).  Also returns 64 x the sum of the
     unrounded counts, which the padding bound is judged on (one sync)."""
     device = indptr.device
     n_slices = -(-n_rows // 64)
@@ -383,8 +384,8 @@ def _sell_slice_ptr(indptr, n_rows, pair):
         "fs_sell_slots",
     )
     unrounded = int(slots.sum().item()) * 64
-    if pair:
-        slots = (slots + 1) // 2 * 2
+    if group > 1:
+        slots = (slots + group - 1) // group * group
     slice_ptr = torch.zeros(n_slices + 1, dtype=torch.int64, device=device)
     torch.cumsum(slots * 64, 0, out=slice_ptr[1:])
     return slice_ptr, unrounded
@@ -392,6 +393,7 @@ def _sell_slice_ptr(indptr, n_rows, pair):
 
 _SELL_I32, _SELL_I64, _SELL_D16 = 0, 1, 2  # enum fs_sell_index
 _SELL_SLOT, _SELL_PAIR = 0, 1  # enum fs_sell_layout
+_SELL_GROUP = {_SELL_SLOT: 1, _SELL_PAIR: 2}  # slots stored side by side
 
 
 def _sell_max_offset(indices, indptr, n_rows):
