@@ -340,10 +340,10 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   // keep more hot B rows in L2: 4 per CU instead of 5, N = 256: 5.69 ->
   // 5.43 ms, N = 128: 2.86 -> 2.73 ms.  On uniform columns it costs 7-13%, so
   // the caller sets plan->spmm_wg_cap only for skewed matrices.
-  size_t lds_pad = 0;
-  int cap = plan->spmm_wg_cap;
-  if (const char* e = std::getenv("FLAGSPARSE_SPMM_WG_CAP")) cap = std::atoi(e);
-  if (VEC == 2) lds_pad = lds_pad_for_cap(cap, 0);  // the kernel has no static LDS
+  // FLAGSPARSE_SPMM_WG_CAP=N sets the cap for every lane width (A/B runs).
+  size_t lds_pad = 0;  // the kernel has no static LDS
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_WG_CAP")) lds_pad = lds_pad_for_cap(std::atoi(e), 0);
+  else if (VEC == 2) lds_pad = lds_pad_for_cap(plan->spmm_wg_cap, 0);
   int u = spmm_batch<V, VEC>();
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_U")) u = std::atoi(e);
   auto go = [&](auto icode, auto pcode) {
