@@ -2,19 +2,19 @@
 //
 // A prepared matrix whose rows are short and of similar length (stencils,
 // FEM meshes) is copied once into SELL-64: rows are cut into slices of 64
-// consecutive rows, one slice per wave; slot j of the slice holds entry j of
-// each of its 64 rows, stored contiguously (slot-major), so the slot's loads
-// are one coalesced 64-lane access. Slice s starts at slice_ptr[s] and has
-// (slice_ptr[s+1] - slice_ptr[s]) / 64 slots = its longest row. Rows keep
-// their CSR entry order, and each lane sums its own row sequentially in the
-// accumulator type (f64 for f32 data), so no cross-lane reduction and no LDS
-// are needed.
+// consecutive rows, one slice per wave, and entry k of each row is stored
+// next to entry k of the slice's other rows, so a wave's load of one slot
+// is one coalesced 64-lane access.  In the pair layout (real values with
+// 16-bit column offsets) a row's slots 2i and 2i+1 also sit side by side,
+// so each lane loads two slots with one vector load.  Rows keep their CSR
+// entry order, and each lane sums its own row sequentially in the
+// accumulator type (f64 for f32 data): no cross-lane reduction, no LDS.
 //
 // What it buys over the row-block stream kernel: on matrices whose
 // neighbouring rows have neighbouring columns (a stencil's slot j of rows
 // r..r+63 gathers x[r + offset_j .. r + 63 + offset_j]) the x gather becomes
 // as coalesced as the A stream, which takes most of the per-CU address work
-// off the gather.  Slots past a row's length are padding: never loaded,
+// off the gather.  Slots past a row's length are padding: never gathered,
 // never multiplied (an inf / nan in x cannot leak in through 0 * x).
 //
 // Reference path replaced: the per-row SpMV kernels behind
@@ -27,7 +27,6 @@
 #include <type_traits>
 
 namespace fs {
-
 
 template <class T>
 struct type_tag {
@@ -54,6 +53,7 @@ __global__ __launch_bounds__(256) void sell_slots_kernel(const P* __restrict__ r
 
 // Entry k of row r goes to slice_ptr[r / 64] + (k / G) * 64 G + G (r % 64)
 // + k % G with G slots side by side: 1 (slot layout) or 2 (pair layout).
+//
 // Build kernels: one wave per slice.  A slice's entries are contiguous in
 // the CSR arrays, so the wave reads them with unit stride; each entry's row
 // inside the slice comes from a binary search over the slice's 65 row
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void sell_max_offset_kernel(const I* __restric
 // One wave per slice, lane = row.  Row lengths come from the CSR row
 // pointer; the loop runs to the slice's slot count with every slot past a
 // lane's own length masked off.  U slots are loaded before any is used.
-// Slot layout (used for complex values).
+// Slot layout: complex values, and columns stored as int32 / int64.
 template <class V, class I, class P, int U, bool DELTA>
 __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ sell_vals,
                                                         const I* __restrict__ sell_cols,
@@ -190,8 +190,9 @@ __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ se
 // halves the load instructions and doubles the bytes per request (27-point
 // stencil with int16 offsets, f64: 0.1140 -> 0.1075 ms; f32: 0.0858 ->
 // 0.0756 ms).  Groups of 4 measured no better for f32 (0.0750 ms) and worse
-// for f64 (0.132 ms).  UP groups are loaded before any is used.  The tail of a row's last group may be
-// padding: it is loaded with its group but never gathered or multiplied.
+// for f64 (0.132 ms).  UP groups are loaded before any is used.  The tail
+// of a row's last group may be padding: it is loaded with its group but
+// never gathered or multiplied.
 template <class V, class I, class P, int G, int UP, bool DELTA>
 __global__ __launch_bounds__(256) void spmv_sell_group_kernel(const V* __restrict__ sell_vals,
                                                               const I* __restrict__ sell_cols,
