@@ -96,16 +96,15 @@ __global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict
   K key[kChunks];
   load_tile_keys<K>(keys, kind, base, n, lane, key);
   wave_sync_t();
+  // Counts only (no ranks): one LDS integer atomic per entry.  Integer sums do
+  // not depend on order, so the counts are deterministic; the stable ranks
+  // come from the scatter pass.  (Ballot peer groups here measured 98 us per
+  // pass on 33.5 M keys.)
 #pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
-    const bool valid = base + (int64_t)ch * 64 + lane < n;
-    const uint64_t active = __ballot(valid);
-    if (active == 0) break;
-    const unsigned digit = (unsigned)(key[ch] >> shift) & (kDigits - 1);
-    const uint64_t peers = peer_mask(digit, active);
-    if (valid && count_below_t(peers) == 0) hist[digit] += (unsigned)__popcll(peers);
-    wave_sync_t();
+    if (base + (int64_t)ch * 64 + lane < n) atomicAdd(&hist[(unsigned)(key[ch] >> shift) & (kDigits - 1)], 1u);
   }
+  wave_sync_t();
   for (int d = lane; d < kDigits; d += 64) counts[(int64_t)d * n_sub + sub] = hist[d];
 }
 
