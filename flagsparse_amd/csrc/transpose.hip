@@ -162,17 +162,11 @@ __global__ __launch_bounds__(64) void radix_scatter_kernel(const void* __restric
     s_glob[d] = offsets[(int64_t)d * n_sub + sub];
   }
   wave_sync_t();
-  // 2. per-digit counts of the tile
+  // 2. per-digit counts of the tile (LDS integer atomics: order independent)
 #pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch) {
-    const bool valid = ch * 64 + lane < cnt;
-    const uint64_t active = __ballot(valid);
-    if (active == 0) break;
-    const unsigned digit = (unsigned)(key[ch] >> shift) & (kDigits - 1);
-    const uint64_t peers = peer_mask(digit, active);
-    if (valid && count_below_t(peers) == 0) s_cur[digit] += (unsigned)__popcll(peers);
-    wave_sync_t();
-  }
+  for (int ch = 0; ch < kChunks; ++ch)
+    if (ch * 64 + lane < cnt) atomicAdd(&s_cur[(unsigned)(key[ch] >> shift) & (kDigits - 1)], 1u);
+  wave_sync_t();
   unsigned c4[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) c4[k] = s_cur[4 * lane + k];
