@@ -457,3 +457,59 @@ def test_spmv_copy_out_of_memory_falls_back_to_csr(device, monkeypatch, copy):
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
     assert rel_err(np_(y), ref) <= REL_TOL[torch.float64]
+
+
+def _grid_stencil(dims, offsets, dtype, device):
+    """CSR of a grid stencil (row-major grid, neighbours truncated at the
+    boundary), columns sorted within each row."""
+    n = 1
+    for d in dims:
+        n *= d
+    idx = torch.arange(n, device=device)
+    coords, rem = [], idx
+    for d in reversed(dims):
+        coords.append(rem % d)
+        rem = rem // d
+    coords = coords[::-1]
+    rows, cols = [], []
+    for off in offsets:
+        ok = torch.ones(n, dtype=torch.bool, device=device)
+        nb = torch.zeros(n, dtype=torch.int64, device=device)
+        stride = 1
+        for ax in reversed(range(len(dims))):
+            c = coords[ax] + off[ax]
+            ok &= (c >= 0) & (c < dims[ax])
+            nb += c.clamp(0, dims[ax] - 1) * stride
+            stride *= dims[ax]
+        rows.append(idx[ok])
+        cols.append(nb[ok])
+    r, c = torch.cat(rows), torch.cat(cols)
+    order = torch.argsort(r * n + c)
+    r, c = r[order], c[order]
+    indptr = torch.zeros(n + 1, dtype=torch.int32, device=device)
+    indptr[1:] = torch.cumsum(torch.bincount(r, minlength=n), 0)
+    data = S.vector(c.numel(), torch.float64, device, seed=21).to(dtype)
+    return data, c.to(torch.int32), indptr, (n, n)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize(
+    "grid",
+    [((64, 64, 64), [(0, 0, 0), (1, 0, 0), (-1, 0, 0), (0, 1, 0), (0, -1, 0), (0, 0, 1), (0, 0, -1)]),
+     ((512, 512), [(0, 0), (1, 0), (-1, 0), (0, 1), (0, -1)])],
+    ids=["3d-7pt", "2d-5pt"],
+)
+def test_spmv_sell_other_stencils(device, monkeypatch, grid, dtype):
+    """7-point 3D and 5-point 2D stencils (262,144 rows) also get the SELL copy
+    (int16 offsets, pair layout) and match the oracle on sampled rows."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS", "FLAGSPARSE_SELL_DELTA"):
+        monkeypatch.delenv(k, raising=False)
+    dims, offsets = grid
+    data, indices, indptr, sh = _grid_stencil(dims, offsets, dtype, device)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep.kernel_name == "sell" and prep._sell.layout == 1 and prep._sell.cols.dtype == torch.int16
+    x = S.vector(sh[1], dtype, device, seed=22)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    gen = np.random.default_rng(5)
+    rows = sorted(set(gen.integers(0, sh[0], 3000).tolist()) | {0, 1, sh[0] - 2, sh[0] - 1})
+    _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[dtype])
