@@ -99,3 +99,16 @@ def test_spmm_int64_columns_above_int32(wide):
     C = fs.flagsparse_spmm_csr(wide["data"], wide["indices"], wide["indptr"], B, shape)
     assert torch.equal(C[:, 0].double(), wide["y_non"])
     assert torch.equal(C[:, 1].double(), -wide["y_non"])
+
+
+def test_spmv_sell_int64_columns(wide, monkeypatch):
+    """The SELL copy forced on this matrix stores int64 absolute columns (the
+    offsets exceed int16 and n_cols - 1 exceeds int32) in the slot layout,
+    and computes exactly."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    shape = (WIDE_ROWS, WIDE_COLS)
+    prep = fs.prepare_spmv_csr(wide["data"], wide["indices"], wide["indptr"], shape)
+    assert prep.kernel_name == "sell"
+    assert prep._sell.cols.dtype == torch.int64 and prep._sell.layout == 0
+    y = fs.flagsparse_spmv_csr(x=wide["x"], prepared=prep)
+    assert torch.equal(y.double(), wide["y_non"])
