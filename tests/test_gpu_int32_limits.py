@@ -126,3 +126,15 @@ def test_spmm_nnz_above_int32(big):
     assert torch.equal(C[:, 0].double(), big["y_non"])
     assert torch.equal(C[:, 1].double(), -2 * big["y_non"])
 
+
+
+def test_spmv_sell_nnz_above_int32(big, monkeypatch):
+    """The SELL copy forced on the matrix with more than 2^31 entries (slot
+    layout, int32 columns: the column offsets exceed int16) computes exactly."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    prep = fs.prepare_spmv_csr(big["data"], big["indices"], big["indptr"], (N, N))
+    assert prep.kernel_name == "sell" and prep._sell.cols.dtype == torch.int32
+    assert prep._sell.padded >= big["nnz"]
+    y = fs.flagsparse_spmv_csr(x=big["x"], prepared=prep)
+    assert torch.equal(y.double(), big["y_non"])
+    del prep
