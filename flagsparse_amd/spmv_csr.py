@@ -173,17 +173,8 @@ class PreparedCsrSpmv:
             # hold one next to the caller's matrix, the CSR kernels run instead.
             if _spmv_use_sell(p, self.kernel_indices, self.kernel_indptr, self._one_shot):
                 try:
-                    col_code = _sell_column_code(self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols)
-                    # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.080);
-                    # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
-                    layout = _SELL_SLOT
-                    if col_code == _SELL_D16 and not data.dtype.is_complex:
-                        layout = _SELL_PAIR
-                    slice_ptr, stored = _sell_slice_ptr(self.kernel_indptr, self.n_rows, _SELL_GROUP[layout])
-                    if stored <= _SELL_MAX_PADDING * max(1, int(p.nnz)) or _sell_forced():
-                        self._sell = SellCsr(
-                            data, self.kernel_indices, self.kernel_indptr, slice_ptr, col_code, layout
-                        )
+                    self._sell = _build_sell(data, self.kernel_indices, self.kernel_indptr, self.n_rows,
+                                             self.n_cols, int(p.nnz))
                 except torch.OutOfMemoryError:
                     self._sell = None
                     torch.cuda.empty_cache()
@@ -418,6 +409,19 @@ def _sell_column_code(indices, indptr, n_rows, n_cols):
     if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0" and _sell_max_offset(indices, indptr, n_rows) <= 32767:
         return _SELL_D16
     return _SELL_I32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else _SELL_I64
+
+
+def _build_sell(data, indices, indptr, n_rows, n_cols, nnz):
+    """The SELL-64 copy, or None when its stored slots would exceed
+    _SELL_MAX_PADDING x nnz (rows too uneven) and it is not forced."""
+    col_code = _sell_column_code(indices, indptr, n_rows, n_cols)
+    # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.076);
+    # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
+    layout = _SELL_PAIR if col_code == _SELL_D16 and not data.dtype.is_complex else _SELL_SLOT
+    slice_ptr, stored = _sell_slice_ptr(indptr, n_rows, _SELL_GROUP[layout])
+    if stored > _SELL_MAX_PADDING * max(1, nnz) and not _sell_forced():
+        return None
+    return SellCsr(data, indices, indptr, slice_ptr, col_code, layout)
 
 
 class SellCsr:
