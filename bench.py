@@ -287,8 +287,9 @@ def run(args):
         C = torch.empty((m, n_dense), dtype=data.dtype, device=device)
         lib = _lib.lib()
         ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(data.dtype), plan.n_tiles, n_dense), device)
+        launch_indices, launch_plan = plan.launch_indices(route.kernel_indices, route.data.dtype)
         args_abi = (
-            plan.csr.plan, _lib.ptr(route.data), _lib.ptr(route.kernel_indices), _lib.ptr(route.kernel_indptr),
+            launch_plan, _lib.ptr(route.data), _lib.ptr(launch_indices), _lib.ptr(route.kernel_indptr),
             _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.ptr(plan.part), plan.tile_items, plan.n_tiles,
             _lib.ptr(ws), ws.numel(), _lib.stream_handle(device),
         )

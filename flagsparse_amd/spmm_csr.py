@@ -14,6 +14,7 @@ Error types and messages are the reference's.  Device work is one call
 each into libflagsparse_hip; there is no CPU path.
 """
 
+import ctypes
 import math
 import time
 from dataclasses import dataclass
@@ -224,7 +225,7 @@ def _column_skew(indices, n_cols):
 class _SpmmPlan:
     """Analysis + partition + workspace for one (matrix, N) SpMM."""
 
-    __slots__ = ("csr", "part", "tile_items", "n_tiles", "_skew_checked")
+    __slots__ = ("csr", "part", "tile_items", "n_tiles", "_skew_checked", "_wide")
 
     def __init__(self, data, indices, indptr, n_rows, n_cols):
         self.csr = analyze_csr(data, indices, indptr, n_rows, n_cols)
@@ -232,6 +233,28 @@ class _SpmmPlan:
         self.n_tiles = self.csr.n_tiles(self.tile_items)
         self.part = self.csr.partition(indptr, self.tile_items)
         self._skew_checked = False
+        self._wide = None
+
+    def launch_indices(self, indices, value_dtype):
+        """(column indices, plan struct) a launch passes to fs_spmm_csr.
+
+        complex64 with int32 column indices runs the int64-index kernel on a
+        widened copy of the indices (built once per plan).  On gfx950 the
+        int32 instantiation of that kernel serialises its B-row gathers
+        behind waits for every outstanding load, which measured 10-34% slower
+        (R-MAT 2^20, N = 32 / 64 / 128: 1.29 / 1.69 / 2.93 ms, against 1.05 /
+        1.26 / 2.67 ms with int64 indices); for f32 / f64 int32 indices are as
+        fast or faster.  The widening costs one pass over the indices."""
+        if value_dtype != torch.complex64 or indices.dtype != torch.int32:
+            return indices, self.csr.plan
+        if self._wide is None:
+            wide_plan = _lib.FsCsrPlan()
+            ctypes.memmove(ctypes.byref(wide_plan), ctypes.byref(self.csr.plan), ctypes.sizeof(wide_plan))
+            wide_plan.idx_t = _lib.index_code(torch.int64)
+            self._wide = (indices.to(torch.int64), wide_plan)
+        wide_indices, wide_plan = self._wide
+        wide_plan.spmm_wg_cap = self.csr.plan.spmm_wg_cap  # may be set after the copy
+        return wide_indices, wide_plan
 
     def set_residency(self, indices, n_cols, n_dense, value_dtype):
         """Sets plan.spmm_wg_cap once, when a launch will use the two-columns-
@@ -267,15 +290,16 @@ def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
         C_k.zero_()
     else:
         plan.set_residency(indices, int(plan.csr.plan.n_cols), n_dense, cdt)
+        launch_indices, launch_plan = plan.launch_indices(indices, cdt)
         lib = _lib.lib()
         ws = _lib.workspace(
             lib.fs_spmm_workspace_bytes(_lib.value_code(cdt), plan.n_tiles, n_dense), device
         )
         _lib.check(
             lib.fs_spmm_csr(
-                plan.csr.plan,
+                launch_plan,
                 _lib.ptr(data_c),
-                _lib.ptr(indices),
+                _lib.ptr(launch_indices),
                 _lib.ptr(indptr),
                 _lib.ptr(B_c),
                 int(B_c.stride(0)) if B_c.shape[0] > 0 else n_dense,
