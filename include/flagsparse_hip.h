@@ -12,7 +12,8 @@
  *   - all array arguments are raw device pointers; sizes are int64_t;
  *   - value / index types are passed as the enums below;
  *   - every launch goes to the caller's hipStream_t and returns without
- *     synchronising, except fs_csr_analyze (documented below);
+ *     synchronising, except fs_csr_analyze and fs_csr_panelize, which read
+ *     small results back to the host (documented below);
  *   - nothing is allocated: scratch memory comes from a caller workspace
  *     whose size the matching *_workspace_bytes / plan fields report;
  *   - the return value is 0 on success, a negative FS_E* code otherwise;
