@@ -15,7 +15,6 @@ each into libflagsparse_hip; there is no CPU path.
 """
 
 import ctypes
-import math
 import time
 from dataclasses import dataclass
 
@@ -23,7 +22,6 @@ import torch
 
 from . import _lib
 from ._common import (
-    _INDEX_LIMIT_INT32,
     SUPPORTED_INDEX_DTYPES,
     SUPPORTED_VALUE_DTYPES,
     _compute_dtype,

@@ -25,7 +25,6 @@ from ._common import (
     _INDEX_LIMIT_INT32,
     SUPPORTED_INDEX_DTYPES,
     _compute_dtype,
-    _is_complex_dtype,
 )
 from ._csr import analyze_csr, transpose_csr
 

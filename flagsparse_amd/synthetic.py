@@ -18,7 +18,6 @@ Configs (BASELINE.json "configs"):
                        values, i64 indices, dense B 2^21 x 256 N(0,1)
 """
 
-import math
 
 import torch
 
