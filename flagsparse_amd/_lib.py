@@ -39,6 +39,8 @@ KERNEL_NAMES = {
 EXPORTED_SYMBOLS = (
     "fs_last_error",
     "fs_version",
+    "fs_csr_check_bytes",
+    "fs_csr_check",
     "fs_csr_stats_bytes",
     "fs_csr_analyze",
     "fs_csr_partition",
@@ -103,6 +105,10 @@ def _declare(lib):
     lib.fs_last_error.argtypes = []
     lib.fs_version.restype = ctypes.c_char_p
     lib.fs_version.argtypes = []
+    lib.fs_csr_check_bytes.restype = _sz
+    lib.fs_csr_check_bytes.argtypes = []
+    lib.fs_csr_check.restype = _i32
+    lib.fs_csr_check.argtypes = [_vp, _i32, _vp, _i32, _i64, _i64, _vp, ctypes.POINTER(_i64), _vp]
     lib.fs_csr_stats_bytes.restype = _sz
     lib.fs_csr_stats_bytes.argtypes = []
     lib.fs_csr_analyze.restype = _i32

@@ -94,6 +94,79 @@ __global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr
 }
 
 // ---------------------------------------------------------------------------
+// Structure check: indptr[0], indptr[n_rows], whether any row pointer
+// decreases, and the column range, in one pass over indptr and indices.
+// check layout (uint64): [0] indptr[0], [1] indptr[n_rows], [2] rows whose
+// pointer decreases, [3] min column, [4] max column; the columns are stored
+// with the sign bit flipped so that the unsigned atomics order signed values.
+// ---------------------------------------------------------------------------
+constexpr unsigned long long kSignFlip = 1ull << 63;
+
+template <class P>
+__global__ void check_init_kernel(const P* __restrict__ rowptr, int64_t n_rows, unsigned long long* check) {
+  const int k = threadIdx.x;
+  if (k == 0) check[0] = (unsigned long long)(int64_t)rowptr[0];
+  if (k == 1) check[1] = (unsigned long long)(int64_t)rowptr[n_rows];
+  if (k == 2) check[2] = 0ull;
+  if (k == 3) check[3] = ~0ull;
+  if (k == 4) check[4] = 0ull;
+}
+
+template <class P, class I>
+__global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                                    const I* __restrict__ cols, int64_t nnz,
+                                                    unsigned long long* check) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long bad = 0;
+  for (int64_t r = tid; r < n_rows; r += stride)
+    bad += __builtin_nontemporal_load(rowptr + r + 1) < __builtin_nontemporal_load(rowptr + r) ? 1ull : 0ull;
+  unsigned long long lo = ~0ull, hi = 0;
+  int64_t k = tid;
+  for (; k + 3 * stride < nnz; k += 4 * stride) {
+    I c[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) c[u] = __builtin_nontemporal_load(cols + k + u * stride);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const unsigned long long v = (unsigned long long)(int64_t)c[u] ^ kSignFlip;
+      lo = v < lo ? v : lo;
+      hi = v > hi ? v : hi;
+    }
+  }
+  for (; k < nnz; k += stride) {
+    const unsigned long long v = (unsigned long long)(int64_t)__builtin_nontemporal_load(cols + k) ^ kSignFlip;
+    lo = v < lo ? v : lo;
+    hi = v > hi ? v : hi;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    bad += __shfl_xor(bad, off);
+    const unsigned long long olo = __shfl_xor(lo, off), ohi = __shfl_xor(hi, off);
+    lo = olo < lo ? olo : lo;
+    hi = ohi > hi ? ohi : hi;
+  }
+  __shared__ unsigned long long s_bad[4], s_lo[4], s_hi[4];
+  if ((threadIdx.x & 63) == 0) {
+    s_bad[threadIdx.x >> 6] = bad;
+    s_lo[threadIdx.x >> 6] = lo;
+    s_hi[threadIdx.x >> 6] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+      bad += s_bad[w];
+      lo = s_lo[w] < lo ? s_lo[w] : lo;
+      hi = s_hi[w] > hi ? s_hi[w] : hi;
+    }
+    if (bad) atomicAdd(&check[2], bad);
+    if (nnz > 0) {
+      atomicMin(&check[3], lo);
+      atomicMax(&check[4], hi);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Merge-path partition.  The merge path interleaves the row-end offsets
 // (rowptr[1..n_rows]) with the nnz indices 0..nnz-1; a row end is consumed
 // before nnz j when rowptr[i+1] <= j.  Tile t starts at diagonal t*T; part[t]
@@ -1013,6 +1086,44 @@ extern "C" int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_
     plan->min_row = (int64_t)host[FS_HIST_BINS + 1];
   }
   choose_spmv_kernel(plan, force_kernel);
+  return FS_OK;
+}
+
+extern "C" size_t fs_csr_check_bytes(void) { return 5 * sizeof(unsigned long long); }
+
+extern "C" int fs_csr_check(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows,
+                            int64_t nnz, void* check_dev, int64_t* out, hipStream_t stream) {
+  if (!indptr || !check_dev || !out) return fail(FS_E_INVALID, "fs_csr_check: null pointer");
+  if ((ptr_t != FS_I32 && ptr_t != FS_I64) || (idx_t != FS_I32 && idx_t != FS_I64))
+    return fail(FS_E_INVALID, "fs_csr_check: bad index type code");
+  if (n_rows < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_csr_check: negative size");
+  if (nnz > 0 && !indices) return fail(FS_E_INVALID, "fs_csr_check: indices is null");
+  unsigned long long* ck = static_cast<unsigned long long*>(check_dev);
+  // enough workgroups to stream the indices at full rate; each ends with
+  // three global atomics
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(std::max(n_rows, nnz), 1024), 2048));
+#define FS_CHECK_CASE(P, I)                                                                                   \
+  do {                                                                                                        \
+    hipLaunchKernelGGL((check_init_kernel<P>), dim3(1), dim3(64), 0, stream, static_cast<const P*>(indptr),   \
+                       n_rows, ck);                                                                           \
+    FS_CHECK_LAUNCH("check_init_kernel");                                                                     \
+    hipLaunchKernelGGL((check_kernel<P, I>), dim3((unsigned)blocks), dim3(256), 0, stream,                    \
+                       static_cast<const P*>(indptr), n_rows, static_cast<const I*>(indices), nnz, ck);       \
+    FS_CHECK_LAUNCH("check_kernel");                                                                          \
+  } while (0)
+  if (ptr_t == FS_I32 && idx_t == FS_I32) FS_CHECK_CASE(int32_t, int32_t);
+  else if (ptr_t == FS_I32) FS_CHECK_CASE(int32_t, int64_t);
+  else if (idx_t == FS_I32) FS_CHECK_CASE(int64_t, int32_t);
+  else FS_CHECK_CASE(int64_t, int64_t);
+#undef FS_CHECK_CASE
+  unsigned long long host[5];
+  FS_CHECK_HIP(hipMemcpyAsync(host, ck, sizeof(host), hipMemcpyDeviceToHost, stream));
+  FS_CHECK_HIP(hipStreamSynchronize(stream));
+  out[0] = (int64_t)host[0];
+  out[1] = (int64_t)host[1];
+  out[2] = (int64_t)host[2];
+  out[3] = nnz > 0 ? (int64_t)(host[3] ^ kSignFlip) : 0;
+  out[4] = nnz > 0 ? (int64_t)(host[4] ^ kSignFlip) : -1;
   return FS_OK;
 }
 

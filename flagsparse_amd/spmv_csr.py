@@ -486,35 +486,44 @@ def _transpose_csr_for_spmv(data, indices, indptr, shape):
 
 
 def _check_structure(data, indices, indptr, n_cols, messages):
-    """indptr / index checks with one device->host transfer.
+    """indptr / index checks in one native pass with one device->host sync
+    (fs_csr_check).
 
     The reference checks indptr[0], indptr[-1], monotonicity and the column
     range with separate .item() syncs (spmv_csr.py:546-558); the checks and
-    the order in which their errors are raised are kept, the syncs merged.
+    the order in which their errors are raised are kept.  Returns the column
+    range (lo, hi), or None when nnz == 0.
     """
     nnz = data.numel()
     if indptr.numel() == 0:
-        return
-    probes = [indptr[:1].to(torch.int64), indptr[-1:].to(torch.int64)]
-    if indptr.numel() > 1:
-        probes.append(torch.any(indptr[1:] < indptr[:-1]).reshape(1).to(torch.int64))
-    else:
-        probes.append(torch.zeros(1, dtype=torch.int64, device=indptr.device))
-    if nnz > 0:
-        lo, hi = torch.aminmax(indices)  # one pass over the indices for both bounds
-        probes.append(lo.reshape(1).to(torch.int64))
-        probes.append(hi.reshape(1).to(torch.int64))
-    vals = torch.cat(probes).cpu().tolist()
-    if int(vals[0]) != 0:
+        return None
+    lib = _lib.lib()
+    check = _lib.workspace(lib.fs_csr_check_bytes(), indptr.device)
+    vals = (ctypes.c_int64 * 5)()
+    _lib.check(
+        lib.fs_csr_check(
+            _lib.ptr(indptr),
+            _lib.index_code(indptr.dtype),
+            _lib.ptr(indices) if nnz > 0 else None,
+            _lib.index_code(indices.dtype),
+            indptr.numel() - 1,
+            nnz,
+            _lib.ptr(check),
+            vals,
+            _lib.stream_handle(indptr.device),
+        ),
+        "fs_csr_check",
+    )
+    if vals[0] != 0:
         raise ValueError(messages["start"])
-    if int(vals[1]) != nnz:
-        raise ValueError(messages["last"](int(vals[1])))
-    if int(vals[2]) != 0:
+    if vals[1] != nnz:
+        raise ValueError(messages["last"](vals[1]))
+    if vals[2] != 0:
         raise ValueError(messages["monotone"])
     if nnz > 0:
-        if int(vals[3]) < 0 or int(vals[4]) >= n_cols:
+        if vals[3] < 0 or vals[4] >= n_cols:
             raise IndexError("indices out of range for n_cols")
-        return int(vals[3]), int(vals[4])
+        return vals[3], vals[4]
     return None
 
 

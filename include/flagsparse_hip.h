@@ -12,8 +12,9 @@
  *   - all array arguments are raw device pointers; sizes are int64_t;
  *   - value / index types are passed as the enums below;
  *   - every launch goes to the caller's hipStream_t and returns without
- *     synchronising, except fs_csr_analyze and fs_csr_panelize, which read
- *     small results back to the host (documented below);
+ *     synchronising, except fs_csr_check, fs_csr_analyze and
+ *     fs_csr_panelize, which read small results back to the host
+ *     (documented below);
  *   - nothing is allocated: scratch memory comes from a caller workspace
  *     whose size the matching *_workspace_bytes / plan fields report;
  *   - the return value is 0 on success, a negative FS_E* code otherwise;
@@ -98,6 +99,21 @@ int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t,
                    int64_t n_rows, int64_t n_cols, int64_t nnz,
                    int force_kernel, void* stats_dev, fs_csr_plan* plan,
                    hipStream_t stream);
+
+/*
+ * Structure check of a CSR matrix, replacing the reference's separate
+ * indptr / column-range checks (spmv_csr.py:546-558; the same checks guard
+ * spmm_csr.py's prepare).  One pass over indptr and indices into `check_dev`
+ * (>= fs_csr_check_bytes() bytes of device memory), then synchronises
+ * `stream` and writes five values to host `out`: indptr[0], indptr[n_rows],
+ * the number of rows r with indptr[r+1] < indptr[r], the smallest and the
+ * largest column index (0 and -1 when nnz == 0).  The caller raises the
+ * reference's errors from them, in the reference's order.
+ */
+size_t fs_csr_check_bytes(void);
+int fs_csr_check(const void* indptr, int ptr_t, const void* indices, int idx_t,
+                 int64_t n_rows, int64_t nnz, void* check_dev, int64_t* out,
+                 hipStream_t stream);
 
 /*
  * Merge-path partition: for each tile t, the row coordinate where the

@@ -513,3 +513,58 @@ def test_spmv_sell_other_stencils(device, monkeypatch, grid, dtype):
     gen = np.random.default_rng(5)
     rows = sorted(set(gen.integers(0, sh[0], 3000).tolist()) | {0, 1, sh[0] - 2, sh[0] - 1})
     _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[dtype])
+
+
+@pytest.mark.parametrize("ptr_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+@pytest.mark.parametrize("idx_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+def test_spmv_structure_errors(device, ptr_dtype, idx_dtype):
+    """The reference's structure checks (spmv_csr.py:546-558), their messages
+    and order, with each fault placed deep in arrays larger than one
+    workgroup's share so that the one-pass device check must find it."""
+    n = 300_000
+    per = 3
+    indptr = torch.arange(0, (n + 1) * per, per, dtype=torch.int64)
+    cols = (torch.arange(n * per, dtype=torch.int64) * 7) % n
+    data = torch.ones(n * per, dtype=torch.float32, device=device)
+    x = torch.ones(n, dtype=torch.float32, device=device)
+
+    def call(p, c, shape=(n, n)):
+        return fs.flagsparse_spmv_csr(data, c.to(idx_dtype).to(device), p.to(ptr_dtype).to(device), x, shape)
+
+    y = call(indptr, cols)  # valid: every row sums three ones
+    assert torch.equal(y, torch.full((n,), 3.0, device=device))
+
+    bad = indptr.clone()
+    bad += 1
+    with pytest.raises(ValueError, match="indptr must start at zero"):
+        call(bad, cols)
+    bad = indptr.clone()
+    bad[-1] -= 1
+    with pytest.raises(ValueError, match="indptr\\[-1\\] must equal nnz"):
+        call(bad, cols)
+    bad = indptr.clone()
+    bad[n - 7] = bad[n - 6] + 1  # one decreasing step near the end
+    with pytest.raises(ValueError, match="non-decreasing"):
+        call(bad, cols)
+    # a wrong start is reported before a decreasing step
+    bad[0] = 5
+    with pytest.raises(ValueError, match="start at zero"):
+        call(bad, cols)
+    for pos, v in ((n * per - 2, n), (n * per // 2 + 11, -1), (0, -(2 ** 31) if idx_dtype == torch.int32 else -(2 ** 40))):
+        c = cols.clone()
+        c[pos] = v
+        with pytest.raises(IndexError, match="indices out of range for n_cols"):
+            call(indptr, c)
+    # a column index equal to n_cols - 1 at the very end is in range
+    c = cols.clone()
+    c[-1] = n - 1
+    call(indptr, c)
+    # empty matrices pass the check
+    empty = fs.flagsparse_spmv_csr(
+        data[:0], cols[:0].to(idx_dtype).to(device), torch.zeros(5, dtype=ptr_dtype, device=device),
+        x[:3], (4, 3))
+    assert torch.equal(empty, torch.zeros(4, device=device))
+    with pytest.raises(ValueError, match="must equal nnz"):
+        fs.flagsparse_spmv_csr(
+            data[:0], cols[:0].to(idx_dtype).to(device), torch.tensor([0, 0, 1], dtype=ptr_dtype, device=device),
+            x[:3], (2, 3))
