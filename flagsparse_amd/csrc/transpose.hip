@@ -444,7 +444,7 @@ struct Layout {
   size_t key_bytes, pos_bytes, rowid_bytes;
   int64_t n_sub, n_counts, n_partials;
   size_t off_keys_a, off_keys_b, off_pos_a, off_pos_b, off_rowid, off_counts, off_partials, total;
-  size_t off_counts_extra = 0, off_key2 = 0;
+  size_t off_key2 = 0;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -699,27 +699,148 @@ int coo_to_csr_idx(const Layout& L, char* ws, int idx_t, int64_t n, int64_t n_ro
 // ---- column panels (stacked CSR: panel-major rows) ----
 // Panel of an entry = col / panel_width.  A stable partition by panel keeps
 // CSR order inside every panel, so the stacked matrix with rows
-// (panel * n_rows + row) is again a CSR, read off the sorted composite keys.
-template <class I, class K>
-__global__ __launch_bounds__(256) void panel_keys_kernel(const I* __restrict__ cols, int64_t n, int64_t width,
-                                                         K* __restrict__ keys) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k < n) keys[k] = (K)((int64_t)cols[k] / width);
+// (panel * n_rows + row) is again a CSR, read off the composite keys.  With
+// at most 64 panels the partition is one counting pass: per wave sub-tile,
+// count the entries of every panel, scan the [panel][sub-tile] counts, then
+// scatter.  Within a 64-entry chunk, lanes of one panel write consecutive
+// slots, so stores leave in at most one run per panel; the sources are read
+// once, in order.
+constexpr int kMaxPanels = 64;
+
+// col / width for 0 <= col < 2^53: a double-precision estimate, corrected by
+// one step either way (no 64-bit integer division).
+__device__ inline int panel_of(int64_t c, int64_t width, double inv_width) {
+  int64_t q = (int64_t)((double)c * inv_width);
+  if (q * width > c) --q;
+  else if ((q + 1) * width <= c) ++q;
+  return (int)q;
 }
 
-template <class V, class I, class OP, class Pos>
-__global__ __launch_bounds__(256) void panel_gather_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
-                                                           const int64_t* __restrict__ rowid,
-                                                           const Pos* __restrict__ perm, int64_t n, int64_t n_rows,
-                                                           int64_t width, V* __restrict__ p_vals,
-                                                           I* __restrict__ p_cols, int64_t* __restrict__ key2) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= n) return;
-  const int64_t p = perm ? (int64_t)perm[k] : k;
-  const I c = cols[p];
-  p_vals[k] = vals[p];
-  p_cols[k] = c;
-  key2[k] = ((int64_t)c / width) * n_rows + rowid[p];
+template <class I>
+__global__ __launch_bounds__(256) void panel_count_kernel(const I* __restrict__ cols, int64_t n, int64_t width,
+                                                          double inv_width, int n_panels, int64_t n_sub,
+                                                          int64_t* __restrict__ counts) {
+  __shared__ unsigned s_hist[kWavesPerBlock][kMaxPanels];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t sub = (int64_t)blockIdx.x * kWavesPerBlock + w;
+  if (sub >= n_sub) return;  // wave-local work only
+  unsigned* hist = s_hist[w];
+  hist[lane] = 0;
+  const int64_t base = sub * kSub;
+  I c[kChunks];
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int64_t e = base + (int64_t)ch * 64 + lane;
+    c[ch] = e < n ? __builtin_nontemporal_load(cols + e) : (I)0;
+  }
+  wave_sync_t();
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch)
+    if (base + (int64_t)ch * 64 + lane < n) atomicAdd(&hist[panel_of((int64_t)c[ch], width, inv_width)], 1u);
+  wave_sync_t();
+  if (lane < n_panels) counts[(int64_t)lane * n_sub + sub] = hist[lane];
+}
+
+// One wave per sub-tile of kSub entries.
+//  1. row id of every entry into LDS: lane l walks entries [32l, 32l + 32)
+//     of the tile from one binary search (slot j + j/32 keeps that stride-32
+//     walk free of bank conflicts);
+//  2. the global start of panel q's run in this sub-tile, offsets[q][sub]
+//     (exclusive scan of panel_count_kernel's counts), into LDS;
+//  3. chunk by chunk, rank = lanes of the same panel below this lane (peer
+//     masks from ceil(log2 n_panels) ballots) plus the panel's cursor, which
+//     keeps the partition stable.
+template <class V, class I, class P, class RT>
+__global__ __launch_bounds__(64) void panel_scatter_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
+                                                           const P* __restrict__ rowptr, int64_t n_rows, int64_t n,
+                                                           int64_t width, double inv_width, int n_panels,
+                                                           int qbits, int64_t n_sub,
+                                                           const int64_t* __restrict__ offsets,
+                                                           V* __restrict__ p_vals, I* __restrict__ p_cols,
+                                                           int64_t* __restrict__ key2) {
+  constexpr int kItems = (int)(kSub / 64);
+  __shared__ RT s_row[kSub + kSub / 32];
+  __shared__ int64_t s_glob[kMaxPanels];
+  __shared__ unsigned s_cur[kMaxPanels];
+  __shared__ int64_t s_bounds[2];
+  const int lane = threadIdx.x;
+  const int64_t sub = blockIdx.x;
+  if (sub >= n_sub) return;
+  const int64_t base = sub * kSub;
+  const int cnt = n - base < kSub ? (int)(n - base) : (int)kSub;
+  I c[kChunks];
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int e = ch * 64 + lane;
+    c[ch] = e < cnt ? __builtin_nontemporal_load(cols + base + e) : (I)0;
+  }
+  s_glob[lane] = lane < n_panels ? offsets[(int64_t)lane * n_sub + sub] : 0;
+  s_cur[lane] = 0;
+  // rows of the tile's first and last entries bound every lane's search
+  if (lane < 2) {
+    const int64_t e = lane == 0 ? base : base + cnt - 1;
+    int64_t lo = 0, hi = n_rows - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if ((int64_t)rowptr[mid + 1] <= e)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    s_bounds[lane] = lo;
+  }
+  wave_sync_t();
+  {
+    const int j0 = lane * kItems;
+    if (j0 < cnt) {
+      const int64_t e0 = base + j0;
+      int64_t lo = s_bounds[0], hi = s_bounds[1];
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)rowptr[mid + 1] <= e0)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      int64_t row = lo;
+      int64_t rend = (int64_t)rowptr[row + 1];
+      for (int k = 0; k < kItems && j0 + k < cnt; ++k) {
+        const int64_t e = e0 + k;
+        while (rend <= e) {
+          ++row;
+          rend = (int64_t)rowptr[row + 1];
+        }
+        const int j = j0 + k;
+        s_row[j + (j >> 5)] = (RT)row;
+      }
+    }
+  }
+  wave_sync_t();
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int j = ch * 64 + lane;
+    const bool valid = j < cnt;
+    const uint64_t active = __ballot(valid);
+    if (active == 0) break;
+    const int q = valid ? panel_of((int64_t)c[ch], width, inv_width) : 0;
+    uint64_t peers = active;
+    for (int b = 0; b < qbits; ++b) {
+      const bool bit = (q >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = count_below_t(peers);
+    if (valid) {
+      const int64_t dst = s_glob[q] + (int64_t)s_cur[q] + rank;
+      p_vals[dst] = vals[base + j];
+      p_cols[dst] = c[ch];
+      key2[dst] = (int64_t)q * n_rows + (int64_t)s_row[j + (j >> 5)];
+    }
+    wave_sync_t();
+    if (valid && rank == 0) s_cur[q] += (unsigned)__popcll(peers);
+    wave_sync_t();
+  }
 }
 
 template <class OP>
@@ -739,29 +860,27 @@ __global__ void panel_starts_kernel(const OP* __restrict__ indptr, int64_t n_row
   if (q <= n_panels) out[q] = (int64_t)indptr[(int64_t)q * n_rows];
 }
 
-template <class V, class I, class P, class K, class Pos>
+template <class V, class I, class P, class RT>
 int panelize_typed(const Layout& L, char* ws, int64_t n_rows, int64_t n_cols, int64_t nnz, int n_panels,
                    const void* vals, const void* cols, const void* indptr, void* p_vals, void* p_cols,
                    void* p_indptr, hipStream_t s) {
   const int64_t width = ceil_div(n_cols, n_panels);
-  K* keys0 = reinterpret_cast<K*>(ws + L.off_counts_extra);
-  int64_t* rowid = reinterpret_cast<int64_t*>(ws + L.off_rowid);
+  const double inv_width = 1.0 / (double)width;
+  int qbits = 0;
+  while ((1 << qbits) < n_panels) ++qbits;
+  int64_t* counts = reinterpret_cast<int64_t*>(ws + L.off_counts);
+  int64_t* partial = reinterpret_cast<int64_t*>(ws + L.off_partials);
   int64_t* key2 = reinterpret_cast<int64_t*>(ws + L.off_key2);
-  const unsigned blocks = (unsigned)ceil_div(nnz, 256);
-  hipLaunchKernelGGL((panel_keys_kernel<I, K>), dim3(blocks), dim3(256), 0, s, static_cast<const I*>(cols), nnz,
-                     width, keys0);
-  FS_CHECK_LAUNCH("panel_keys_kernel");
-  const K* sorted = nullptr;
-  const Pos* perm = nullptr;
-  int rc = radix_sort_cols<K, Pos>(L, ws, keys0, 2, nnz, n_panels, &sorted, &perm, s);
+  hipLaunchKernelGGL((panel_count_kernel<I>), dim3((unsigned)ceil_div(L.n_sub, kWavesPerBlock)), dim3(256), 0, s,
+                     static_cast<const I*>(cols), nnz, width, inv_width, n_panels, L.n_sub, counts);
+  FS_CHECK_LAUNCH("panel_count_kernel");
+  int rc = device_exclusive_scan(counts, L.n_counts, partial, s);
   if (rc != FS_OK) return rc;
-  hipLaunchKernelGGL((expand_rows_kernel<P, int64_t>), dim3((unsigned)ceil_div(ceil_div(nnz, kExpandItems), 256)),
-                     dim3(256), 0, s, static_cast<const P*>(indptr), n_rows, nnz, rowid);
-  FS_CHECK_LAUNCH("expand_rows_kernel");
-  hipLaunchKernelGGL((panel_gather_kernel<V, I, P, Pos>), dim3(blocks), dim3(256), 0, s, static_cast<const V*>(vals),
-                     static_cast<const I*>(cols), rowid, perm, nnz, n_rows, width, static_cast<V*>(p_vals),
+  hipLaunchKernelGGL((panel_scatter_kernel<V, I, P, RT>), dim3((unsigned)L.n_sub), dim3(64), 0, s,
+                     static_cast<const V*>(vals), static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows,
+                     nnz, width, inv_width, n_panels, qbits, L.n_sub, counts, static_cast<V*>(p_vals),
                      static_cast<I*>(p_cols), key2);
-  FS_CHECK_LAUNCH("panel_gather_kernel");
+  FS_CHECK_LAUNCH("panel_scatter_kernel");
   const int64_t n_out = (int64_t)n_panels * n_rows;
   hipLaunchKernelGGL((panel_indptr_kernel<P>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, key2, nnz,
                      n_out, static_cast<P*>(p_indptr));
@@ -784,9 +903,9 @@ int read_panel_starts(const void* p_indptr, int64_t n_rows, int n_panels, int64_
 template <class V, class I, class P>
 int panelize_pos(const Layout& L, char* ws, int64_t n_rows, int64_t n_cols, int64_t nnz, int n_panels,
                  const void* vals, const void* cols, const void* indptr, void* pv, void* pc, void* pp, hipStream_t s) {
-  if (L.pos_bytes == 4)
-    return panelize_typed<V, I, P, uint32_t, uint32_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
-  return panelize_typed<V, I, P, uint32_t, uint64_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+  if (n_rows <= (int64_t)0xffffffffLL)
+    return panelize_typed<V, I, P, uint32_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
+  return panelize_typed<V, I, P, uint64_t>(L, ws, n_rows, n_cols, nnz, n_panels, vals, cols, indptr, pv, pc, pp, s);
 }
 
 template <class V>
@@ -880,13 +999,19 @@ extern "C" int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_col
   }
 }
 
-// Panel layout: the radix buffers sized for keys in [0, n_panels) plus the
-// unsorted keys, row ids and composite (panel, row) keys.
+// Panel layout: the [panel][sub-tile] counts and their scan partials, then
+// the composite (panel, row) keys.
 static Layout panel_layout(int64_t n_rows, int64_t n_panels, int64_t nnz) {
-  Layout L = make_layout(n_rows, n_panels, nnz);
-  size_t o = L.total;
-  L.off_counts_extra = o;
-  o = align256(o + 4 * (size_t)nnz);
+  (void)n_rows;
+  Layout L{};
+  L.n_sub = ceil_div(nnz, kSub);
+  L.n_counts = n_panels * L.n_sub;
+  L.n_partials = ceil_div(L.n_counts, kScanTile);
+  size_t o = 0;
+  L.off_counts = o;
+  o = align256(o + sizeof(int64_t) * L.n_counts);
+  L.off_partials = o;
+  o = align256(o + sizeof(int64_t) * (L.n_partials + 1));
   L.off_key2 = o;  // also stages the n_panels + 1 panel starts afterwards
   o = align256(o + 8 * (size_t)std::max<int64_t>(nnz, n_panels + 1));
   L.total = o;

@@ -568,3 +568,36 @@ def test_spmv_structure_errors(device, ptr_dtype, idx_dtype):
         fs.flagsparse_spmv_csr(
             data[:0], cols[:0].to(idx_dtype).to(device), torch.tensor([0, 0, 1], dtype=ptr_dtype, device=device),
             x[:3], (2, 3))
+
+
+@pytest.mark.parametrize("idx_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+@pytest.mark.parametrize("n_panels", [1, 2, 3, 5, 8, 17, 64])
+@pytest.mark.parametrize("shape", [(1, 7), (300, 1000), (20_000, 333_333), (70_000, 64)],
+                         ids=["1row", "small", "wide", "narrow"])
+def test_panelize_matches_stable_partition(device, idx_dtype, n_panels, shape):
+    """The stacked column-panel CSR equals a stable sort of the entries by
+    (panel, row) computed on the host, exactly: values, columns, row
+    pointer and panel offsets.  Rows are ragged and include empty rows and a
+    row spanning several sub-tiles."""
+    n_rows, n_cols = shape
+    g = torch.Generator().manual_seed(n_rows * 131 + n_panels)
+    lengths = torch.randint(0, 9, (n_rows,), generator=g)
+    lengths[torch.randint(0, n_rows, (max(1, n_rows // 50),), generator=g)] = 0
+    lengths[n_rows // 2] = 5000
+    indptr = torch.zeros(n_rows + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(lengths, 0)
+    nnz = int(indptr[-1])
+    cols = torch.randint(0, n_cols, (nnz,), generator=g)
+    vals = torch.randn(nnz, generator=g, dtype=torch.float64)
+    pc = spmv_mod.PanelledCsr(vals.to(device), cols.to(idx_dtype).to(device), indptr.to(device), n_rows, n_cols,
+                              n_panels)
+    width = -(-n_cols // n_panels)
+    rows = torch.repeat_interleave(torch.arange(n_rows), lengths)
+    key = (cols // width) * n_rows + rows
+    order = torch.sort(key, stable=True)[1]
+    assert torch.equal(pc.data.cpu(), vals[order])
+    assert torch.equal(pc.indices.cpu().to(torch.int64), cols[order])
+    want_ptr = torch.zeros(n_panels * n_rows + 1, dtype=torch.int64)
+    want_ptr[1:] = torch.cumsum(torch.bincount(key, minlength=n_panels * n_rows), 0)
+    assert torch.equal(pc.indptr.cpu().to(torch.int64), want_ptr)
+    assert list(pc.panel_nnz) == [int(want_ptr[q * n_rows]) for q in range(n_panels + 1)]
