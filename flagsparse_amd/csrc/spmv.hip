@@ -38,30 +38,45 @@ __global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr
   if (threadIdx.x < FS_HIST_BINS) s_hist[threadIdx.x] = 0;
   __syncthreads();
   unsigned long long vmax = 0, vmin = ~0ull;
-  static_assert(FS_HIST_BINS <= 64, "bins are grouped with 6 ballots");
+  static_assert(FS_HIST_BINS <= 32, "bins are grouped with 5 ballots");
   // Whole waves run every iteration (the bound is wave-uniform), so the
   // ballots below see every active lane.
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63);
-  for (int64_t r0 = first; r0 < n_rows; r0 += stride) {
-    const int64_t r = r0 + (threadIdx.x & 63);
-    const bool valid = r < n_rows;
-    unsigned long long len = valid ? (unsigned long long)(rowptr[r + 1] - rowptr[r]) : 0ull;
-    int bin = len == 0 ? 0 : (64 - __clzll(len));
-    bin = bin < FS_HIST_BINS ? bin : FS_HIST_BINS - 1;
-    // lanes with the same bin: one of them adds the group's count
-    unsigned long long peers = __ballot(valid);
+  // kStatsUnroll rows per lane per step, all loads issued before any is used:
+  // with a few hundred workgroups, one dependent pair of loads per step left
+  // the kernel latency-bound (88 us for 4 M rows).
+  constexpr int kStatsUnroll = 8;
+  for (int64_t r0 = first; r0 < n_rows; r0 += kStatsUnroll * stride) {
+    unsigned long long lens[kStatsUnroll];
+    bool valids[kStatsUnroll];
 #pragma unroll
-    for (int b = 0; b < 6; ++b) {
-      const bool bit = (bin >> b) & 1;
-      const unsigned long long m = __ballot(bit);
-      peers &= bit ? m : ~m;
+    for (int u = 0; u < kStatsUnroll; ++u) {
+      const int64_t r = r0 + u * stride + (threadIdx.x & 63);
+      valids[u] = r < n_rows;
+      lens[u] = valids[u] ? (unsigned long long)(rowptr[r + 1] - rowptr[r]) : 0ull;
     }
-    const int below = __builtin_amdgcn_mbcnt_hi((unsigned)(peers >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)peers, 0u));
-    if (valid && below == 0) atomicAdd(&s_hist[bin], (unsigned)__popcll(peers));
-    if (valid) {
-      vmax = len > vmax ? len : vmax;
-      vmin = len < vmin ? len : vmin;
+#pragma unroll
+    for (int u = 0; u < kStatsUnroll; ++u) {
+      const bool valid = valids[u];
+      const unsigned long long len = lens[u];
+      int bin = len == 0 ? 0 : (64 - __clzll(len));
+      bin = bin < FS_HIST_BINS ? bin : FS_HIST_BINS - 1;
+      // lanes with the same bin: one of them adds the group's count
+      unsigned long long peers = __ballot(valid);
+      if (peers == 0) continue;  // wave-uniform
+#pragma unroll
+      for (int b = 0; b < 5; ++b) {
+        const bool bit = (bin >> b) & 1;
+        const unsigned long long m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      const int below = __builtin_amdgcn_mbcnt_hi((unsigned)(peers >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)peers, 0u));
+      if (valid && below == 0) atomicAdd(&s_hist[bin], (unsigned)__popcll(peers));
+      if (valid) {
+        vmax = len > vmax ? len : vmax;
+        vmin = len < vmin ? len : vmin;
+      }
     }
   }
   // Max / min over the workgroup first (wave butterflies, then 4 partials in
@@ -112,7 +127,16 @@ __global__ void check_init_kernel(const P* __restrict__ rowptr, int64_t n_rows, 
   if (k == 4) check[4] = 0ull;
 }
 
-template <class P, class I>
+template <class I>
+__device__ inline void check_range(I c, unsigned long long& lo, unsigned long long& hi) {
+  const unsigned long long v = (unsigned long long)(int64_t)c ^ kSignFlip;
+  lo = v < lo ? v : lo;
+  hi = v > hi ? v : hi;
+}
+
+// VEC: the indices are 16-byte aligned and read as 16-byte vectors, four per
+// lane in flight (64 bytes; 4-byte loads left the pass at 3.3 TB/s).
+template <class P, class I, bool VEC>
 __global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr, int64_t n_rows,
                                                     const I* __restrict__ cols, int64_t nnz,
                                                     unsigned long long* check) {
@@ -122,23 +146,30 @@ __global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr
   for (int64_t r = tid; r < n_rows; r += stride)
     bad += __builtin_nontemporal_load(rowptr + r + 1) < __builtin_nontemporal_load(rowptr + r) ? 1ull : 0ull;
   unsigned long long lo = ~0ull, hi = 0;
-  int64_t k = tid;
-  for (; k + 3 * stride < nnz; k += 4 * stride) {
-    I c[4];
+  int64_t done = 0;  // leading entries covered by the vector loop
+  if constexpr (VEC) {
+    constexpr int W = 16 / sizeof(I);
+    typedef I vec_t __attribute__((ext_vector_type(W)));
+    const vec_t* cv = reinterpret_cast<const vec_t*>(cols);
+    const int64_t nv = nnz / W;
+    int64_t k = tid;
+    for (; k + 3 * stride < nv; k += 4 * stride) {
+      vec_t c[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) c[u] = __builtin_nontemporal_load(cols + k + u * stride);
+      for (int u = 0; u < 4; ++u) c[u] = __builtin_nontemporal_load(cv + k + u * stride);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const unsigned long long v = (unsigned long long)(int64_t)c[u] ^ kSignFlip;
-      lo = v < lo ? v : lo;
-      hi = v > hi ? v : hi;
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int w = 0; w < W; ++w) check_range<I>(c[u][w], lo, hi);
     }
+    for (; k < nv; k += stride) {
+      const vec_t c = __builtin_nontemporal_load(cv + k);
+#pragma unroll
+      for (int w = 0; w < W; ++w) check_range<I>(c[w], lo, hi);
+    }
+    done = nv * W;
   }
-  for (; k < nnz; k += stride) {
-    const unsigned long long v = (unsigned long long)(int64_t)__builtin_nontemporal_load(cols + k) ^ kSignFlip;
-    lo = v < lo ? v : lo;
-    hi = v > hi ? v : hi;
-  }
+  for (int64_t k = done + tid; k < nnz; k += stride) check_range<I>(__builtin_nontemporal_load(cols + k), lo, hi);
   for (int off = 32; off > 0; off >>= 1) {
     bad += __shfl_xor(bad, off);
     const unsigned long long olo = __shfl_xor(lo, off), ohi = __shfl_xor(hi, off);
@@ -1068,9 +1099,12 @@ extern "C" int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_
     unsigned long long* st = static_cast<unsigned long long*>(stats_dev);
     hipLaunchKernelGGL(stats_init_kernel, dim3(1), dim3(64), 0, stream, st);
     FS_CHECK_LAUNCH("stats_init_kernel");
-    // few workgroups: each ends with a handful of global atomics on shared
-    // addresses, which serialise in L2 (2048 workgroups measured 52 us on 1M rows)
-    int64_t blocks = std::min<int64_t>(ceil_div(n_rows, 256), 256);
+    // Each workgroup ends with a handful of global atomics on shared addresses,
+    // which serialise in L2, so the grid is bounded: at least 2048 rows per
+    // workgroup (8 per lane), at most 1024 workgroups.  Measured on 4 M + 16.7 M
+    // rows (a power-law matrix and its 4-panel stacked copy): 256 / 512 / 1024 /
+    // 2048 / 4096 workgroups 173 / 113 / 104 / 135 / 177 us.
+    int64_t blocks = std::min<int64_t>(ceil_div(n_rows, 2048), 1024);
     if (ptr_t == FS_I32)
       hipLaunchKernelGGL((stats_kernel<int32_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
                          static_cast<const int32_t*>(indptr), n_rows, st);
@@ -1107,8 +1141,12 @@ extern "C" int fs_csr_check(const void* indptr, int ptr_t, const void* indices, 
     hipLaunchKernelGGL((check_init_kernel<P>), dim3(1), dim3(64), 0, stream, static_cast<const P*>(indptr),   \
                        n_rows, ck);                                                                           \
     FS_CHECK_LAUNCH("check_init_kernel");                                                                     \
-    hipLaunchKernelGGL((check_kernel<P, I>), dim3((unsigned)blocks), dim3(256), 0, stream,                    \
-                       static_cast<const P*>(indptr), n_rows, static_cast<const I*>(indices), nnz, ck);       \
+    if (reinterpret_cast<uintptr_t>(indices) % 16 == 0)                                                       \
+      hipLaunchKernelGGL((check_kernel<P, I, true>), dim3((unsigned)blocks), dim3(256), 0, stream,            \
+                         static_cast<const P*>(indptr), n_rows, static_cast<const I*>(indices), nnz, ck);     \
+    else                                                                                                      \
+      hipLaunchKernelGGL((check_kernel<P, I, false>), dim3((unsigned)blocks), dim3(256), 0, stream,           \
+                         static_cast<const P*>(indptr), n_rows, static_cast<const I*>(indices), nnz, ck);     \
     FS_CHECK_LAUNCH("check_kernel");                                                                          \
   } while (0)
   if (ptr_t == FS_I32 && idx_t == FS_I32) FS_CHECK_CASE(int32_t, int32_t);

@@ -515,12 +515,15 @@ def test_spmv_sell_other_stencils(device, monkeypatch, grid, dtype):
     _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[dtype])
 
 
+@pytest.mark.parametrize("offset", [0, 1], ids=["aligned", "offset"])
 @pytest.mark.parametrize("ptr_dtype", INDEX_DTYPES, ids=INDEX_IDS)
 @pytest.mark.parametrize("idx_dtype", INDEX_DTYPES, ids=INDEX_IDS)
-def test_spmv_structure_errors(device, ptr_dtype, idx_dtype):
+def test_spmv_structure_errors(device, ptr_dtype, idx_dtype, offset):
     """The reference's structure checks (spmv_csr.py:546-558), their messages
     and order, with each fault placed deep in arrays larger than one
-    workgroup's share so that the one-pass device check must find it."""
+    workgroup's share so that the one-pass device check must find it.
+    offset=1 passes indices that start one element into their storage (not
+    16-byte aligned), which takes the scalar-load path of the check."""
     n = 300_000
     per = 3
     indptr = torch.arange(0, (n + 1) * per, per, dtype=torch.int64)
@@ -529,7 +532,8 @@ def test_spmv_structure_errors(device, ptr_dtype, idx_dtype):
     x = torch.ones(n, dtype=torch.float32, device=device)
 
     def call(p, c, shape=(n, n)):
-        return fs.flagsparse_spmv_csr(data, c.to(idx_dtype).to(device), p.to(ptr_dtype).to(device), x, shape)
+        c_dev = torch.cat([c[:offset], c]).to(idx_dtype).to(device)[offset:]
+        return fs.flagsparse_spmv_csr(data, c_dev, p.to(ptr_dtype).to(device), x, shape)
 
     y = call(indptr, cols)  # valid: every row sums three ones
     assert torch.equal(y, torch.full((n,), 3.0, device=device))
