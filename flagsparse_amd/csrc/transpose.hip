@@ -444,7 +444,7 @@ struct Layout {
   size_t key_bytes, pos_bytes, rowid_bytes;
   int64_t n_sub, n_counts, n_partials;
   size_t off_keys_a, off_keys_b, off_pos_a, off_pos_b, off_rowid, off_counts, off_partials, total;
-  size_t off_key2 = 0;
+  size_t off_prow = 0, off_tile_rows = 0;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -718,7 +718,7 @@ __device__ inline int panel_of(int64_t c, int64_t width, double inv_width) {
 
 template <class I>
 __global__ __launch_bounds__(256) void panel_count_kernel(const I* __restrict__ cols, int64_t n, int64_t width,
-                                                          double inv_width, int n_panels, int64_t n_sub,
+                                                          double inv_width, int n_panels, int qbits, int64_t n_sub,
                                                           int64_t* __restrict__ counts) {
   __shared__ unsigned s_hist[kWavesPerBlock][kMaxPanels];
   const int lane = threadIdx.x & 63;
@@ -735,30 +735,67 @@ __global__ __launch_bounds__(256) void panel_count_kernel(const I* __restrict__ 
     c[ch] = e < n ? __builtin_nontemporal_load(cols + e) : (I)0;
   }
   wave_sync_t();
+  // Lanes of one panel find each other with qbits ballots; one LDS atomic per
+  // panel present in the chunk (an atomic per entry on a handful of addresses
+  // serialised: 137 us on C3).
 #pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch)
-    if (base + (int64_t)ch * 64 + lane < n) atomicAdd(&hist[panel_of((int64_t)c[ch], width, inv_width)], 1u);
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const bool valid = base + (int64_t)ch * 64 + lane < n;
+    const uint64_t active = __ballot(valid);
+    if (active == 0) break;
+    const int q = valid ? panel_of((int64_t)c[ch], width, inv_width) : 0;
+    uint64_t peers = active;
+    for (int b = 0; b < qbits; ++b) {
+      const bool bit = (q >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    if (valid && count_below_t(peers) == 0) atomicAdd(&hist[q], (unsigned)__popcll(peers));
+  }
   wave_sync_t();
   if (lane < n_panels) counts[(int64_t)lane * n_sub + sub] = hist[lane];
 }
 
+// Row of the first entry of every sub-tile (first r with rowptr[r + 1] > e),
+// one independent binary search per thread, so that the scatter waves start
+// from known bounds instead of each searching all rows.
+template <class P>
+__global__ __launch_bounds__(256) void tile_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t n_sub,
+                                                        int64_t* __restrict__ tile_row) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_sub) return;
+  const int64_t e = t * kSub;
+  int64_t lo = 0, hi = n_rows - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)rowptr[mid + 1] <= e)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  tile_row[t] = lo;
+}
+
 // One wave per sub-tile of kSub entries.
 //  1. row id of every entry into LDS: lane l walks entries [32l, 32l + 32)
-//     of the tile from one binary search (slot j + j/32 keeps that stride-32
-//     walk free of bank conflicts);
+//     of the tile from one binary search between the first rows of this and
+//     the next sub-tile (slot j + j/32 keeps that stride-32 walk free of bank
+//     conflicts);
 //  2. the global start of panel q's run in this sub-tile, offsets[q][sub]
 //     (exclusive scan of panel_count_kernel's counts), into LDS;
 //  3. chunk by chunk, rank = lanes of the same panel below this lane (peer
 //     masks from ceil(log2 n_panels) ballots) plus the panel's cursor, which
-//     keeps the partition stable.
+//     keeps the partition stable; value, column and row id go to the
+//     entry's slot of the stacked copy.
 template <class V, class I, class P, class RT>
 __global__ __launch_bounds__(64) void panel_scatter_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
                                                            const P* __restrict__ rowptr, int64_t n_rows, int64_t n,
                                                            int64_t width, double inv_width, int n_panels,
                                                            int qbits, int64_t n_sub,
                                                            const int64_t* __restrict__ offsets,
+                                                           const int64_t* __restrict__ tile_row,
                                                            V* __restrict__ p_vals, I* __restrict__ p_cols,
-                                                           int64_t* __restrict__ key2) {
+                                                           RT* __restrict__ prow) {
   constexpr int kItems = (int)(kSub / 64);
   __shared__ RT s_row[kSub + kSub / 32];
   __shared__ int64_t s_glob[kMaxPanels];
@@ -777,19 +814,9 @@ __global__ __launch_bounds__(64) void panel_scatter_kernel(const V* __restrict__
   }
   s_glob[lane] = lane < n_panels ? offsets[(int64_t)lane * n_sub + sub] : 0;
   s_cur[lane] = 0;
-  // rows of the tile's first and last entries bound every lane's search
-  if (lane < 2) {
-    const int64_t e = lane == 0 ? base : base + cnt - 1;
-    int64_t lo = 0, hi = n_rows - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if ((int64_t)rowptr[mid + 1] <= e)
-        lo = mid + 1;
-      else
-        hi = mid;
-    }
-    s_bounds[lane] = lo;
-  }
+  // rows of this and the next sub-tile's first entries bound every lane's search
+  if (lane == 0) s_bounds[0] = tile_row[sub];
+  if (lane == 1) s_bounds[1] = sub + 1 < n_sub ? tile_row[sub + 1] : n_rows - 1;
   wave_sync_t();
   {
     const int j0 = lane * kItems;
@@ -835,7 +862,7 @@ __global__ __launch_bounds__(64) void panel_scatter_kernel(const V* __restrict__
       const int64_t dst = s_glob[q] + (int64_t)s_cur[q] + rank;
       p_vals[dst] = vals[base + j];
       p_cols[dst] = c[ch];
-      key2[dst] = (int64_t)q * n_rows + (int64_t)s_row[j + (j >> 5)];
+      prow[dst] = s_row[j + (j >> 5)];
     }
     wave_sync_t();
     if (valid && rank == 0) s_cur[q] += (unsigned)__popcll(peers);
@@ -843,14 +870,53 @@ __global__ __launch_bounds__(64) void panel_scatter_kernel(const V* __restrict__
   }
 }
 
-template <class OP>
-__global__ __launch_bounds__(256) void panel_indptr_kernel(const int64_t* __restrict__ key2, int64_t n, int64_t n_out,
-                                                           OP* __restrict__ indptr) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k > n) return;
-  const int64_t prev = k > 0 ? key2[k - 1] : -1;
-  const int64_t cur = k < n ? key2[k] : n_out;
-  for (int64_t r = prev + 1; r <= cur; ++r) indptr[r] = (OP)k;
+// Stacked row pointer from the row id of every stacked entry.  The panel of
+// position k is the last panel whose start (the scanned count of its first
+// sub-tile) is <= k, so the entries carry only their row: 4 bytes per entry
+// when row ids fit, instead of a composite (panel, row) key.
+constexpr int kIndptrItems = 8;  // positions per thread (strided by 256 within the block's range)
+
+template <class OP, class RT>
+__global__ __launch_bounds__(256) void panel_indptr_kernel(const RT* __restrict__ prow, int64_t n, int64_t n_rows,
+                                                           int n_panels, const int64_t* __restrict__ offsets,
+                                                           int64_t n_sub, OP* __restrict__ indptr) {
+  __shared__ int64_t s_start[kMaxPanels + 1];
+  __shared__ int s_qrange[2];
+  if (threadIdx.x < n_panels) s_start[threadIdx.x] = offsets[(int64_t)threadIdx.x * n_sub];
+  __syncthreads();
+  const int64_t block_first = (int64_t)blockIdx.x * (256 * kIndptrItems);
+  auto panel_at = [&](int64_t e, int lo, int hi) -> int {  // last panel in [lo, hi] whose start is <= e
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_start[mid] <= e)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    return lo;
+  };
+  // panels of the block's first (minus one) and last positions bound every
+  // search; most blocks lie inside one panel and search nothing
+  if (threadIdx.x == 0) s_qrange[0] = panel_at(block_first > 0 ? block_first - 1 : 0, 0, n_panels - 1);
+  if (threadIdx.x == 64) s_qrange[1] = panel_at(block_first + 256 * kIndptrItems - 1, 0, n_panels - 1);
+  __syncthreads();
+  const int q_lo = s_qrange[0], q_hi = s_qrange[1];
+  auto composite = [&](int64_t e) -> int64_t {
+    if (e >= n) return (int64_t)n_panels * n_rows;
+    return (int64_t)panel_at(e, q_lo, q_hi) * n_rows + (int64_t)prow[e];
+  };
+  const int64_t base = block_first + threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kIndptrItems; ++i) {
+    // every lane computes its own key; the previous one comes from the lane
+    // below (lane 0 computes it)
+    const int64_t k = base + i * 256;
+    const int64_t cur = composite(k);
+    int64_t prev = __shfl_up(cur, 1);
+    if ((threadIdx.x & 63) == 0) prev = k > 0 ? composite(k - 1) : -1;
+    if (k <= n)
+      for (int64_t r = prev + 1; r <= cur; ++r) indptr[r] = (OP)k;
+  }
 }
 
 template <class OP>
@@ -870,20 +936,24 @@ int panelize_typed(const Layout& L, char* ws, int64_t n_rows, int64_t n_cols, in
   while ((1 << qbits) < n_panels) ++qbits;
   int64_t* counts = reinterpret_cast<int64_t*>(ws + L.off_counts);
   int64_t* partial = reinterpret_cast<int64_t*>(ws + L.off_partials);
-  int64_t* key2 = reinterpret_cast<int64_t*>(ws + L.off_key2);
+  RT* prow = reinterpret_cast<RT*>(ws + L.off_prow);
   hipLaunchKernelGGL((panel_count_kernel<I>), dim3((unsigned)ceil_div(L.n_sub, kWavesPerBlock)), dim3(256), 0, s,
-                     static_cast<const I*>(cols), nnz, width, inv_width, n_panels, L.n_sub, counts);
+                     static_cast<const I*>(cols), nnz, width, inv_width, n_panels, qbits, L.n_sub, counts);
   FS_CHECK_LAUNCH("panel_count_kernel");
   int rc = device_exclusive_scan(counts, L.n_counts, partial, s);
   if (rc != FS_OK) return rc;
+  int64_t* tile_row = reinterpret_cast<int64_t*>(ws + L.off_tile_rows);
+  hipLaunchKernelGGL((tile_rows_kernel<P>), dim3((unsigned)ceil_div(L.n_sub, 256)), dim3(256), 0, s,
+                     static_cast<const P*>(indptr), n_rows, L.n_sub, tile_row);
+  FS_CHECK_LAUNCH("tile_rows_kernel");
   hipLaunchKernelGGL((panel_scatter_kernel<V, I, P, RT>), dim3((unsigned)L.n_sub), dim3(64), 0, s,
                      static_cast<const V*>(vals), static_cast<const I*>(cols), static_cast<const P*>(indptr), n_rows,
-                     nnz, width, inv_width, n_panels, qbits, L.n_sub, counts, static_cast<V*>(p_vals),
-                     static_cast<I*>(p_cols), key2);
+                     nnz, width, inv_width, n_panels, qbits, L.n_sub, counts, tile_row, static_cast<V*>(p_vals),
+                     static_cast<I*>(p_cols), prow);
   FS_CHECK_LAUNCH("panel_scatter_kernel");
-  const int64_t n_out = (int64_t)n_panels * n_rows;
-  hipLaunchKernelGGL((panel_indptr_kernel<P>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, key2, nnz,
-                     n_out, static_cast<P*>(p_indptr));
+  hipLaunchKernelGGL((panel_indptr_kernel<P, RT>), dim3((unsigned)ceil_div(nnz + 1, 256 * kIndptrItems)), dim3(256), 0,
+                     s, prow, nnz,
+                     n_rows, n_panels, counts, L.n_sub, static_cast<P*>(p_indptr));
   FS_CHECK_LAUNCH("panel_indptr_kernel");
   return FS_OK;
 }
@@ -999,8 +1069,9 @@ extern "C" int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_col
   }
 }
 
-// Panel layout: the [panel][sub-tile] counts and their scan partials, then
-// the composite (panel, row) keys.
+// Panel layout: the [panel][sub-tile] counts and their scan partials, the
+// first row of every sub-tile, then the row id of every stacked entry (up to
+// 8 bytes).
 static Layout panel_layout(int64_t n_rows, int64_t n_panels, int64_t nnz) {
   (void)n_rows;
   Layout L{};
@@ -1012,7 +1083,9 @@ static Layout panel_layout(int64_t n_rows, int64_t n_panels, int64_t nnz) {
   o = align256(o + sizeof(int64_t) * L.n_counts);
   L.off_partials = o;
   o = align256(o + sizeof(int64_t) * (L.n_partials + 1));
-  L.off_key2 = o;  // also stages the n_panels + 1 panel starts afterwards
+  L.off_tile_rows = o;
+  o = align256(o + sizeof(int64_t) * L.n_sub);
+  L.off_prow = o;  // also stages the n_panels + 1 panel starts afterwards
   o = align256(o + 8 * (size_t)std::max<int64_t>(nnz, n_panels + 1));
   L.total = o;
   return L;
@@ -1059,7 +1132,7 @@ extern "C" int fs_csr_panelize(int val_t, int idx_t, int ptr_t, int64_t n_rows, 
   }
   if (rc != FS_OK) return rc;
   // the composite-key slot is free once the indptr is built (stream order)
-  int64_t* tmp = reinterpret_cast<int64_t*>(w + L.off_key2);
+  int64_t* tmp = reinterpret_cast<int64_t*>(w + L.off_prow);
   if (ptr_t == FS_I32) return read_panel_starts<int32_t>(p_indptr, n_rows, n_panels, tmp, panel_nnz, stream);
   return read_panel_starts<int64_t>(p_indptr, n_rows, n_panels, tmp, panel_nnz, stream);
 }
