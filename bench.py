@@ -239,13 +239,17 @@ def run(args):
             # SELL-64 copy of a short-row matrix with column locality (the stencil)
             args_abi = (
                 _lib.value_code(sell.vals.dtype), sell.col_code, _lib.index_code(sell.indptr.dtype), sell.layout,
-                sell.n_rows, _lib.ptr(sell.vals), _lib.ptr(sell.cols), _lib.ptr(sell.slice_ptr), _lib.ptr(sell.indptr),
-                _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(device),
+                sell.n_rows, _lib.ptr(sell.vals), _lib.ptr(sell.cols),
+                _lib.ptr(sell.table) if sell.table is not None else None, _lib.ptr(sell.slice_ptr),
+                _lib.ptr(sell.indptr), _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(device),
             )
             kernel_call = lambda: lib.fs_spmv_sell(*args_abi)  # noqa: E731
             extra["sell_stored_slots"] = sell.padded
             extra["sell_layout"] = "pair" if sell.layout == 1 else "slot"
-            extra["sell_column_storage"] = {0: "int32", 1: "int64", 2: "int16 offset from the row"}[sell.col_code]
+            extra["sell_column_storage"] = {0: "int32", 1: "int64", 2: "int16 offset from the row",
+                                            3: "uint8 code of the offset from the row"}[sell.col_code]
+            if sell.table is not None:
+                extra["sell_distinct_offsets"] = sell.n_codes
         pan = prep._panels
         if pan is not None:
             # column panels: the timed call is the whole panel sequence

@@ -149,11 +149,11 @@ def _declare(lib):
     lib.fs_sell_slots.restype = _i32
     lib.fs_sell_slots.argtypes = [_i32, _i64, _vp, _vp, _vp]
     lib.fs_sell_max_offset.restype = _i32
-    lib.fs_sell_max_offset.argtypes = [_i32, _i32, _i64, _vp, _vp, _vp, _vp]
+    lib.fs_sell_max_offset.argtypes = [_i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp]
     lib.fs_csr_to_sell.restype = _i32
-    lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_sell.restype = _i32
-    lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
 
 
 def load_library(path=None):

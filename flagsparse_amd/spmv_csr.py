@@ -18,6 +18,7 @@ import ctypes
 import os
 import time
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -381,59 +382,78 @@ def _sell_slice_ptr(indptr, n_rows, group):
     return slice_ptr, unrounded
 
 
-_SELL_I32, _SELL_I64, _SELL_D16 = 0, 1, 2  # enum fs_sell_index
+_SELL_I32, _SELL_I64, _SELL_D16, _SELL_C8 = 0, 1, 2, 3  # enum fs_sell_index
 _SELL_SLOT, _SELL_PAIR = 0, 1  # enum fs_sell_layout
 _SELL_GROUP = {_SELL_SLOT: 1, _SELL_PAIR: 2}  # slots stored side by side
+_SELL_CODES = 256  # uint8 codes: at most this many distinct offsets
 
 
-def _sell_max_offset(indices, indptr, n_rows):
-    """max |c - r| over the entries (one device->host sync)."""
+def _sell_offsets(indices, indptr, n_rows, want_bits):
+    """max |c - r| over the entries and, with want_bits, the sorted distinct
+    offsets c - r when every |c - r| <= 32767 (one device->host sync)."""
     if indices.numel() == 0:
-        return 0
-    out = torch.zeros(1, dtype=torch.int64, device=indices.device)
+        return 0, ([] if want_bits else None)
+    device = indices.device
+    out = torch.zeros(1 + (2048 // 2 if want_bits else 0), dtype=torch.int64, device=device)
+    bits = out[1:].view(torch.int32) if want_bits else None
     _lib.check(
         _lib.lib().fs_sell_max_offset(
             _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype), n_rows, _lib.ptr(indices),
-            _lib.ptr(indptr), _lib.ptr(out), _lib.stream_handle(indices.device),
+            _lib.ptr(indptr), _lib.ptr(out), _lib.ptr(bits) if want_bits else None, _lib.stream_handle(device),
         ),
         "fs_sell_max_offset",
     )
-    return int(out.item())
+    host = out.cpu()
+    max_off = int(host[0])
+    if not want_bits or max_off > 32767:
+        return max_off, None
+    words = host[1:].view(torch.int32).numpy().view(np.uint32)
+    present = np.nonzero(np.unpackbits(words.view(np.uint8), bitorder="little"))[0]
+    return max_off, (present.astype(np.int64) - 32768).tolist()
 
 
-def _sell_column_code(indices, indptr, n_rows, n_cols):
-    """Column storage of the SELL copy: int16 offsets c - r when every
-    |c - r| <= 32767 (off with FLAGSPARSE_SELL_DELTA=0), else int32 when
-    n_cols - 1 fits, else int64."""
-    if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0" and _sell_max_offset(indices, indptr, n_rows) <= 32767:
-        return _SELL_D16
-    return _SELL_I32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else _SELL_I64
+def _sell_column_code(indices, indptr, n_rows, n_cols, real_values=True):
+    """Column storage of the SELL copy, and the offsets the codes stand for:
+    uint8 codes when every |c - r| <= 32767 and at most 256 distinct offsets
+    occur (real values; off with FLAGSPARSE_SELL_CODES=0), else int16
+    offsets c - r when every |c - r| <= 32767 (off with
+    FLAGSPARSE_SELL_DELTA=0), else int32 when n_cols - 1 fits, else int64."""
+    if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0":
+        want_bits = real_values and os.environ.get("FLAGSPARSE_SELL_CODES") != "0"
+        max_off, offsets = _sell_offsets(indices, indptr, n_rows, want_bits)
+        if max_off <= 32767:
+            if offsets is not None and len(offsets) <= _SELL_CODES:
+                return _SELL_C8, offsets
+            return _SELL_D16, None
+    return (_SELL_I32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else _SELL_I64), None
 
 
 def _build_sell(data, indices, indptr, n_rows, n_cols, nnz):
     """The SELL-64 copy, or None when its stored slots would exceed
     _SELL_MAX_PADDING x nnz (rows too uneven) and it is not forced."""
-    col_code = _sell_column_code(indices, indptr, n_rows, n_cols)
+    col_code, offsets = _sell_column_code(indices, indptr, n_rows, n_cols, real_values=not data.dtype.is_complex)
     # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.076);
     # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
-    layout = _SELL_PAIR if col_code == _SELL_D16 and not data.dtype.is_complex else _SELL_SLOT
+    pair = col_code in (_SELL_D16, _SELL_C8) and not data.dtype.is_complex
+    layout = _SELL_PAIR if pair else _SELL_SLOT
     slice_ptr, stored = _sell_slice_ptr(indptr, n_rows, _SELL_GROUP[layout])
     if stored > _SELL_MAX_PADDING * max(1, nnz) and not _sell_forced():
         return None
-    return SellCsr(data, indices, indptr, slice_ptr, col_code, layout)
+    return SellCsr(data, indices, indptr, slice_ptr, col_code, layout, offsets)
 
 
 class SellCsr:
     """A as SELL-64: slices of 64 consecutive rows, built once per prepared
     matrix (fs_sell_slots, fs_csr_to_sell).  Columns are stored as chosen by
-    _sell_column_code; with int16 offsets, real values use the pair layout (a
-    row's consecutive slots side by side, loaded two at a time), otherwise
-    the slot layout.  The CSR row pointer of the prepared matrix supplies the
+    _sell_column_code; with offset codes or int16 offsets, real values use
+    the pair layout (a row's consecutive slots side by side, loaded two at a
+    time), otherwise the slot layout.  With codes, `table` holds the 256
+    offsets the codes stand for.  The CSR row pointer of the prepared matrix supplies the
     row lengths."""
 
-    __slots__ = ("vals", "cols", "col_code", "layout", "slice_ptr", "indptr", "n_rows", "padded")
+    __slots__ = ("vals", "cols", "col_code", "layout", "slice_ptr", "indptr", "n_rows", "padded", "table", "n_codes")
 
-    def __init__(self, data, indices, indptr, slice_ptr, col_code, layout):
+    def __init__(self, data, indices, indptr, slice_ptr, col_code, layout, offsets=None):
         device = data.device
         lib = _lib.lib()
         stream = _lib.stream_handle(device)
@@ -445,23 +465,39 @@ class SellCsr:
         self.n_rows = n_rows
         self.vals = torch.zeros(self.padded, dtype=data.dtype, device=device)
         self.col_code = col_code
-        col_dtype = {_SELL_D16: torch.int16, _SELL_I32: torch.int32, _SELL_I64: torch.int64}[col_code]
+        col_dtype = {_SELL_C8: torch.uint8, _SELL_D16: torch.int16, _SELL_I32: torch.int32,
+                     _SELL_I64: torch.int64}[col_code]
         self.cols = torch.zeros(self.padded, dtype=col_dtype, device=device)
+        self.table = None
+        self.n_codes = 0
+        lut = None
+        if col_code == _SELL_C8:
+            self.n_codes = len(offsets)
+            # code k stands for offsets[k]; the lookup maps offset d (at d + 32768) to its code
+            table = np.zeros(_SELL_CODES, dtype=np.int32)
+            table[: len(offsets)] = offsets
+            lut_host = np.zeros(65536, dtype=np.uint8)
+            lut_host[np.asarray(offsets, dtype=np.int64) + 32768] = np.arange(len(offsets), dtype=np.uint8)
+            self.table = torch.from_numpy(table).to(device)
+            lut = torch.from_numpy(lut_host).to(device)
         _lib.check(
             lib.fs_csr_to_sell(
                 _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype),
                 self.col_code, layout, n_rows, _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr),
-                _lib.ptr(self.slice_ptr), _lib.ptr(self.vals), _lib.ptr(self.cols), stream,
+                _lib.ptr(self.slice_ptr), _lib.ptr(lut) if lut is not None else None, _lib.ptr(self.vals),
+                _lib.ptr(self.cols), stream,
             ),
             "fs_csr_to_sell",
         )
+        del lut  # stream-ordered: the caching allocator reuses it only after the fill
 
     def spmv(self, x, y):
         _lib.check(
             _lib.lib().fs_spmv_sell(
                 _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype), self.layout,
-                self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols), _lib.ptr(self.slice_ptr), _lib.ptr(self.indptr),
-                _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(self.vals.device),
+                self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols),
+                _lib.ptr(self.table) if self.table is not None else None, _lib.ptr(self.slice_ptr),
+                _lib.ptr(self.indptr), _lib.ptr(x), _lib.ptr(y), _lib.stream_handle(self.vals.device),
             ),
             "fs_spmv_sell",
         )

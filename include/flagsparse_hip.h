@@ -39,9 +39,11 @@ extern "C" {
 enum fs_value_type { FS_F32 = 0, FS_F64 = 1, FS_C64 = 2, FS_C128 = 3 };
 /* Index types: SUPPORTED_INDEX_DTYPES (_common.py:29). */
 enum fs_index_type { FS_I32 = 0, FS_I64 = 1 };
-/* Column storage of a SELL-64 copy: absolute int32 / int64, or the int16
- * offset c - r from the entry's row (banded matrices, |c - r| <= 32767). */
-enum fs_sell_index { FS_SELL_I32 = 0, FS_SELL_I64 = 1, FS_SELL_D16 = 2 };
+/* Column storage of a SELL-64 copy: absolute int32 / int64, the int16
+ * offset c - r from the entry's row (banded matrices, |c - r| <= 32767), or
+ * a uint8 code of that offset into a table of at most 256 offsets (matrices
+ * with few distinct offsets, such as stencils; pair layout only). */
+enum fs_sell_index { FS_SELL_I32 = 0, FS_SELL_I64 = 1, FS_SELL_D16 = 2, FS_SELL_C8 = 3 };
 /* Entry order inside a SELL-64 slice: one slot of 64 rows after another, or
  * pairs of a row's consecutive slots side by side (real values only). */
 enum fs_sell_layout { FS_SELL_SLOT = 0, FS_SELL_PAIR = 1 };
@@ -262,28 +264,37 @@ int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
  *
  * fs_sell_slots writes slots[s] (device, int64, n_slices).
  * fs_sell_max_offset raises *max_dev (device, caller-initialised to 0) to
- * the largest |c - r| over the entries (c = column, r = row).
+ * the largest |c - r| over the entries (c = column, r = row).  When
+ * offset_bits_dev is not null (2048 uint32 words of device memory,
+ * caller-zeroed) it also sets bit d + 32768 for every offset d = c - r with
+ * |d| <= 32767.
  * fs_csr_to_sell writes the values and the columns into buffers of
  * slice_ptr[n_slices] entries, as sell_idx_t: FS_SELL_I32 / FS_SELL_I64
- * (absolute, wide enough for n_cols - 1) or FS_SELL_D16 (int16 c - r; the
- * caller has checked fs_sell_max_offset <= 32767).
+ * (absolute, wide enough for n_cols - 1), FS_SELL_D16 (int16 c - r; the
+ * caller has checked fs_sell_max_offset <= 32767) or FS_SELL_C8 (uint8
+ * code_lut[c - r + 32768]; code_lut is 65536 bytes of device memory that map
+ * every offset present to its index in the code table; FS_SELL_PAIR only).
+ * code_lut is ignored for the other column storages.
  * fs_spmv_sell computes y = A x from the copy; row lengths come from the
- * CSR indptr (ptr_t).  Rows may hold up to 2^31 - 1 entries.
+ * CSR indptr (ptr_t).  With FS_SELL_C8, code_table holds 256 int32 offsets
+ * (device memory; entry k is the offset of code k); otherwise it is ignored.
+ * Rows may hold up to 2^31 - 1 entries.
  * None of the three synchronises `stream`.
  */
 int fs_sell_slots(int ptr_t, int64_t n_rows, const void* indptr,
                   int64_t* slots_dev, hipStream_t stream);
 int fs_sell_max_offset(int idx_t, int ptr_t, int64_t n_rows, const void* cols,
                        const void* indptr, unsigned long long* max_dev,
-                       hipStream_t stream);
+                       unsigned* offset_bits_dev, hipStream_t stream);
 int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t,
                    int layout, int64_t n_rows, const void* vals, const void* cols,
                    const void* indptr, const int64_t* slice_ptr,
-                   void* sell_vals, void* sell_cols, hipStream_t stream);
+                   const void* code_lut, void* sell_vals, void* sell_cols,
+                   hipStream_t stream);
 int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
                  const void* sell_vals, const void* sell_cols,
-                 const int64_t* slice_ptr, const void* indptr,
-                 const void* x, void* y, hipStream_t stream);
+                 const int32_t* code_table, const int64_t* slice_ptr,
+                 const void* indptr, const void* x, void* y, hipStream_t stream);
 
 #ifdef __cplusplus
 }

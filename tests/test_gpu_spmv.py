@@ -329,15 +329,28 @@ def _dropped(data, indices, indptr, shape, frac, seed):
     return data[keep].contiguous(), indices[keep].contiguous(), p, shape
 
 
-@pytest.mark.parametrize("delta", ["1", "0"], ids=["int16-offsets", "int32-columns"])
+# column storage of the SELL copy -> (FLAGSPARSE_SELL_DELTA, FLAGSPARSE_SELL_CODES)
+_SELL_STORAGE_ENV = {"codes": ("1", "1"), "int16": ("1", "0"), "int32": ("0", "1")}
+
+
+def _sell_cols_dtype(storage, dtype):
+    """dtype of the SELL copy's columns for a stencil-like matrix: uint8 codes
+    are for real values; complex values keep int16 offsets."""
+    if storage == "int32":
+        return torch.int32
+    return torch.uint8 if storage == "codes" and not dtype.is_complex else torch.int16
+
+
+@pytest.mark.parametrize("storage", ["codes", "int16", "int32"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
-def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, delta):
+def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, storage):
     """A prepared 27-point stencil (64^3, 262,144 rows) gets the SELL-64 copy
     by itself and matches the oracle on sampled rows and the row-block stream
     kernel to within rounding; one-shot calls keep the CSR kernels."""
     for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS"):
         monkeypatch.delenv(k, raising=False)
-    monkeypatch.setenv("FLAGSPARSE_SELL_DELTA", delta)
+    monkeypatch.setenv("FLAGSPARSE_SELL_DELTA", _SELL_STORAGE_ENV[storage][0])
+    monkeypatch.setenv("FLAGSPARSE_SELL_CODES", _SELL_STORAGE_ENV[storage][1])
     data, indices, indptr, sh = S.stencil27(64, torch.float64, torch.int32, device, seed=5)
     if dtype == torch.complex64:
         imag = S.vector(data.numel(), torch.float64, device, seed=6)
@@ -347,11 +360,13 @@ def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, delta):
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
     assert prep.kernel_name == "sell"
     # 27 entries per interior row: 28 stored slots with pairs (real values with
-    # int16 offsets), 27 with slots
-    pair = delta == "1" and not dtype.is_complex
+    # offset codes or int16 offsets), 27 with slots
+    pair = storage != "int32" and not dtype.is_complex
     assert prep._sell.layout == (1 if pair else 0)
     assert prep._sell.padded <= (1.07 if pair else 1.03) * data.numel()
-    assert prep._sell.cols.dtype == (torch.int16 if delta == "1" else torch.int32)
+    assert prep._sell.cols.dtype == _sell_cols_dtype(storage, dtype)
+    if prep._sell.cols.dtype == torch.uint8:
+        assert prep._sell.n_codes == 27
     x = S.vector(sh[1], dtype, device, seed=7)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=prep))  # deterministic
@@ -381,16 +396,17 @@ def test_spmv_sell_not_chosen_without_locality_or_with_padding(device, monkeypat
     assert prep.kernel_name != "sell"
 
 
-@pytest.mark.parametrize("delta", ["1", "0"], ids=["int16-offsets", "absolute-columns"])
+@pytest.mark.parametrize("storage", ["int16", "int32"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
-def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype, delta):
+def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype, storage):
     """Rows of one slice with different lengths (1..7 entries, so odd lengths
     leave half-used pairs too).  Every row references only columns n..2n-1;
     x is infinite on columns 0..n-1, which is where a padding entry points
     (column 0, or offset 0 = the row's own index).  A padding entry that was
     gathered and multiplied would turn its row into nan; no row may."""
     monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
-    monkeypatch.setenv("FLAGSPARSE_SELL_DELTA", delta)
+    monkeypatch.setenv("FLAGSPARSE_SELL_DELTA", _SELL_STORAGE_ENV[storage][0])
+    monkeypatch.setenv("FLAGSPARSE_SELL_CODES", _SELL_STORAGE_ENV[storage][1])
     n = 256
     lengths = torch.tensor([(r % 7) + 1 for r in range(n)], dtype=torch.int64, device=device)
     indptr = torch.zeros(n + 1, dtype=torch.int32, device=device)
@@ -405,7 +421,7 @@ def test_spmv_sell_padding_never_multiplied(device, monkeypatch, dtype, delta):
     x[:n] = float("inf")
     prep = fs.prepare_spmv_csr(data, indices, indptr, (n, 2 * n))
     assert prep.kernel_name == "sell" and prep._sell.padded > data.numel()
-    assert prep._sell.cols.dtype == (torch.int16 if delta == "1" else torch.int32)
+    assert prep._sell.cols.dtype == _sell_cols_dtype(storage, dtype)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert torch.equal(y, lengths.to(dtype))
 
@@ -501,13 +517,15 @@ def _grid_stencil(dims, offsets, dtype, device):
 )
 def test_spmv_sell_other_stencils(device, monkeypatch, grid, dtype):
     """7-point 3D and 5-point 2D stencils (262,144 rows) also get the SELL copy
-    (int16 offsets, pair layout) and match the oracle on sampled rows."""
-    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS", "FLAGSPARSE_SELL_DELTA"):
+    (offset codes, pair layout) and match the oracle on sampled rows."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS", "FLAGSPARSE_SELL_DELTA",
+              "FLAGSPARSE_SELL_CODES"):
         monkeypatch.delenv(k, raising=False)
     dims, offsets = grid
     data, indices, indptr, sh = _grid_stencil(dims, offsets, dtype, device)
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
-    assert prep.kernel_name == "sell" and prep._sell.layout == 1 and prep._sell.cols.dtype == torch.int16
+    assert prep.kernel_name == "sell" and prep._sell.layout == 1 and prep._sell.cols.dtype == torch.uint8
+    assert prep._sell.n_codes == len(offsets)
     x = S.vector(sh[1], dtype, device, seed=22)
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     gen = np.random.default_rng(5)
@@ -605,3 +623,81 @@ def test_panelize_matches_stable_partition(device, idx_dtype, n_panels, shape):
     want_ptr[1:] = torch.cumsum(torch.bincount(key, minlength=n_panels * n_rows), 0)
     assert torch.equal(pc.indptr.cpu().to(torch.int64), want_ptr)
     assert list(pc.panel_nnz) == [int(want_ptr[q * n_rows]) for q in range(n_panels + 1)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("n_offsets", [1, 255, 256, 257])
+def test_spmv_sell_offset_codes_limit(device, monkeypatch, dtype, n_offsets):
+    """Rows whose entries sit at offsets drawn from a set of K distinct offsets
+    in [-1000, 1000]: with K <= 256 the SELL copy stores uint8 codes, with
+    K = 257 int16 offsets.  The code path gathers the same x entries and sums
+    in the same order as the int16 path, so the results are bit-identical;
+    both match the oracle."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    monkeypatch.delenv("FLAGSPARSE_SELL_DELTA", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SELL_CODES", raising=False)
+    n = 20_000
+    gen = np.random.default_rng(n_offsets)
+    offsets = np.sort(gen.choice(np.arange(-1000, 1001), n_offsets, replace=False))
+    per = min(4, n_offsets)
+    rows, cols = [], []
+    for r in range(n):
+        picks = sorted({int(offsets[(per * r + j) % n_offsets]) for j in range(per)})
+        for d in picks:
+            if 0 <= r + d < n:
+                rows.append(r)
+                cols.append(r + d)
+    rows = np.asarray(rows)
+    indptr = torch.zeros(n + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(torch.bincount(torch.from_numpy(rows), minlength=n), 0)
+    indices = torch.tensor(cols, dtype=torch.int32, device=device)
+    indptr = indptr.to(torch.int32).to(device)
+    data = S.vector(indices.numel(), dtype, device, seed=31)
+    x = S.vector(n, dtype, device, seed=32)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, (n, n))
+    assert prep.kernel_name == "sell" and prep._sell.layout == 1
+    if n_offsets <= 256:
+        assert prep._sell.cols.dtype == torch.uint8 and prep._sell.n_codes == n_offsets
+    else:
+        assert prep._sell.cols.dtype == torch.int16
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    monkeypatch.setenv("FLAGSPARSE_SELL_CODES", "0")
+    prep16 = fs.prepare_spmv_csr(data, indices, indptr, (n, n))
+    assert prep16._sell.cols.dtype == torch.int16
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=prep16))
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), (n, n))
+    assert rel_err(np_(y), ref) <= REL_TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
+def test_spmv_sell_codes_padding_never_multiplied(device, monkeypatch, dtype):
+    """With offset codes a padding entry holds code 0, the smallest offset.
+    Row 0 alone has offset 0 (column 0); every row has 1..7 entries at
+    offsets 1000..1006, so rows of one slice differ in length and leave
+    padding, including half-used pairs.  x is infinite on columns 1..n-1,
+    where the padding of rows 1..n-1 points (offset 0 = the row's own
+    index), and no real entry reads there.  A padding entry that was gathered
+    and multiplied would turn its row into nan; no row may."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
+    monkeypatch.delenv("FLAGSPARSE_SELL_DELTA", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SELL_CODES", raising=False)
+    n = 256
+    n_cols = n + 1007
+    cols, lengths = [], []
+    for r in range(n):
+        row = ([0] if r == 0 else []) + [r + 1000 + j for j in range((r % 7) + 1)]
+        cols.extend(row)
+        lengths.append(len(row))
+    lengths = torch.tensor(lengths, dtype=torch.int64, device=device)
+    indptr = torch.zeros(n + 1, dtype=torch.int32, device=device)
+    indptr[1:] = torch.cumsum(lengths, 0)
+    indices = torch.tensor(cols, dtype=torch.int32, device=device)
+    data = torch.ones(indices.numel(), dtype=dtype, device=device)
+    x = torch.ones(n_cols, dtype=dtype, device=device)
+    x[1:n] = float("inf")
+    prep = fs.prepare_spmv_csr(data, indices, indptr, (n, n_cols))
+    assert prep.kernel_name == "sell" and prep._sell.padded > data.numel()
+    assert prep._sell.cols.dtype == torch.uint8 and prep._sell.n_codes == 8
+    assert int(prep._sell.table[0]) == 0
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert torch.equal(y, lengths.to(dtype))
