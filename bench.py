@@ -51,7 +51,7 @@ DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 # roofline.traffic; configs not profiled with the current kernels report null.
 MEASURED_TRAFFIC = {
     "c1_spmv_uniform4096_f32_i32": 0.747e6,
-    "c2_spmv_stencil128_f64_i32": 641.5e6,
+    "c2_spmv_stencil128_f64_i32": 583.5e6,
     "c3_spmv_powerlaw4M_f32_i32": 1762.1e6,
     "c3_spmv_powerlaw4M_f32_i64": 1761.1e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
