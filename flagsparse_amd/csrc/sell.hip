@@ -192,14 +192,25 @@ __global__ __launch_bounds__(256) void sell_max_offset_kernel(const I* __restric
 // pointer; the loop runs to the slice's slot count with every slot past a
 // lane's own length masked off.  U slots are loaded before any is used.
 // Slot layout: complex values, and columns stored as int32 / int64.
+// Offset codes (I = uint8_t): code k stands for table[k], one of at most
+// kSellCodes int32 offsets c - r, staged in LDS per workgroup.
+constexpr int kSellCodes = 256;
+
 template <class V, class I, class P, int U, bool DELTA>
 __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ sell_vals,
                                                         const I* __restrict__ sell_cols,
+                                                        const int* __restrict__ table,
                                                         const int64_t* __restrict__ slice_ptr,
                                                         const P* __restrict__ rowptr, const V* __restrict__ x,
                                                         V* __restrict__ y, int64_t n_rows, int64_t n_slices) {
   using T = VT<V>;
   using A = typename T::acc;
+  constexpr bool kCodes = std::is_same<I, uint8_t>::value;
+  __shared__ int s_tab[kCodes ? kSellCodes : 1];
+  if constexpr (kCodes) {
+    s_tab[threadIdx.x] = table[threadIdx.x];  // blockDim.x == kSellCodes
+    __syncthreads();
+  }
   const int lane = threadIdx.x & 63;
   const int64_t slice = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (slice >= n_slices) return;  // whole wave
@@ -224,7 +235,12 @@ __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ se
     V xv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (j + u < len) xv[u] = DELTA ? x[r + (int64_t)c[u]] : x[c[u]];
+      if (j + u < len) {
+        if constexpr (kCodes)
+          xv[u] = x[r + s_tab[c[u]]];
+        else
+          xv[u] = DELTA ? x[r + (int64_t)c[u]] : x[c[u]];
+      }
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (j + u < len) acc = T::fma(v[u], xv[u], acc);
@@ -240,12 +256,9 @@ __global__ __launch_bounds__(256) void spmv_sell_kernel(const V* __restrict__ se
 // for f64 (0.132 ms).  UP groups are loaded before any is used.  The tail
 // of a row's last group may be padding: it is loaded with its group but
 // never gathered or multiplied.
-// With I = uint8_t the columns are codes into `table` (kSellCodes int32
-// offsets), staged in LDS: a stencil has a few dozen distinct offsets, and one
-// byte per entry instead of two is 9% less traffic (27-point 128^3 f64:
-// 0.1077 -> 0.0930 ms).
-constexpr int kSellCodes = 256;
-
+// With I = uint8_t the columns are codes into `table`, as in the slot
+// kernel: one byte per entry instead of two is 9% less traffic (27-point
+// 128^3 f64: 0.1077 -> 0.0930 ms).
 template <class V, class I, class P, int G, int UP, bool DELTA>
 __global__ __launch_bounds__(256) void spmv_sell_group_kernel(const V* __restrict__ sell_vals,
                                                               const I* __restrict__ sell_cols,
@@ -380,14 +393,11 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
     }
   }
   if (layout != FS_SELL_SLOT) return fail(FS_E_INVALID, "fs_spmv_sell: the pair layout is for real values");
-  if constexpr (std::is_same<I, uint8_t>::value) {
-    return fail(FS_E_INVALID, "fs_spmv_sell: offset codes need the pair layout (real values)");
-  } else {
   // Slots in flight: 16 for 4-byte values, 4 for wider ones.
   const int u = env_int("FLAGSPARSE_SELL_U", sizeof(V) <= 4 ? 16 : 4);
   auto go = [&](auto uc) {
     hipLaunchKernelGGL((spmv_sell_kernel<V, I, P, decltype(uc)::value, DELTA>), grid, dim3(256), 0, s,
-                       static_cast<const V*>(sv), static_cast<const I*>(sc), slice_ptr,
+                       static_cast<const V*>(sv), static_cast<const I*>(sc), table, slice_ptr,
                        static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y), n_rows,
                        n_slices);
   };
@@ -396,7 +406,6 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
   else go(std::integral_constant<int, 16>{});
   FS_CHECK_LAUNCH("spmv_sell_kernel");
   return FS_OK;
-  }
 }
 
 // Type dispatch: F is a functor template taking <V, I, P>.
@@ -483,8 +492,7 @@ extern "C" int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t, i
   if (!valid_types(val_t, idx_t, ptr_t) || !(sell_idx_t == FS_SELL_I32 || sell_idx_t == FS_SELL_I64 ||
                                              sell_idx_t == FS_SELL_D16 || sell_idx_t == FS_SELL_C8))
     return fail(FS_E_INVALID, "fs_csr_to_sell: bad type code");
-  if (sell_idx_t == FS_SELL_C8 && (layout != FS_SELL_PAIR || !code_lut))
-    return fail(FS_E_INVALID, "fs_csr_to_sell: offset codes need the pair layout and a code table");
+  if (sell_idx_t == FS_SELL_C8 && !code_lut) return fail(FS_E_INVALID, "fs_csr_to_sell: code_lut is null");
   if (!(layout == FS_SELL_SLOT || layout == FS_SELL_PAIR) ||
       (layout == FS_SELL_PAIR && (val_t == FS_C64 || val_t == FS_C128)))
     return fail(FS_E_INVALID, "fs_csr_to_sell: bad layout (the pair layout is for real values)");

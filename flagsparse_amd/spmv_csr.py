@@ -412,14 +412,19 @@ def _sell_offsets(indices, indptr, n_rows, want_bits):
     return max_off, (present.astype(np.int64) - 32768).tolist()
 
 
-def _sell_column_code(indices, indptr, n_rows, n_cols, real_values=True):
+def _sell_column_code(indices, indptr, n_rows, n_cols, value_bytes):
     """Column storage of the SELL copy, and the offsets the codes stand for:
     uint8 codes when every |c - r| <= 32767 and at most 256 distinct offsets
-    occur (real values; off with FLAGSPARSE_SELL_CODES=0), else int16
-    offsets c - r when every |c - r| <= 32767 (off with
-    FLAGSPARSE_SELL_DELTA=0), else int32 when n_cols - 1 fits, else int64."""
+    occur, for values of at most 8 bytes (off with FLAGSPARSE_SELL_CODES=0),
+    else int16 offsets c - r when every |c - r| <= 32767 (off with
+    FLAGSPARSE_SELL_DELTA=0), else int32 when n_cols - 1 fits, else int64.
+
+    Codes measured on the 27-point 128^3 stencil (ms, int16 -> codes): f32
+    0.0772 -> 0.0650, f64 0.1071 -> 0.0924, complex64 0.1387 -> 0.1194, but
+    complex128 0.1714 -> 0.1943 (the table lookup before each gather costs
+    more than the byte saved on a 17-byte entry)."""
     if os.environ.get("FLAGSPARSE_SELL_DELTA") != "0":
-        want_bits = real_values and os.environ.get("FLAGSPARSE_SELL_CODES") != "0"
+        want_bits = value_bytes <= 8 and os.environ.get("FLAGSPARSE_SELL_CODES") != "0"
         max_off, offsets = _sell_offsets(indices, indptr, n_rows, want_bits)
         if max_off <= 32767:
             if offsets is not None and len(offsets) <= _SELL_CODES:
@@ -431,7 +436,7 @@ def _sell_column_code(indices, indptr, n_rows, n_cols, real_values=True):
 def _build_sell(data, indices, indptr, n_rows, n_cols, nnz):
     """The SELL-64 copy, or None when its stored slots would exceed
     _SELL_MAX_PADDING x nnz (rows too uneven) and it is not forced."""
-    col_code, offsets = _sell_column_code(indices, indptr, n_rows, n_cols, real_values=not data.dtype.is_complex)
+    col_code, offsets = _sell_column_code(indices, indptr, n_rows, n_cols, data.element_size())
     # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.076);
     # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
     pair = col_code in (_SELL_D16, _SELL_C8) and not data.dtype.is_complex

@@ -42,7 +42,7 @@ enum fs_index_type { FS_I32 = 0, FS_I64 = 1 };
 /* Column storage of a SELL-64 copy: absolute int32 / int64, the int16
  * offset c - r from the entry's row (banded matrices, |c - r| <= 32767), or
  * a uint8 code of that offset into a table of at most 256 offsets (matrices
- * with few distinct offsets, such as stencils; pair layout only). */
+ * with few distinct offsets, such as stencils). */
 enum fs_sell_index { FS_SELL_I32 = 0, FS_SELL_I64 = 1, FS_SELL_D16 = 2, FS_SELL_C8 = 3 };
 /* Entry order inside a SELL-64 slice: one slot of 64 rows after another, or
  * pairs of a row's consecutive slots side by side (real values only). */
@@ -273,7 +273,7 @@ int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
  * (absolute, wide enough for n_cols - 1), FS_SELL_D16 (int16 c - r; the
  * caller has checked fs_sell_max_offset <= 32767) or FS_SELL_C8 (uint8
  * code_lut[c - r + 32768]; code_lut is 65536 bytes of device memory that map
- * every offset present to its index in the code table; FS_SELL_PAIR only).
+ * every offset present to its index in the code table).
  * code_lut is ignored for the other column storages.
  * fs_spmv_sell computes y = A x from the copy; row lengths come from the
  * CSR indptr (ptr_t).  With FS_SELL_C8, code_table holds 256 int32 offsets

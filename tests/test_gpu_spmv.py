@@ -334,15 +334,16 @@ _SELL_STORAGE_ENV = {"codes": ("1", "1"), "int16": ("1", "0"), "int32": ("0", "1
 
 
 def _sell_cols_dtype(storage, dtype):
-    """dtype of the SELL copy's columns for a stencil-like matrix: uint8 codes
-    are for real values; complex values keep int16 offsets."""
-    if storage == "int32":
-        return torch.int32
-    return torch.uint8 if storage == "codes" and not dtype.is_complex else torch.int16
+    """dtype of the SELL copy's columns for a stencil-like matrix: codes are
+    for values of at most 8 bytes (complex128 keeps int16 offsets)."""
+    if storage == "codes" and dtype.itemsize > 8:
+        return torch.int16
+    return {"codes": torch.uint8, "int16": torch.int16, "int32": torch.int32}[storage]
 
 
 @pytest.mark.parametrize("storage", ["codes", "int16", "int32"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64, torch.complex128],
+                         ids=["f32", "f64", "c64", "c128"])
 def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, storage):
     """A prepared 27-point stencil (64^3, 262,144 rows) gets the SELL-64 copy
     by itself and matches the oracle on sampled rows and the row-block stream
