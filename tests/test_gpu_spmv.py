@@ -626,9 +626,10 @@ def test_panelize_matches_stable_partition(device, idx_dtype, n_panels, shape):
     assert list(pc.panel_nnz) == [int(want_ptr[q * n_rows]) for q in range(n_panels + 1)]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64], ids=["i32", "i64"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
 @pytest.mark.parametrize("n_offsets", [1, 255, 256, 257])
-def test_spmv_sell_offset_codes_limit(device, monkeypatch, dtype, n_offsets):
+def test_spmv_sell_offset_codes_limit(device, monkeypatch, dtype, n_offsets, index_dtype):
     """Rows whose entries sit at offsets drawn from a set of K distinct offsets
     in [-1000, 1000]: with K <= 256 the SELL copy stores uint8 codes, with
     K = 257 int16 offsets.  The code path gathers the same x entries and sums
@@ -651,12 +652,12 @@ def test_spmv_sell_offset_codes_limit(device, monkeypatch, dtype, n_offsets):
     rows = np.asarray(rows)
     indptr = torch.zeros(n + 1, dtype=torch.int64)
     indptr[1:] = torch.cumsum(torch.bincount(torch.from_numpy(rows), minlength=n), 0)
-    indices = torch.tensor(cols, dtype=torch.int32, device=device)
-    indptr = indptr.to(torch.int32).to(device)
+    indices = torch.tensor(cols, dtype=index_dtype, device=device)
+    indptr = indptr.to(index_dtype).to(device)
     data = S.vector(indices.numel(), dtype, device, seed=31)
     x = S.vector(n, dtype, device, seed=32)
     prep = fs.prepare_spmv_csr(data, indices, indptr, (n, n))
-    assert prep.kernel_name == "sell" and prep._sell.layout == 1
+    assert prep.kernel_name == "sell" and prep._sell.layout == (0 if dtype.is_complex else 1)
     if n_offsets <= 256:
         assert prep._sell.cols.dtype == torch.uint8 and prep._sell.n_codes == n_offsets
     else:
