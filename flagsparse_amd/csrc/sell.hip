@@ -107,9 +107,11 @@ __global__ __launch_bounds__(256) void sell_fill_kernel(const V* __restrict__ va
   const int64_t base = slice_ptr[slice];
   const int64_t row0 = slice * kSellRows;
   // Entry-major: loads are coalesced, stores scattered over the slice's slots.
-  // (Lanes walking the output slots instead, with coalesced stores and
-  // scattered loads, measured 1.0 ms against 0.55 ms on the 27-point 128^3
-  // stencil.)  Padding is the caller's zero fill.
+  // Measured against it on the 27-point 128^3 stencil (0.55 ms, plus 0.08 ms
+  // for the caller's zero fill of the padding): lanes walking the output
+  // slots with coalesced stores and scattered loads, 1.0 ms; the slice staged
+  // in LDS (one wave per workgroup, 24 KB), then slot-order stores with the
+  // padding written, 0.71 ms.
   for (int64_t e = ptr[0] + lane; e < ptr[kSellRows]; e += kSellRows) {
     const int lr = sell_local_row(ptr, e);
     const unsigned k = (unsigned)(e - ptr[lr]);  // rows hold < 2^31 entries
