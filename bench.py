@@ -400,8 +400,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(
-            json.dumps({"error": "this build runs on one GPU only; the path's multi-GPU sharding is described "
-                                 "in DESIGN.md and not implemented", "n_gpus": args.gpus}),
+            json.dumps({"error": "this build runs on one GPU only: sharding the path over several GPUs "
+                                 "is not implemented", "n_gpus": args.gpus}),
             flush=True,
         )
         sys.exit(2)
