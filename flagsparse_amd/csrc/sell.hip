@@ -374,9 +374,12 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
   const dim3 grid((unsigned)ceil_div(n_slices, 4));
   if constexpr (!VT<V>::complex) {
     if (layout == FS_SELL_PAIR) {
-      // pairs in flight: 4 for 8-byte values (f64 stencil: 0.1084 / 0.1074 / 0.1178 ms with
-      // 2 / 4 / 8), 8 for 4-byte ones (f32: 0.0852 / 0.0804 / 0.0756 ms)
-      const int up = env_int("FLAGSPARSE_SELL_UP", sizeof(V) <= 4 ? 8 : 4);
+      // pairs in flight: 8 for 4-byte values (f32 stencil with int16 offsets: 0.0852 /
+      // 0.0804 / 0.0756 ms with 2 / 4 / 8; with codes 0.0697 / 0.0675 / 0.0633); for 8-byte
+      // values 4 with int16 offsets (f64: 0.1084 / 0.1074 / 0.1178) and 2 with codes
+      // (0.0898 / 0.0921 / 0.1036)
+      constexpr bool kCodes = std::is_same<I, uint8_t>::value;
+      const int up = env_int("FLAGSPARSE_SELL_UP", sizeof(V) <= 4 ? 8 : (kCodes ? 2 : 4));
       auto go = [&](auto gc, auto uc) {
         hipLaunchKernelGGL((spmv_sell_group_kernel<V, I, P, decltype(gc)::value, decltype(uc)::value, DELTA>), grid,
                            dim3(256), 0, s, static_cast<const V*>(sv), static_cast<const I*>(sc), table,
