@@ -377,7 +377,7 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
       // pairs in flight: 8 for 4-byte values (f32 stencil with int16 offsets: 0.0852 /
       // 0.0804 / 0.0756 ms with 2 / 4 / 8; with codes 0.0697 / 0.0675 / 0.0633); for 8-byte
       // values 4 with int16 offsets (f64: 0.1084 / 0.1074 / 0.1178) and 2 with codes
-      // (0.0898 / 0.0921 / 0.1036)
+      // (0.0898 / 0.0921 / 0.1036; 1 pair: 0.1096).  16 pairs of f32 with codes: 0.0842.
       constexpr bool kCodes = std::is_same<I, uint8_t>::value;
       const int up = env_int("FLAGSPARSE_SELL_UP", sizeof(V) <= 4 ? 8 : (kCodes ? 2 : 4));
       auto go = [&](auto gc, auto uc) {
