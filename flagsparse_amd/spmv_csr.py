@@ -407,9 +407,15 @@ def _sell_offsets(indices, indptr, n_rows, want_bits):
     max_off = int(host[0])
     if not want_bits or max_off > 32767:
         return max_off, None
-    words = host[1:].view(torch.int32).numpy().view(np.uint32)
-    present = np.nonzero(np.unpackbits(words.view(np.uint8), bitorder="little"))[0]
-    return max_off, (present.astype(np.int64) - 32768).tolist()
+    return max_off, _offsets_from_bits(host[1:].view(torch.int32).numpy())
+
+
+def _offsets_from_bits(words):
+    """Sorted offsets d whose bit d + 32768 is set in 2048 32-bit words
+    (bit b of word w is offset 32 * w + b - 32768)."""
+    words = np.ascontiguousarray(words).view(np.uint32)
+    bits = np.unpackbits(words.astype("<u4").view(np.uint8), bitorder="little")
+    return (np.nonzero(bits)[0].astype(np.int64) - 32768).tolist()
 
 
 def _sell_column_code(indices, indptr, n_rows, n_cols, value_bytes):

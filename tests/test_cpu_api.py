@@ -291,3 +291,22 @@ def test_alpha_spmm_alg1_surface_and_validation_on_cpu():
         fs.flagsparse_alpha_spmm_alg1(d, i, None, torch.ones(2, 2), (1, 2))
     with pytest.raises(ValueError, match="must be CUDA tensors|CUDA"):
         fs.prepare_alpha_spmm_alg1(d, i, p, (1, 2))
+
+
+def test_sell_offsets_from_bits_matches_brute_force():
+    """The SELL offset set comes back from the device as 2048 32-bit words,
+    bit d + 32768 for offset d; decoding must return exactly the offsets set,
+    sorted, including both ends of the range and bits in every byte of a
+    word."""
+    import numpy as np
+
+    from flagsparse_amd.spmv_csr import _offsets_from_bits
+
+    gen = np.random.default_rng(7)
+    for offsets in ([], [0], [-32767, 32767], [-32768], sorted(gen.choice(np.arange(-32768, 32768), 300,
+                                                                         replace=False).tolist())):
+        words = np.zeros(2048, dtype=np.uint32)
+        for d in offsets:
+            b = d + 32768
+            words[b >> 5] |= np.uint32(1) << np.uint32(b & 31)
+        assert _offsets_from_bits(words.view(np.int32)) == sorted(offsets)
