@@ -171,10 +171,11 @@ class PreparedCsrSpmv:
             p = self._plan.plan
             # The SELL and panel copies are optional: when device memory cannot
             # hold one next to the caller's matrix, the CSR kernels run instead.
-            if _spmv_use_sell(p, self.kernel_indices, self.kernel_indptr, self._one_shot):
+            locality = _spmv_sell_locality(p, self.kernel_indices, self.kernel_indptr, self._one_shot)
+            if locality is not None:
                 try:
                     self._sell = _build_sell(data, self.kernel_indices, self.kernel_indptr, self.n_rows,
-                                             self.n_cols, int(p.nnz))
+                                             self.n_cols, int(p.nnz), locality)
                 except torch.OutOfMemoryError:
                     self._sell = None
                     torch.cuda.empty_cache()
@@ -318,10 +319,13 @@ _SELL_MAX_PADDING = 1.03     # stored slots / nnz
 # the 128^3 f64 stencil with 5 / 10 / 30% of its entries dropped (stored
 # slots 1.10 / 1.16 / 1.30 x nnz) runs 0.0928 / 0.0950 / 0.0899 ms on the
 # copy against 0.1417 / 0.1364 / 0.1119 ms on the row-block stream kernel.
-# (At 30% the locality test already keeps the CSR kernel: dropped entries
-# misalign the k-th columns of neighbouring rows.)
 _SELL_MAX_PADDING_CODES = 1.35
 _SELL_MIN_LOCALITY = 0.5     # share of sampled (row, k) whose column is row r-1's + 1
+# With offset codes the copy wins at lower locality: the 128^3 stencil with
+# 30% of its entries dropped samples 0.245 (10%: 0.50, 20%: 0.34) and runs
+# 0.0899 ms on the copy against 0.1119 ms on the row-block stream kernel;
+# uniformly random and power-law columns sample 0.
+_SELL_MIN_LOCALITY_CODES = 0.2
 _SELL_SAMPLE_SLICES = 256
 _SELL_SAMPLE_K = 8
 
@@ -352,19 +356,22 @@ def _sell_locality(indices, indptr, n_rows):
     return float((hits.double() / total.double()).item())
 
 
-def _spmv_use_sell(plan, indices, indptr, one_shot):
-    """Whether a prepared matrix gets a SELL-64 copy.  FLAGSPARSE_SPMV_SELL=0/1
-    forces it off / on; otherwise only for a kept prepared matrix (the copy
-    costs more than one launch) whose rows are short (not the merge-path
-    kernel), with at least _SELL_MIN_SLICES slices and column locality.  The
-    padding bound is checked after the slot count."""
+def _spmv_sell_locality(plan, indices, indptr, one_shot):
+    """The sampled column locality when a prepared matrix may get a SELL-64
+    copy, else None.  FLAGSPARSE_SPMV_SELL=0/1 forces it off / on (1.0);
+    otherwise only for a kept prepared matrix (the copy costs more than one
+    launch) whose rows are short (not the merge-path kernel), with at least
+    _SELL_MIN_SLICES slices and a locality of at least
+    _SELL_MIN_LOCALITY_CODES.  _build_sell applies the bound that fits the
+    column storage, and the padding bound after the slot count."""
     env = os.environ.get("FLAGSPARSE_SPMV_SELL")
     n_rows = int(plan.n_rows)
     if env is not None:
-        return env == "1" and n_rows > 0
+        return 1.0 if env == "1" and n_rows > 0 else None
     if one_shot or plan.kernel == _lib.FS_KERNEL_MERGE or n_rows < 64 * _SELL_MIN_SLICES:
-        return False
-    return _sell_locality(indices, indptr, n_rows) >= _SELL_MIN_LOCALITY
+        return None
+    locality = _sell_locality(indices, indptr, n_rows)
+    return locality if locality >= _SELL_MIN_LOCALITY_CODES else None
 
 
 def _sell_slice_ptr(indptr, n_rows, group):
@@ -446,17 +453,21 @@ def _sell_column_code(indices, indptr, n_rows, n_cols, value_bytes):
     return (_SELL_I32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else _SELL_I64), None
 
 
-def _build_sell(data, indices, indptr, n_rows, n_cols, nnz):
-    """The SELL-64 copy, or None when its stored slots would exceed
-    _SELL_MAX_PADDING x nnz (_SELL_MAX_PADDING_CODES x nnz with offset codes;
-    rows too uneven) and it is not forced."""
+def _build_sell(data, indices, indptr, n_rows, n_cols, nnz, locality=1.0):
+    """The SELL-64 copy, or None, unless forced, when the sampled locality is
+    below _SELL_MIN_LOCALITY (_SELL_MIN_LOCALITY_CODES with offset codes) or
+    its stored slots would exceed _SELL_MAX_PADDING x nnz
+    (_SELL_MAX_PADDING_CODES x nnz with offset codes; rows too uneven)."""
     col_code, offsets = _sell_column_code(indices, indptr, n_rows, n_cols, data.element_size())
+    codes = col_code == _SELL_C8
+    if locality < (_SELL_MIN_LOCALITY_CODES if codes else _SELL_MIN_LOCALITY) and not _sell_forced():
+        return None
     # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.076);
     # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
     pair = col_code in (_SELL_D16, _SELL_C8) and not data.dtype.is_complex
     layout = _SELL_PAIR if pair else _SELL_SLOT
     slice_ptr, stored = _sell_slice_ptr(indptr, n_rows, _SELL_GROUP[layout])
-    bound = _SELL_MAX_PADDING_CODES if col_code == _SELL_C8 else _SELL_MAX_PADDING
+    bound = _SELL_MAX_PADDING_CODES if codes else _SELL_MAX_PADDING
     if stored > bound * max(1, nnz) and not _sell_forced():
         return None
     return SellCsr(data, indices, indptr, slice_ptr, col_code, layout, offsets)

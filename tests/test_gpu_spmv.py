@@ -387,26 +387,28 @@ def test_spmv_sell_chosen_for_stencils(device, monkeypatch, dtype, storage):
 
 def test_spmv_sell_not_chosen_without_locality_or_with_padding(device, monkeypatch):
     """Uniformly random columns (no locality) keep the CSR kernels.  Uneven
-    rows: a stencil with 10% of its entries dropped (stored slots ~1.16 x
-    nnz) gets the copy with offset codes (padding bound 1.35) but not with
-    int16 offsets (bound 1.03); with 60% dropped it gets none."""
+    rows: a stencil with 10% or 30% of its entries dropped (stored slots
+    ~1.16 / ~1.30 x nnz, sampled locality ~0.50 / ~0.25) gets the copy with
+    offset codes (bounds 1.35 and 0.2) but not with int16 offsets (bounds
+    1.03 and 0.5); with 60% dropped it gets none."""
     for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS", "FLAGSPARSE_SELL_DELTA",
               "FLAGSPARSE_SELL_CODES"):
         monkeypatch.delenv(k, raising=False)
     d, i, p, sh = S.uniform_rows(1 << 18, 1 << 18, 16, torch.float32, torch.int32, device, seed=8)
     assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell"
     stencil = S.stencil27(64, torch.float64, torch.int32, device, seed=5)
-    d, i, p, sh = _dropped(*stencil, 0.1, 9)
-    prep = fs.prepare_spmv_csr(d, i, p, sh)
-    assert prep.kernel_name == "sell" and prep._sell.cols.dtype == torch.uint8
-    x = S.vector(sh[1], torch.float64, device, seed=10)
-    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
-    gen = np.random.default_rng(3)
-    rows = sorted(set(gen.integers(0, sh[0], 2000).tolist()) | {0, sh[0] - 1})
-    _sampled_rows_check(d, i, p, sh, x, y, rows, REL_TOL[torch.float64])
-    monkeypatch.setenv("FLAGSPARSE_SELL_CODES", "0")
-    assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell"
-    monkeypatch.delenv("FLAGSPARSE_SELL_CODES")
+    for frac in (0.1, 0.3):
+        d, i, p, sh = _dropped(*stencil, frac, 9)
+        prep = fs.prepare_spmv_csr(d, i, p, sh)
+        assert prep.kernel_name == "sell" and prep._sell.cols.dtype == torch.uint8, frac
+        x = S.vector(sh[1], torch.float64, device, seed=10)
+        y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+        gen = np.random.default_rng(3)
+        rows = sorted(set(gen.integers(0, sh[0], 2000).tolist()) | {0, sh[0] - 1})
+        _sampled_rows_check(d, i, p, sh, x, y, rows, REL_TOL[torch.float64])
+        monkeypatch.setenv("FLAGSPARSE_SELL_CODES", "0")
+        assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell", frac
+        monkeypatch.delenv("FLAGSPARSE_SELL_CODES")
     d, i, p, sh = _dropped(*stencil, 0.6, 9)
     assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell"
 
