@@ -290,17 +290,18 @@ def run(args):
         plan.set_residency(route.kernel_indices, k, n_dense, route.data.dtype)  # as the public call does
         C = torch.empty((m, n_dense), dtype=data.dtype, device=device)
         lib = _lib.lib()
-        ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(data.dtype), plan.n_tiles, n_dense), device)
+        tile_items, n_tiles, part = plan.tiling(data.dtype, n_dense)
+        ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(data.dtype), n_tiles, n_dense), device)
         launch_indices, launch_plan = plan.launch_indices(route.kernel_indices, route.data.dtype)
         args_abi = (
             launch_plan, _lib.ptr(route.data), _lib.ptr(launch_indices), _lib.ptr(route.kernel_indptr),
-            _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.ptr(plan.part), plan.tile_items, plan.n_tiles,
+            _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.ptr(part), tile_items, n_tiles,
             _lib.ptr(ws), ws.numel(), _lib.stream_handle(device),
         )
         kernel_call = lambda: lib.fs_spmm_csr(*args_abi)  # noqa: E731
         bytes_alg = S.bytes_spmm(nnz, m, k, n_dense, vb, ib, pb)
         flops = S.flops_spmm(nnz, n_dense, complex_values)
-        kernel_name = "spmm_merge_kernel"
+        kernel_name = "spmm_group_kernel"
         extra.update(max_row_nnz=plan.csr.max_row_nnz, analysis_ms=round(analysis_ms, 3), n_dense=n_dense)
         if op != "non":
             # Public call including the per-call transpose (reference semantics).

@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "fs_spmm_workspace_bytes",
     "fs_spmm_tile_items",
     "fs_spmm_csr",
+    "fs_spmm_csr_strided",
     "fs_csr_transpose_workspace_bytes",
     "fs_csr_transpose",
     "fs_coo_to_csr_workspace_bytes",
@@ -127,6 +128,9 @@ def _declare(lib):
     lib.fs_spmm_csr.restype = _i32
     lib.fs_spmm_csr.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
                                 _vp, _i32, _i64, _vp, _sz, _vp]
+    lib.fs_spmm_csr_strided.restype = _i32
+    lib.fs_spmm_csr_strided.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64,
+                                        _i64, _vp, _i32, _i64, _vp, _sz, _vp]
     lib.fs_csr_transpose_workspace_bytes.restype = _sz
     lib.fs_csr_transpose_workspace_bytes.argtypes = [_i64, _i64, _i64]
     lib.fs_csr_transpose.restype = _i32

@@ -30,6 +30,7 @@ merge-path tiles of 512 items, and the column tiling the kernel uses.
 
 import torch
 
+from ._common import _compute_dtype
 from .spmm_csr import _SpmmPlan, _hip_spmm, _prepare_spmm_csr_matrix
 
 SUPPORTED_ALPHA_SPMM_ALG1_DTYPES = (torch.float32, torch.float64)
@@ -39,7 +40,6 @@ _TLE_REASON = (
 )
 _WAVE = 64
 _WAVES_PER_GROUP = 4
-_TILE_ITEMS = 512
 
 
 class PreparedAlphaSpmmAlg1:
@@ -143,20 +143,22 @@ def _launch_meta(prepared, B, plan, route):
     """The reference's meta keys, filled with this build's launch."""
     n_dense = int(B.shape[1])
     props = torch.cuda.get_device_properties(prepared.data.device)
-    # columns per lane and lane groups, as fs_spmm_csr chooses them
-    vec = 1
-    while vec < 2 and n_dense > _WAVE * vec:
-        vec *= 2
-    groups = 2 if n_dense <= (_WAVE // 2) * vec else 1
-    block_cols = (_WAVE // groups) * vec
-    n_tiles = int(plan.n_tiles) if plan is not None else 0
+    # lanes per B row and columns per lane, as fs_spmm_csr chooses them
+    epl = 16 // torch.empty(0, dtype=_compute_dtype(prepared.data.dtype)).element_size()
+    lanes = 8
+    while lanes < _WAVE and lanes * epl < n_dense:
+        lanes *= 2
+    vec = epl
+    block_cols = lanes * epl
+    tile_items, n_tiles = plan.tiling(prepared.data.dtype, n_dense)[:2] if plan is not None else (0, 0)
+    waves = -(-n_tiles // (_WAVE // lanes))
     return {
         "device_name": str(getattr(props, "name", "hip")),
         "sm_count": int(getattr(props, "multi_processor_count", 0) or 0),
         "block_size": _WAVE * _WAVES_PER_GROUP,
-        "block_rows": _TILE_ITEMS,  # merge items (row ends + nnz) per wave tile
+        "block_rows": tile_items * (_WAVE // lanes),  # merge items (row ends + nnz) per wave
         "block_cols": block_cols,
-        "grid_m": -(-n_tiles // _WAVES_PER_GROUP),
+        "grid_m": -(-waves // _WAVES_PER_GROUP),
         "grid_n": -(-n_dense // block_cols) if n_dense > 0 else 0,
         "warp_size": _WAVE,
         "factor": vec,

@@ -22,7 +22,7 @@ REPO = os.path.dirname(PKG)
 OUT = os.path.join(PKG, "libflagsparse_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["abi.cpp", "spmv.hip", "spmm.hip", "transpose.hip", "sell.hip"]
+SOURCES = ["abi.cpp", "spmv.hip", "spmm.hip", "spmm_group.hip", "transpose.hip", "sell.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -60,7 +60,7 @@ def build(verbose=False, extra_flags=None):
     """Compile every HIP source for gfx950 and link the shared library."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     extra = list(extra_flags or [])
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
         results = list(ex.map(lambda s: _compile(s, extra), SOURCES))
     objs = [r[0] for r in results]
     if verbose:

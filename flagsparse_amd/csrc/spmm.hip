@@ -1,4 +1,6 @@
-// spmm.hip — CSR SpMM (C = A B, dense B/C row-major) for gfx950.
+// spmm.hip — merge-path CSR SpMM (C = A B, dense B/C row-major) for gfx950,
+// the FLAGSPARSE_SPMM_KERNEL=merge variant (the default kernel and the C-ABI
+// entry points are in spmm_group.hip).
 //
 // Replaces the reference's base SpMM (spmm_csr.py:2684-2789 with
 // _spmm_csr_real_kernel / _spmm_csr_complex_kernel, spmm_csr.py:134-237)
@@ -401,38 +403,11 @@ int launch_spmm(const fs_csr_plan* plan, int vec, int groups, const void* vals, 
   return fail(FS_E_INVALID, "fs_spmm_csr: unsupported vector width");
 }
 
-}  // namespace fs
 
-using namespace fs;
-
-extern "C" int fs_spmm_tile_items(int val_t, int64_t n_dense) {
-  (void)val_t;
-  (void)n_dense;
-  return kSpmmTile;
-}
-
-extern "C" size_t fs_spmm_workspace_bytes(int val_t, int64_t n_tiles, int64_t n_dense) {
-  const size_t acc = (val_t == FS_C64 || val_t == FS_C128) ? sizeof(c64) : sizeof(double);
-  return (size_t)n_tiles * (size_t)n_dense * 2 * acc;
-}
-
-extern "C" int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
-                           const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense,
-                           const void* part_dev, int tile_items, int64_t n_tiles, void* ws, size_t ws_bytes,
-                           hipStream_t stream) {
-  if (!plan) return fail(FS_E_INVALID, "fs_spmm_csr: plan is null");
-  if (!valid_types(plan->val_t, plan->idx_t, plan->ptr_t)) return fail(FS_E_INVALID, "fs_spmm_csr: bad type code");
-  if (n_dense < 0 || ldb < 0 || ldc < 0) return fail(FS_E_INVALID, "fs_spmm_csr: negative size");
-  if (plan->n_rows == 0 || n_dense == 0) return FS_OK;
-  if (tile_items != kSpmmTile) return fail(FS_E_INVALID, "fs_spmm_csr: tile_items must come from fs_spmm_tile_items");
-  if (n_tiles != ceil_div(plan->n_rows + plan->nnz, kSpmmTile))
-    return fail(FS_E_INVALID, "fs_spmm_csr: n_tiles does not match the matrix");
-  if (ldc < n_dense || (plan->n_cols > 0 && ldb < n_dense))
-    return fail(FS_E_INVALID, "fs_spmm_csr: leading dimension smaller than n_dense");
-  if (!indptr || !C || !part_dev || (plan->nnz > 0 && (!vals || !cols || !B)))
-    return fail(FS_E_INVALID, "fs_spmm_csr: null pointer");
-  if (ws_bytes < fs_spmm_workspace_bytes(plan->val_t, n_tiles, n_dense) || (!ws && n_tiles > 0))
-    return fail(FS_E_WORKSPACE, "fs_spmm_csr: workspace too small");
+// Merge-path kernel entry (FLAGSPARSE_SPMM_KERNEL=merge): row-major B / C.
+int spmm_merge_dispatch(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
+                        const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense, const int64_t* part,
+                        int64_t n_tiles, void* ws, hipStream_t stream) {
   const size_t vsz[] = {4, 8, 8, 16};
   const size_t esz = vsz[plan->val_t];
   int vec = spmm_vec_for(plan->val_t, n_dense);
@@ -449,7 +424,6 @@ extern "C" int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void
     const int gv = std::atoi(e);
     if (gv == 1 || gv == 2) groups = gv;
   }
-  const int64_t* part = static_cast<const int64_t*>(part_dev);
   switch (plan->val_t) {
     case FS_F32: return launch_spmm<float>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
     case FS_F64: return launch_spmm<double>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
@@ -457,3 +431,5 @@ extern "C" int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void
     default: return launch_spmm<c64>(plan, vec, groups, vals, cols, indptr, B, ldb, C, ldc, n_dense, part, n_tiles, ws, stream);
   }
 }
+
+}  // namespace fs

@@ -199,8 +199,9 @@ def _check_segment_override(max_row_nnz, block_nnz, max_segments):
 
 
 # Skewed columns (a few columns hold much of the matrix, as in R-MAT / power-law
-# graphs): the two-columns-per-lane SpMM kernel then runs with at most
-# _SPMM_SKEW_WG_CAP workgroups per CU, which keeps more hot B rows in L2.
+# graphs): for B rows of at least 512 bytes fs_spmm_csr then runs the merge-path
+# kernel with at most _SPMM_SKEW_WG_CAP workgroups per CU, which keeps more hot
+# B rows in L2.
 _SPMM_SKEW_MIN_NNZ = 1 << 20
 _SPMM_SKEW_SHARE = 0.2   # share of nnz in the top 1% of columns (uniform columns: ~1%)
 _SPMM_SKEW_WG_CAP = 4
@@ -221,17 +222,24 @@ def _column_skew(indices, n_cols):
 
 
 class _SpmmPlan:
-    """Analysis + partition + workspace for one (matrix, N) SpMM."""
+    """Analysis + merge-path partitions + workspace sizing for one SpMM matrix.
 
-    __slots__ = ("csr", "part", "tile_items", "n_tiles", "_skew_checked", "_wide")
+    The sub-tile size of the SpMM kernel depends on the dense width (it sets
+    the lanes per B row), so partitions are built per tile size and cached."""
+
+    __slots__ = ("csr", "indptr", "_skew_checked", "_wide")
 
     def __init__(self, data, indices, indptr, n_rows, n_cols):
         self.csr = analyze_csr(data, indices, indptr, n_rows, n_cols)
-        self.tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(_compute_dtype(data.dtype)), 0))
-        self.n_tiles = self.csr.n_tiles(self.tile_items)
-        self.part = self.csr.partition(indptr, self.tile_items)
+        self.indptr = indptr
         self._skew_checked = False
         self._wide = None
+
+    def tiling(self, value_dtype, n_dense):
+        """(tile_items, n_tiles, partition) of the kernel fs_spmm_csr runs for
+        this value type and dense width."""
+        tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(_compute_dtype(value_dtype)), int(n_dense)))
+        return tile_items, self.csr.n_tiles(tile_items), self.csr.partition(self.indptr, tile_items)
 
     def launch_indices(self, indices, value_dtype):
         """(column indices, plan struct) a launch passes to fs_spmm_csr.
@@ -255,10 +263,11 @@ class _SpmmPlan:
         return wide_indices, wide_plan
 
     def set_residency(self, indices, n_cols, n_dense, value_dtype):
-        """Sets plan.spmm_wg_cap once, when a launch will use the two-columns-
-        per-lane kernel (N > 64, values of at most 8 bytes): only that kernel
-        reads the cap, so other launches skip the column count."""
-        if self._skew_checked or n_dense <= 64 or torch.empty(0, dtype=value_dtype).element_size() > 8:
+        """Sets plan.spmm_wg_cap once, when a launch has B rows of at least
+        512 bytes: for those, fs_spmm_csr picks its kernel by column skew (the
+        merge-path kernel, under this residency cap, on skewed columns).
+        Narrower launches never read it, so they skip the column count."""
+        if self._skew_checked or n_dense * torch.empty(0, dtype=value_dtype).element_size() < 512:
             return
         self._skew_checked = True
         if (
@@ -270,15 +279,20 @@ class _SpmmPlan:
 
 
 def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
-    """C = A @ B with dense row-major B (any row stride); returns C."""
+    """C = A @ B for a dense B of any non-negative strides (row-major,
+    column-major or strided views); returns C.
+
+    C is written in place when it is given with the compute dtype, else a
+    row-major C is allocated.  Strides go to the kernel as they are: no copy
+    of B or C is made for column-major layouts."""
     device = data.device
     n_dense = int(B.shape[1])
     cdt = _compute_dtype(data.dtype)
     data_c = data if data.dtype == cdt else data.to(cdt)
     B_c = B if B.dtype == cdt else B.to(cdt)
-    if B_c.stride(1) != 1:
+    if any(st < 0 for st in B_c.stride()):
         B_c = B_c.contiguous()
-    if C is None or C.dtype != cdt or C.stride(1) != 1:
+    if C is None or C.dtype != cdt:
         C_k = torch.empty((n_rows, n_dense), dtype=cdt, device=device)
     else:
         C_k = C
@@ -289,24 +303,25 @@ def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
     else:
         plan.set_residency(indices, int(plan.csr.plan.n_cols), n_dense, cdt)
         launch_indices, launch_plan = plan.launch_indices(indices, cdt)
+        tile_items, n_tiles, part = plan.tiling(cdt, n_dense)
         lib = _lib.lib()
-        ws = _lib.workspace(
-            lib.fs_spmm_workspace_bytes(_lib.value_code(cdt), plan.n_tiles, n_dense), device
-        )
+        ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(cdt), n_tiles, n_dense), device)
         _lib.check(
-            lib.fs_spmm_csr(
+            lib.fs_spmm_csr_strided(
                 launch_plan,
                 _lib.ptr(data_c),
                 _lib.ptr(launch_indices),
                 _lib.ptr(indptr),
                 _lib.ptr(B_c),
-                int(B_c.stride(0)) if B_c.shape[0] > 0 else n_dense,
+                int(B_c.stride(0)),
+                int(B_c.stride(1)),
                 _lib.ptr(C_k),
                 int(C_k.stride(0)),
+                int(C_k.stride(1)),
                 n_dense,
-                _lib.ptr(plan.part),
-                plan.tile_items,
-                plan.n_tiles,
+                _lib.ptr(part),
+                tile_items,
+                n_tiles,
                 _lib.ptr(ws),
                 ws.numel(),
                 _lib.stream_handle(device),
@@ -601,20 +616,13 @@ def _run_hip_route(prepared, B, *, route_name, display_name, timing=False, diagn
         end = torch.cuda.Event(enable_timing=True)
         start.record()
     plan = prepared.hip_plan()
-    if dense_layout == "col":
-        # Column-major B/C: run on the row-major views B^T^T; C is produced
-        # row-major and stored column-major.
-        C_row = _hip_spmm(
-            prepared.data, prepared.kernel_indices, prepared.kernel_indptr, B.contiguous(), prepared.n_rows, plan,
-            prepared.data.dtype,
-        )
-        C = _empty_dense_layout((prepared.n_rows, n_dense), prepared.data.dtype, prepared.data.device, "col")
-        C.copy_(C_row)
-    else:
-        C = _hip_spmm(
-            prepared.data, prepared.kernel_indices, prepared.kernel_indptr, B, prepared.n_rows, plan,
-            prepared.data.dtype,
-        )
+    # Column-major B / C go to the kernel with their strides (spmm_csr.py:134-176
+    # takes stride_bk / stride_bn / stride_cm / stride_cn the same way).
+    C = _empty_dense_layout((prepared.n_rows, n_dense), prepared.data.dtype, prepared.data.device, dense_layout)
+    C = _hip_spmm(
+        prepared.data, prepared.kernel_indices, prepared.kernel_indptr, B, prepared.n_rows, plan,
+        prepared.data.dtype, C=C,
+    )
     if timing:
         end.record()
         torch.cuda.synchronize()
@@ -632,15 +640,16 @@ def _run_hip_route(prepared, B, *, route_name, display_name, timing=False, diagn
         "output_layout": _dense_layout_name(C),
     }
     if diagnostics:
+        tiling = plan.tiling(prepared.data.dtype, n_dense)[:2] if plan is not None else (0, 0)
         meta["diagnostics"] = {
             "launch_config_scope": "matrix",
             "launch_config_count": 1,
             "bucket_count": 0,
             "long_row_count": 0,
-            "launch_version": "hip_merge_v1",
-            "kernel": "spmm_merge",
-            "tile_items": plan.tile_items if plan is not None else 0,
-            "n_tiles": plan.n_tiles if plan is not None else 0,
+            "launch_version": "hip_group_v1",
+            "kernel": "spmm_group",
+            "tile_items": tiling[0],
+            "n_tiles": tiling[1],
             "max_row_nnz": prepared.max_row_nnz,
             "dense_layout": dense_layout,
             "b_stride": meta["b_stride"],

@@ -230,7 +230,7 @@ def _spmm_opt_alg1_impl(data, indices, indptr, B, shape, prepared, out, return_t
             "symbolic_ms": symbolic_ms,
             "compute_ms": compute_ms,
             "op_total_ms": op_total_ms,
-            "long_part_count": int(plan.n_tiles) if plan is not None else 0,
+            "long_part_count": plan.tiling(prepared.data.dtype, B.shape[1])[1] if plan is not None else 0,
             "long_row_count": _long_row_count(plan),
             "bucket_count": 1 if plan is not None else 0,
         }
@@ -294,8 +294,8 @@ def flagsparse_spmm_csr_opt_alg2(data=None, indices=None, indptr=None, B=None, s
     op_total_ms = (symbolic_ms + compute_ms) if do_timing else None
     if return_meta:
         meta = {
-            "kernel": "spmm_merge",
-            "n_tiles": int(plan.n_tiles) if plan is not None else 0,
+            "kernel": "spmm_group",
+            "n_tiles": plan.tiling(prepared.data.dtype, B.shape[1])[1] if plan is not None else 0,
             "symbolic_ms": symbolic_ms,
             "compute_ms": compute_ms,
             "op_total_ms": op_total_ms,

@@ -155,9 +155,10 @@ int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
  * _triton_spmm_csr_impl + _spmm_csr_real_kernel / _spmm_csr_complex_kernel
  * (spmm_csr.py:2684-2789, 134-237).  fp32 accumulates in fp64 (the
  * reference upcasts data and B to fp64, spmm_csr.py:2720-2759).  The
- * matrix is walked along a merge path of tile_items items per tile
- * (partition from fs_csr_partition with the same tile size); rows that
- * cross tiles are finished by a fix-up pass using `ws`
+ * matrix is walked along a merge path of tile_items items per sub-tile:
+ * tile_items = fs_spmm_tile_items(val_t, n_dense) (it depends on the dense
+ * width), partition from fs_csr_partition with the same tile size.  Rows
+ * that cross sub-tiles are finished by a fix-up pass using `ws`
  * (fs_spmm_workspace_bytes bytes).
  */
 size_t fs_spmm_workspace_bytes(int val_t, int64_t n_tiles, int64_t n_dense);
@@ -167,6 +168,21 @@ int fs_spmm_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
                 int64_t ldc, int64_t n_dense, const void* part_dev,
                 int tile_items, int64_t n_tiles, void* ws, size_t ws_bytes,
                 hipStream_t stream);
+
+/*
+ * fs_spmm_csr with any element strides: B(k, n) = B[k * sbk + n * sbn],
+ * C(m, n) = C[m * scm + n * scn].  The reference's SpMM kernel takes the
+ * same four strides (spmm_csr.py:134-176: stride_bk, stride_bn, stride_cm,
+ * stride_cn), which is how its csr_base route serves column-major B / C
+ * (spmm_csr.py:585-639, 2090-2098).  Row-major operands with 16-byte
+ * aligned rows take vector loads / stores; other layouts element accesses.
+ * C's strides must not make two (row, column) pairs share an element.
+ */
+int fs_spmm_csr_strided(const fs_csr_plan* plan, const void* vals, const void* cols,
+                        const void* indptr, const void* B, int64_t sbk, int64_t sbn,
+                        void* C, int64_t scm, int64_t scn, int64_t n_dense,
+                        const void* part_dev, int tile_items, int64_t n_tiles,
+                        void* ws, size_t ws_bytes, hipStream_t stream);
 
 /*
  * Transpose (CSR -> CSR of A^T, conjugating values when conj != 0).

@@ -28,13 +28,26 @@ def _check(data, indices, indptr, shape, B, op, **kw):
     return C
 
 
-@pytest.fixture(params=["auto", "G1", "G2", "VEC2-G2", "VEC4-G1"])
+_LAYOUT_ENV = ("FLAGSPARSE_SPMM_KERNEL", "FLAGSPARSE_SPMM_LPR", "FLAGSPARSE_SPMM_WAVE_ITEMS", "FLAGSPARSE_SPMM_G",
+               "FLAGSPARSE_SPMM_VEC", "FLAGSPARSE_SPMM_XCD", "FLAGSPARSE_SPMM_WG_CAP")
+
+
+@pytest.fixture(params=["auto", "LPR8", "LPR16", "LPR64", "LPR16-WI256", "merge", "merge-VEC2-G2"])
 def lane_layout(request, monkeypatch):
-    """SpMM lane layout under test: lane groups per wave (G) and columns per lane (VEC)."""
-    monkeypatch.delenv("FLAGSPARSE_SPMM_G", raising=False)
-    monkeypatch.delenv("FLAGSPARSE_SPMM_VEC", raising=False)
+    """SpMM kernel and lane layout under test.  Lane-group kernel: lanes per
+    B row (LPR) and items per wave (WI, 256 gives sub-tiles of 32..256 items,
+    so rows cross sub-tiles often).  Merge-path kernel: lane groups per wave
+    (G) and columns per lane (VEC)."""
+    for k in _LAYOUT_ENV:
+        monkeypatch.delenv(k, raising=False)
     for part in request.param.split("-"):
-        if part.startswith("G"):
+        if part == "merge":
+            monkeypatch.setenv("FLAGSPARSE_SPMM_KERNEL", "merge")
+        elif part.startswith("LPR"):
+            monkeypatch.setenv("FLAGSPARSE_SPMM_LPR", part[3:])
+        elif part.startswith("WI"):
+            monkeypatch.setenv("FLAGSPARSE_SPMM_WAVE_ITEMS", part[2:])
+        elif part.startswith("G"):
             monkeypatch.setenv("FLAGSPARSE_SPMM_G", part[1:])
         elif part.startswith("VEC"):
             monkeypatch.setenv("FLAGSPARSE_SPMM_VEC", part[3:])
@@ -101,16 +114,20 @@ def test_spmm_deterministic(device):
     assert torch.equal(C1, C2)
 
 
-@pytest.mark.parametrize("lanes", [("1", "1"), ("2", "1"), ("1", "2")], ids=["VEC1-G1", "VEC2-G1", "VEC1-G2"])
+@pytest.mark.parametrize("lanes", [{"FLAGSPARSE_SPMM_LPR": "16"}, {"FLAGSPARSE_SPMM_LPR": "64"},
+                                   {"FLAGSPARSE_SPMM_KERNEL": "merge", "FLAGSPARSE_SPMM_VEC": "2"},
+                                   {"FLAGSPARSE_SPMM_KERNEL": "merge", "FLAGSPARSE_SPMM_G": "2"}],
+                         ids=["LPR16", "LPR64", "merge-VEC2", "merge-G2"])
 def test_spmm_xcd_column_tiles_bit_identical(device, monkeypatch, lanes):
     """The XCD-affine mapping of column tiles (1-D grid, tile = id % tiles)
     changes only which XCD runs a tile: results are bit-identical to the
     2-D grid, for 2, 4 and 8 column tiles and for other counts."""
-    vec, g = lanes
-    monkeypatch.setenv("FLAGSPARSE_SPMM_VEC", vec)
-    monkeypatch.setenv("FLAGSPARSE_SPMM_G", g)
+    for k in _LAYOUT_ENV:
+        monkeypatch.delenv(k, raising=False)
+    for k, v in lanes.items():
+        monkeypatch.setenv(k, v)
     d, i, p, sh = S.powerlaw(1 << 13, torch.float32, torch.int64, device, seed=4)
-    for n_dense in (64, 128, 200, 256, 512):
+    for n_dense in (64, 128, 200, 256, 512, 1024):
         B = S.dense(sh[1], n_dense, torch.float32, device, seed=n_dense)
         monkeypatch.setenv("FLAGSPARSE_SPMM_XCD", "1")
         C_xcd = fs.flagsparse_spmm_csr(d, i, p, B, sh)
@@ -204,11 +221,14 @@ def test_spmm_meta(device):
 @pytest.mark.parametrize("op", OPS)
 @pytest.mark.parametrize("layout", ["row", "col"])
 def test_spmm_route_api(device, alg, op, layout):
-    if layout == "col" and alg not in ("auto", "csr_base"):
-        pytest.skip("col-major is csr_base only")
     d, i, p, sh = S.random_csr(97, 65, 0.1, torch.float64, torch.int32, device, seed=3)
     prep = fs.prepare_spmm_csr_route(d, i, p, sh, op=op, alg=alg)
     B = S.dense(97 if op != "non" else 65, 40, torch.float64, device, seed=1)
+    if layout == "col" and alg not in ("auto", "csr_base"):
+        # the reference raises for col-major on any route but csr_base (spmm_csr.py:2095-2098)
+        with pytest.raises(fs.SpmmCsrAlgorithmUnavailable, match="only by csr_base"):
+            fs.flagsparse_spmm_csr_run(prep, B, dense_layout=layout)
+        return
     C, ms, meta = fs.flagsparse_spmm_csr_run(prep, B, dense_layout=layout, return_time=True, return_meta=True,
                                              timing=True, diagnostics=True)
     ref = O.spmm_csr_wide(np_(d), np_(i), np_(p), np_(B), sh, op=op)
@@ -224,10 +244,15 @@ def test_spmm_route_unavailable(device):
         fs.flagsparse_spmm_csr_run(prep, torch.randn(9, 4, device=device), alg="alpha_alg1_tle_opt")
 
 
+def _host(a):
+    return a if isinstance(a, np.ndarray) else np_(a)
+
+
 def _sampled_rows(data, indices, indptr, B, C, rows, tol):
-    """Oracle on a subset of rows; only the B rows they touch leave the GPU."""
-    p = np_(indptr).astype(np.int64)
-    d, c = np_(data), np_(indices).astype(np.int64)
+    """Oracle on a subset of rows; only the B rows they touch leave the GPU.
+    The CSR arrays may be device tensors or host numpy arrays."""
+    p = _host(indptr).astype(np.int64)
+    d, c = _host(data), _host(indices).astype(np.int64)
     sub_p, sub_d, sub_c = [0], [], []
     for r in rows:
         sub_d.append(d[p[r]:p[r + 1]])
@@ -257,14 +282,16 @@ def test_spmm_full_size_configs(device, config):
     C = fs.flagsparse_spmm_csr(d, i, p, B, sh, op=op)
     assert torch.equal(C, fs.flagsparse_spmm_csr(d, i, p, B, sh, op=op))
     if op != "non":
-        from flagsparse_amd import _csr
-
-        d, i, p, sh = _csr.transpose_csr(d, i, p, sh, conj=(op == "conj"))
-    lengths = (p[1:] - p[:-1]).to(torch.int64)
-    longest = int(torch.argmax(lengths).item())
+        # A^T / A^H from the CPU oracle's stable transpose, not the product's
+        d, i, p, sh = O.transpose_csr(np_(d), np_(i), np_(p), sh, conj=(op == "conj"))
+        lengths = np.diff(p.astype(np.int64))
+        longest = int(np.argmax(lengths))
+    else:
+        lengths = (p[1:] - p[:-1]).to(torch.int64)
+        longest = int(torch.argmax(lengths).item())
     gen = np.random.default_rng(1)
     rows = sorted(set(gen.integers(0, sh[0], 1500).tolist()) | {0, sh[0] - 1, longest})
-    _sampled_rows(d, i, p, B, C, rows, REL_TOL[d.dtype])
+    _sampled_rows(d, i, p, B, C, rows, REL_TOL[C.dtype])
 
 
 def test_spmm_skewed_columns_cap_residency_bit_identical(device, monkeypatch):
