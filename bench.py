@@ -10,12 +10,18 @@ a fixed seed and resident in HBM before timing starts.  Before the W
 warm-up steps the step runs back to back, untimed, for 0.2 s so that the
 timed steps do not see the GPU's clock ramp from idle.
 
-Default workload: BASELINE config 2 (27-point stencil SpMV, 128^3 grid,
-fp64 / int32).  The line reports effective algorithmic HBM GB/s (bytes =
-values + col indices + row pointer + x (or B) once + y (or C) once) and
-its fraction of the 8 TB/s HBM3E peak, GFLOP/s, the dominant kernel's
-roofline entry timed with HIP events on the launch stream, and the
-reference CPU path (scipy CSR product, 1 thread) on the same matrix.
+By default every BASELINE configuration is run (C1-C5, int32 / int64,
+op = non / trans / conj), each with its own K timed steps, and ONE JSON
+line is printed: the headline fields are those of config 2 (27-point
+stencil SpMV, 128^3 grid, fp64 / int32), and `configs` holds one entry per
+configuration with the same fields.  --config NAME runs one configuration.
+Each entry reports effective algorithmic HBM GB/s (bytes = values + col
+indices + row pointer + x (or B) once + y (or C) once) and its fraction of
+the 8 TB/s HBM3E peak, GFLOP/s, the dominant kernel's roofline entry timed
+with HIP events on the launch stream, the reference CPU path (scipy CSR
+product, 1 thread; torch.sparse.mm on all threads) on a bounded sample of
+the same matrix, and the accuracy of the GPU output on that sample against
+the fp64 oracle.
 """
 
 import argparse
@@ -44,6 +50,7 @@ CONFIGS = {
     "c5_spmm_rmat21_c64_i64_n32_conj": dict(op_kind="spmm", gen="rmat", dtype="c64", index="i64", op="conj", n=32),
 }
 DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
+CONFIG_ORDER = [DEFAULT_CONFIG] + [c for c in CONFIGS if c != DEFAULT_CONFIG]
 
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 1 GiB copy calibration (the commands and raw
@@ -133,20 +140,20 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz, g
         d, i, p, shape = A.data, A.indices, A.indptr.astype(np.int64), A.shape
         n_rows = shape[0]
         op = "non"
-    budget = 3e8 if cfg["op_kind"] == "spmv" else 2e8 / max(1, R.shape[1] if R.ndim == 2 else 1)
+    budget = 1e8 if cfg["op_kind"] == "spmv" else 5e7 / max(1, R.shape[1] if R.ndim == 2 else 1)
     rows = n_rows
     if p[-1] > budget:
         rows = int(np.searchsorted(p, budget))
         rows = max(1, min(rows, n_rows))
     nnz_s = int(p[rows])
-    secs, reps = CB.time_scipy(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R, op=op, min_seconds=10.0)
+    secs, reps = CB.time_scipy(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R, op=op, min_seconds=2.0)
     frac = nnz_s / max(1, full_nnz)
     value = full_bytes * frac / secs / 1e9
     info = CB.host_info()
     # the other CPU path the reference compares against: torch.sparse.mm on a
-    # CPU CSR tensor, all torch threads, same sample (5 s budget)
+    # CPU CSR tensor, all torch threads, same sample (1 s budget)
     t_secs, t_reps, t_threads = CB.time_torch_cpu(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R,
-                                                  min_seconds=5.0)
+                                                  min_seconds=1.0)
     torch_leg = {
         "value": round(full_bytes * frac / t_secs / 1e9, 3),
         "unit": "GB/s",
@@ -195,14 +202,15 @@ def _accuracy(d, i, p, shape, R, out_rows):
     }
 
 
-def run(args):
+def run_config(name, args):
+    """One configuration: its bench entry (the fields of the JSON line)."""
     import torch
 
     import flagsparse_amd as fs
     from flagsparse_amd import _lib
     from flagsparse_amd import synthetic as S
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[name]
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     stream = torch.cuda.current_stream(device)
@@ -221,6 +229,11 @@ def run(args):
         prep = fs.prepare_spmv_csr(data, indices, indptr, shape, op=op)
         torch.cuda.synchronize()
         analysis_ms = (time.perf_counter() - t1) * 1e3
+        # the same prepare again: library, allocator and code objects warm
+        t1 = time.perf_counter()
+        fs.prepare_spmv_csr(data, indices, indptr, shape, op=op)
+        torch.cuda.synchronize()
+        extra["analysis_warm_ms"] = round((time.perf_counter() - t1) * 1e3, 3)
         x = S.vector(prep.n_cols, data.dtype, device, seed=11)
         rhs = x
         step = lambda: fs.flagsparse_spmv_csr(x=x, prepared=prep)  # noqa: E731
@@ -269,6 +282,9 @@ def run(args):
         if sell is not None and sell.layout == 1:
             kernel_name = "spmv_sell_group_kernel"
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
+        if cfg["gen"] == "stencil":
+            extra["one_shot"] = _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for=(
+                S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)), steps=args.steps, stream=stream, device=device)
         m, k, n_dense = prep.n_rows, prep.n_cols, 1
     else:
         n_dense = cfg["n"]
@@ -301,7 +317,9 @@ def run(args):
         kernel_call = lambda: lib.fs_spmm_csr(*args_abi)  # noqa: E731
         bytes_alg = S.bytes_spmm(nnz, m, k, n_dense, vb, ib, pb)
         flops = S.flops_spmm(nnz, n_dense, complex_values)
-        kernel_name = "spmm_group_kernel"
+        from flagsparse_amd.spmm_csr import _spmm_kernel_name
+
+        kernel_name = _spmm_kernel_name(plan, data.dtype, n_dense)
         extra.update(max_row_nnz=plan.csr.max_row_nnz, analysis_ms=round(analysis_ms, 3), n_dense=n_dense)
         if op != "non":
             # Public call including the per-call transpose (reference semantics).
@@ -343,7 +361,7 @@ def run(args):
         "dtype": dtype_name,
         "data": "synthetic (seeded on-device generator, flagsparse_amd/synthetic.py)",
         "config": {
-            "workload": args.config,
+            "workload": name,
             "op": op,
             "n_rows": int(m),
             "n_cols": int(k),
@@ -363,7 +381,7 @@ def run(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": args.traffic_bytes if args.traffic_bytes is not None else MEASURED_TRAFFIC.get(args.config),
+            "traffic": args.traffic_bytes if args.traffic_bytes is not None else MEASURED_TRAFFIC.get(name),
         },
         "extra": dict(extra, generate_s=round(gen_s, 2)),
     }
@@ -373,6 +391,45 @@ def run(args):
         line["cpu_baseline"], line["accuracy"] = cpu_baseline(cfg, data, indices, indptr, shape, rhs, bytes_alg, nnz,
                                                               out)
     return line
+
+
+def _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for, steps, stream, device):
+    """What an unprepared flagsparse_spmv_csr(data, indices, indptr, x, shape)
+    costs: the whole public call (structure check, analysis, launch) per
+    step, and the CSR kernel it runs (no SELL copy) timed alone."""
+    import os
+
+    import torch
+
+    call = lambda: fs.flagsparse_spmv_csr(data, indices, indptr, x, shape)  # noqa: E731
+    for _ in range(3):
+        call()
+    ms_call = time_loop(call, max(5, steps // 2), stream)
+    os.environ["FLAGSPARSE_SPMV_SELL"] = "0"
+    try:
+        prep = fs.prepare_spmv_csr(data, indices, indptr, shape)
+    finally:
+        os.environ.pop("FLAGSPARSE_SPMV_SELL", None)
+    plan = prep.hip_plan()
+    y = torch.empty(prep.n_rows, dtype=data.dtype, device=device)
+    carry = prep._carry
+    lib = _lib.lib()
+    abi = (plan.plan, _lib.ptr(prep.data), _lib.ptr(prep.kernel_indices), _lib.ptr(prep.kernel_indptr), _lib.ptr(x),
+           _lib.ptr(y), _lib.ptr(prep._part), _lib.ptr(carry), 0 if carry is None else carry.numel(),
+           _lib.stream_handle(device))
+    kern = lambda: lib.fs_spmv_csr(*abi)  # noqa: E731
+    for _ in range(20):
+        kern()
+    k_ms = time_loop(kern, steps, stream)
+    names = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
+             "nnzblock": "spmv_nnzblock_kernel", "panel": "spmv_panel_merge_kernel"}
+    return {
+        "ms_per_call": round(ms_call, 5),
+        "kernel": names.get(prep.kernel_name, prep.kernel_name),
+        "kernel_ms": round(k_ms, 5),
+        "achieved": round(bytes_alg_for / (k_ms * 1e-3) / 1e9, 2),
+        "frac": round(bytes_alg_for / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
 
 
 def copy_calibration(args):
@@ -393,7 +450,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default=DEFAULT_CONFIG, choices=sorted(CONFIGS))
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="run one configuration (default: all of them, headline = " + DEFAULT_CONFIG + ")")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--traffic-bytes", type=float, default=None,
                     help="HBM bytes per launch measured with rocprofv3 FETCH_SIZE+WRITE_SIZE (scaled)")
@@ -412,7 +470,21 @@ def main():
     if args.copy_calibration:
         copy_calibration(args)
         return
-    line = run(args)
+    if args.config:
+        print(json.dumps(run_config(args.config, args)), flush=True)
+        return
+    import gc
+
+    import torch
+
+    entries = []
+    for name in CONFIG_ORDER:
+        print(f"bench: {name}", file=sys.stderr, flush=True)
+        entries.append(run_config(name, args))
+        gc.collect()
+        torch.cuda.empty_cache()
+    line = dict(entries[0])
+    line["configs"] = entries
     print(json.dumps(line), flush=True)
 
 
