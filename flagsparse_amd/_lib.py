@@ -46,6 +46,10 @@ EXPORTED_SYMBOLS = (
     "fs_csr_partition",
     "fs_spmv_partition",
     "fs_spmv_csr",
+    "fs_spmv_opt_max_buckets",
+    "fs_spmv_opt_workspace_bytes",
+    "fs_spmv_opt_buckets",
+    "fs_spmv_csr_opt",
     "fs_spmm_workspace_bytes",
     "fs_spmm_tile_items",
     "fs_spmm_csr",
@@ -121,6 +125,15 @@ def _declare(lib):
     lib.fs_spmv_partition.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp]
     lib.fs_spmv_csr.restype = _i32
     lib.fs_spmv_csr.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.fs_spmv_opt_max_buckets.restype = _i32
+    lib.fs_spmv_opt_max_buckets.argtypes = []
+    lib.fs_spmv_opt_workspace_bytes.restype = _sz
+    lib.fs_spmv_opt_workspace_bytes.argtypes = [_i64]
+    lib.fs_spmv_opt_buckets.restype = _i32
+    lib.fs_spmv_opt_buckets.argtypes = [_vp, _i32, _i32, _i64, _vp, _sz, ctypes.POINTER(_i64), _vp]
+    lib.fs_spmv_csr_opt.restype = _i32
+    lib.fs_spmv_csr_opt.argtypes = [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                    ctypes.POINTER(_i64), _vp]
     lib.fs_spmm_workspace_bytes.restype = _sz
     lib.fs_spmm_workspace_bytes.argtypes = [_i32, _i64, _i64]
     lib.fs_spmm_tile_items.restype = _i32

@@ -108,6 +108,7 @@ class PreparedCsrSpmv:
         "_carry",
         "_panels",
         "_sell",
+        "_opt",
         "_one_shot",
     )
 
@@ -159,6 +160,7 @@ class PreparedCsrSpmv:
         self._carry = None
         self._panels = None
         self._sell = None
+        self._opt = None  # row-length buckets of the use_opt path (built on first use)
         self._one_shot = False  # built for a single call: no column-panel copy
 
     # -- HIP plan (built lazily on first run, then cached) ------------------
@@ -812,9 +814,84 @@ def _spmv_prepared_with_int32_indices(prepared, reason):
     return out
 
 
+class _SpmvOptBuckets:
+    """Row ids of the use_opt path partitioned into the reference's row-length
+    tiers (spmv_csr.py:136-161, 353-410), on the device, with the tier sizes
+    on the host."""
+
+    __slots__ = ("ws", "counts")
+
+    def __init__(self, prepared):
+        lib = _lib.lib()
+        device = prepared.data.device
+        n_rows = int(prepared.n_rows)
+        self.ws = _lib.workspace(lib.fs_spmv_opt_workspace_bytes(n_rows), device)
+        self.counts = (ctypes.c_int64 * int(lib.fs_spmv_opt_max_buckets()))()
+        _lib.check(
+            lib.fs_spmv_opt_buckets(
+                _lib.ptr(prepared.kernel_indptr),
+                _lib.index_code(prepared.kernel_indptr.dtype),
+                _lib.value_code(prepared.data.dtype),
+                n_rows,
+                _lib.ptr(self.ws),
+                self.ws.numel(),
+                self.counts,
+                _lib.stream_handle(device),
+            ),
+            "fs_spmv_opt_buckets",
+        )
+
+    @property
+    def bucket_count(self):
+        """Non-empty buckets, as len(opt_buckets) in the reference."""
+        return sum(1 for c in self.counts if c > 0)
+
+
+def _spmv_opt_buckets(prepared):
+    """The use_opt buckets of a prepared matrix: built once and kept, except
+    for a one-shot call (the reference rebuilds them every call,
+    spmv_csr.py:870-880)."""
+    if prepared._opt is not None:
+        return prepared._opt
+    opt = _SpmvOptBuckets(prepared)
+    if not prepared._one_shot:
+        prepared._opt = opt
+    return opt
+
+
+def _hip_spmv_opt(prepared, x, opt):
+    """y = A x with native-precision accumulation over the row-length buckets
+    (_triton_spmv_csr_impl_opt_prepared, spmv_csr.py:412-461)."""
+    device = prepared.data.device
+    y = torch.empty(prepared.n_rows, dtype=prepared.data.dtype, device=device)
+    if prepared.n_rows == 0:
+        return y
+    _lib.check(
+        _lib.lib().fs_spmv_csr_opt(
+            _lib.value_code(prepared.data.dtype),
+            _lib.index_code(prepared.kernel_indices.dtype),
+            _lib.index_code(prepared.kernel_indptr.dtype),
+            int(prepared.n_rows),
+            _lib.ptr(prepared.data),
+            _lib.ptr(prepared.kernel_indices),
+            _lib.ptr(prepared.kernel_indptr),
+            _lib.ptr(x),
+            _lib.ptr(y),
+            _lib.ptr(opt.ws),
+            opt.ws.numel(),
+            opt.counts,
+            _lib.stream_handle(device),
+        ),
+        "fs_spmv_csr_opt",
+    )
+    return y
+
+
 def _run_spmv_prepared(prepared, x, use_opt=False, opt_buckets=None):
-    # use_opt selects the same HIP kernels: their accumulation is already the
-    # accurate one and the variant choice comes from the analysis.
+    """use_opt (float32 / float64 with int32 indices, as supports_opt) runs
+    the native-precision bucketed kernels; otherwise the analysed kernel."""
+    if use_opt and prepared.supports_opt:
+        return _hip_spmv_opt(prepared, x, opt_buckets if opt_buckets is not None else _spmv_opt_buckets(prepared))
     return _hip_spmv_csr_impl_prepared(prepared, x)
 
 
@@ -882,11 +959,17 @@ def flagsparse_spmv_csr(
     x = _validate_spmv_x(x, prepared)
     do_timing = bool(return_time or return_meta)
     symbolic_ms = compute_ms = op_total_ms = None
+    opt = None
+    if do_timing:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+    if use_opt and prepared.supports_opt:
+        opt = _spmv_opt_buckets(prepared)
     if do_timing:
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        symbolic_ms = 0.0
-    y = _run_spmv_prepared_with_fallback(prepared, x, use_opt=use_opt)
+        symbolic_ms = (t1 - t0) * 1000.0 if opt is not None else 0.0
+    y = _run_spmv_prepared_with_fallback(prepared, x, use_opt=use_opt, opt_buckets=opt)
     if do_timing:
         torch.cuda.synchronize()
         compute_ms = (time.perf_counter() - t1) * 1000.0
@@ -905,8 +988,8 @@ def flagsparse_spmv_csr(
             "symbolic_ms": symbolic_ms,
             "compute_ms": compute_ms,
             "op_total_ms": op_total_ms,
-            "bucket_count": 1 if (use_opt and prepared.supports_opt) else 0,
-            "kernel": prepared.kernel_name if prepared.n_rows > 0 else None,
+            "bucket_count": opt.bucket_count if opt is not None else 0,
+            "kernel": ("opt" if opt is not None else prepared.kernel_name) if prepared.n_rows > 0 else None,
         }
         if return_time:
             return y, op_total_ms, meta

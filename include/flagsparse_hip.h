@@ -150,6 +150,32 @@ int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
                 hipStream_t stream);
 
 /*
+ * The use_opt SpMV path: native-precision accumulation (float32 in float32,
+ * float64 in float64) over row-length buckets.  Replaces the reference's
+ * _build_spmv_opt_buckets with its bucket tiers (spmv_csr.py:136-161,
+ * 353-410; float32 <= 64 / <= 512 / <= 4096 / longer, float64 <= 64 /
+ * <= 256 / <= 2048 / <= 8192 / longer, empty rows in the first bucket) and
+ * _triton_spmv_csr_impl_opt_prepared with its four kernels
+ * (spmv_csr.py:233-351, 412-461).  float32 / float64 values, int32 column
+ * indices, int32 / int64 row pointer, as the reference's supports_opt.
+ *
+ * fs_spmv_opt_buckets partitions the row ids into the buckets, in `ws`
+ * (fs_spmv_opt_workspace_bytes(n_rows) bytes of device memory), writes the
+ * fs_spmv_opt_max_buckets() bucket sizes to host `counts_out` and
+ * synchronises `stream`.  fs_spmv_csr_opt runs y = A x from that workspace
+ * and those counts (one launch per non-empty bucket; no synchronisation).
+ */
+int fs_spmv_opt_max_buckets(void);
+size_t fs_spmv_opt_workspace_bytes(int64_t n_rows);
+int fs_spmv_opt_buckets(const void* indptr, int ptr_t, int val_t, int64_t n_rows,
+                        void* ws, size_t ws_bytes, int64_t* counts_out,
+                        hipStream_t stream);
+int fs_spmv_csr_opt(int val_t, int idx_t, int ptr_t, int64_t n_rows,
+                    const void* vals, const void* cols, const void* indptr,
+                    const void* x, void* y, const void* ws, size_t ws_bytes,
+                    const int64_t* counts, hipStream_t stream);
+
+/*
  * C = A B, A CSR (n_rows x n_cols), B dense n_cols x n_dense with row stride
  * ldb (elements), C dense n_rows x n_dense with row stride ldc.  Replaces
  * _triton_spmm_csr_impl + _spmm_csr_real_kernel / _spmm_csr_complex_kernel
