@@ -232,6 +232,28 @@ def _sampled_rows_check(data, indices, indptr, shape, x, y, rows, tol):
     assert err <= tol, f"sampled-row rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("use_opt", [False, True], ids=["base", "opt"])
+def test_spmv_c1_config_full_oracle(device, use_opt):
+    """BASELINE config 1 at its exact shape (4096 x 4096, f32 / int32, exactly
+    16 distinct sorted columns per row): every row against the oracle,
+    through the prepared and the unprepared call."""
+    data, indices, indptr, sh = S.uniform_rows(4096, 4096, 16, torch.float32, torch.int32, device, seed=1)
+    assert data.numel() == 4096 * 16 and indices.dtype == torch.int32 and indptr.dtype == torch.int32
+    p = np_(indptr)
+    c = np_(indices)
+    assert np.array_equal(np.diff(p), np.full(4096, 16))
+    rows_c = c.reshape(4096, 16)
+    assert np.all(np.diff(rows_c, axis=1) > 0) and c.min() >= 0 and c.max() < 4096
+    x = S.vector(4096, torch.float32, device, seed=11)
+    ref = O.spmv_csr_wide(np_(data), c, p, np_(x), sh)
+    y = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh, use_opt=use_opt)
+    assert rel_err(np_(y), ref) <= REL_TOL[torch.float32]
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    y2 = fs.flagsparse_spmv_csr(x=x, prepared=prep, use_opt=use_opt)
+    assert torch.equal(y, y2)
+    assert np.allclose(np_(y2), ref, rtol=ELEM_TOL[torch.float32], atol=ELEM_TOL[torch.float32])
+
+
 @pytest.mark.parametrize("config", ["stencil128_f64_i32", "powerlaw_f32_i32", "powerlaw_f32_i64"])
 def test_spmv_full_size_configs(device, config):
     """BASELINE configs at full size: sampled-row oracle, linearity, determinism."""
