@@ -20,6 +20,7 @@ FS_F32, FS_F64, FS_C64, FS_C128 = 0, 1, 2, 3
 FS_I32, FS_I64 = 0, 1
 FS_KERNEL_VECTOR, FS_KERNEL_MERGE, FS_KERNEL_STREAM, FS_KERNEL_NNZBLOCK = 0, 1, 2, 3
 FS_HIST_BINS = 24
+FS_OK, FS_E_INVALID, FS_E_WORKSPACE, FS_E_HIP = 0, -1, -2, -3
 
 VALUE_TYPE_CODES = {
     torch.float32: FS_F32,
@@ -46,6 +47,8 @@ EXPORTED_SYMBOLS = (
     "fs_csr_partition",
     "fs_spmv_partition",
     "fs_spmv_csr",
+    "fs_spmv_noalloc_scratch_bytes",
+    "fs_spmv_csr_noalloc",
     "fs_spmv_opt_max_buckets",
     "fs_spmv_opt_workspace_bytes",
     "fs_spmv_opt_buckets",
@@ -125,6 +128,10 @@ def _declare(lib):
     lib.fs_spmv_partition.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp]
     lib.fs_spmv_csr.restype = _i32
     lib.fs_spmv_csr.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.fs_spmv_noalloc_scratch_bytes.restype = _sz
+    lib.fs_spmv_noalloc_scratch_bytes.argtypes = []
+    lib.fs_spmv_csr_noalloc.restype = _i32
+    lib.fs_spmv_csr_noalloc.argtypes = [ctypes.POINTER(FsCsrPlan), _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_opt_max_buckets.restype = _i32
     lib.fs_spmv_opt_max_buckets.argtypes = []
     lib.fs_spmv_opt_workspace_bytes.restype = _sz

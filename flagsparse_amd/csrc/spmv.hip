@@ -15,6 +15,7 @@
 #include <type_traits>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace fs {
 
@@ -1218,6 +1219,63 @@ extern "C" int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void
     case FS_C64: return dispatch_idx<c32>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
     default: return dispatch_idx<c64>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
   }
+}
+
+// ---------------------------------------------------------------------------
+// fs_spmv_csr_noalloc: fs_spmv_csr with its carry workspace (the merge-path
+// and entry-block kernels' head / tail fragments of rows that cross tiles)
+// in a file-scope device array instead of a caller buffer.  Each GPU holds
+// its own copy of the array until the process ends; its address on a device
+// comes from hipGetSymbolAddress on the first call there, with that device
+// current, and is kept per device.  The kernels write every fragment the
+// fix-up reads, so nothing needs clearing between calls.  Calls that
+// overlap on one GPU (other streams, other host threads) share the array
+// and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static int scratch_for_current_device(void** out) {
+  int dev = 0;
+  FS_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FS_E_INVALID, "fs_spmv_csr_noalloc: device id out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    FS_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (ptr == nullptr) return fail(FS_E_HIP, "fs_spmv_csr_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FS_OK;
+}
+
+extern "C" size_t fs_spmv_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int fs_spmv_csr_noalloc(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
+                                   const void* x, void* y, const void* part_dev, hipStream_t stream) {
+  if (!plan) return fail(FS_E_INVALID, "fs_spmv_csr_noalloc: plan is null");
+  if (!valid_types(plan->val_t, plan->idx_t, plan->ptr_t))
+    return fail(FS_E_INVALID, "fs_spmv_csr_noalloc: bad type code");
+  if (plan->n_rows == 0) return FS_OK;
+  const bool uses_carry = plan->kernel == FS_KERNEL_MERGE || plan->kernel == FS_KERNEL_NNZBLOCK;
+  const size_t need = uses_carry ? (size_t)(plan->n_tiles > 0 ? plan->n_tiles : 0) * 2 * acc_bytes(plan->val_t) : 0;
+  if (need > kNoAllocScratchBytes)
+    return fail(FS_E_WORKSPACE, "fs_spmv_csr_noalloc: the matrix needs " + std::to_string(need) +
+                                    " bytes of carry scratch, more than the " + std::to_string(kNoAllocScratchBytes) +
+                                    " bytes this entry point holds; call fs_spmv_csr with a workspace");
+  void* carry = nullptr;
+  if (uses_carry) {
+    const int rc = scratch_for_current_device(&carry);
+    if (rc != FS_OK) return rc;
+  }
+  return fs_spmv_csr(plan, vals, cols, indptr, x, y, part_dev, carry, uses_carry ? kNoAllocScratchBytes : 0, stream);
 }
 
 extern "C" size_t fs_spmv_panels_workspace_bytes(const fs_csr_plan* plan, int n_panels) {

@@ -150,6 +150,22 @@ int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
                 hipStream_t stream);
 
 /*
+ * fs_spmv_csr without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * carry fragments of the merge-path / entry-block kernels live in a static
+ * device array of fs_spmv_noalloc_scratch_bytes() bytes (16 MiB) per GPU,
+ * held until the process ends; matrices whose plan needs more
+ * (plan->carry_bytes) are rejected with FS_E_WORKSPACE.  The entry point
+ * calls no allocator.  All calls on one GPU share the array: calls that
+ * overlap in time on that GPU (other streams or host threads) race.
+ */
+size_t fs_spmv_noalloc_scratch_bytes(void);
+int fs_spmv_csr_noalloc(const fs_csr_plan* plan, const void* vals, const void* cols,
+                        const void* indptr, const void* x, void* y,
+                        const void* part_dev, hipStream_t stream);
+
+/*
  * The use_opt SpMV path: native-precision accumulation (float32 in float32,
  * float64 in float64) over row-length buckets.  Replaces the reference's
  * _build_spmv_opt_buckets with its bucket tiers (spmv_csr.py:136-161,
