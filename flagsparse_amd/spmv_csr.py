@@ -173,7 +173,8 @@ class PreparedCsrSpmv:
             p = self._plan.plan
             # The SELL and panel copies are optional: when device memory cannot
             # hold one next to the caller's matrix, the CSR kernels run instead.
-            locality = _spmv_sell_locality(p, self.kernel_indices, self.kernel_indptr, self._one_shot)
+            locality = _spmv_sell_locality(p, self.kernel_indices, self.kernel_indptr, self._one_shot,
+                                            _sell_codes_possible(data.element_size()))
             if locality is not None:
                 try:
                     self._sell = _build_sell(data, self.kernel_indices, self.kernel_indptr, self.n_rows,
@@ -311,23 +312,39 @@ class PanelledCsr:
 # Sliced ELL (SELL-64) pays off when a slice's rows have nearly the same
 # length (padding lanes idle for the whole slot loop) and neighbouring rows
 # have neighbouring columns, so that a slot's 64-lane x gather is coalesced.
-# Measured on MI355X against the row-block stream kernel: 27-point stencil
-# 128^3 f64 0.145 -> 0.123 ms, f32 0.129 -> 0.086 ms; but with 28% padding
-# (a stencil with 30% of entries dropped) 0.112 -> 0.129 ms, and with
-# uniformly random columns (no locality) 0.198 -> 0.203 ms.
+# Measured on MI355X against the row-block stream kernel, with int32 / int16
+# column storage: 27-point stencil 128^3 f64 0.145 -> 0.123 ms, f32 0.129 ->
+# 0.086 ms; but with 28% padding (a stencil with 30% of entries dropped,
+# int16 offsets) 0.112 -> 0.129 ms, and with uniformly random columns (no
+# locality) 0.198 -> 0.203 ms.  One-byte offset codes move the bounds (below).
 _SELL_MIN_SLICES = 2048      # 131,072 rows: enough waves to fill 256 CUs
 _SELL_MAX_PADDING = 1.03     # stored slots / nnz
 # With one-byte offset codes the padding slots (never loaded) cost little:
 # the 128^3 f64 stencil with 5 / 10 / 30% of its entries dropped (stored
 # slots 1.10 / 1.16 / 1.30 x nnz) runs 0.0928 / 0.0950 / 0.0899 ms on the
 # copy against 0.1417 / 0.1364 / 0.1119 ms on the row-block stream kernel.
-_SELL_MAX_PADDING_CODES = 1.35
+# and on random in-band columns (2^21 rows, f64), offsets +-32 / 64 / 96 /
+# 127 with 40 / 20 / 14 / 10% of the band kept, stored slots 1.38 / 1.45 /
+# 1.46 / 1.48 x nnz: 0.116 / 0.118 / 0.125 / 0.121 ms on the copy against
+# 0.164 / 0.163 / 0.168 / 0.164 ms; +-64 with 10% kept (1.70 x nnz): 0.074
+# against 0.083 ms.
+_SELL_MAX_PADDING_CODES = 1.75
 _SELL_MIN_LOCALITY = 0.5     # share of sampled (row, k) whose column is row r-1's + 1
 # With offset codes the copy wins at lower locality: the 128^3 stencil with
 # 30% of its entries dropped samples 0.245 (10%: 0.50, 20%: 0.34) and runs
 # 0.0899 ms on the copy against 0.1119 ms on the row-block stream kernel;
 # uniformly random and power-law columns sample 0.
 _SELL_MIN_LOCALITY_CODES = 0.2
+# With few offsets (codes) the copy wins at any sampled locality, bounded by
+# padding instead: 2^21 rows, f64, random in-band columns, offsets +-16 / 24
+# / 32 / 64 with 80 / 55 / 40 / 20% of the band kept (sampled locality 0.34 /
+# 0.16 / 0.10 / 0.04): 0.100 / 0.110 / 0.112 / 0.118 ms on the copy against
+# 0.162 / 0.164 / 0.161 / 0.163 ms on the row-block stream kernel; the 128^3
+# stencil with 45 / 60% of its entries dropped (locality 0.16 / 0.12):
+# 0.0804 / 0.0673 against 0.0938 / 0.0713 ms (with 75% dropped the copy
+# holds 1.91 x nnz slots and loses, 0.0524 against 0.0490 ms).  So a sample
+# whose offsets c - r take at most _SELL_CODES values counts as local.
+_SELL_SAMPLE_OFFSETS = 32
 _SELL_SAMPLE_SLICES = 256
 _SELL_SAMPLE_K = 8
 
@@ -337,9 +354,14 @@ def _sell_forced():
 
 
 def _sell_locality(indices, indptr, n_rows):
-    """Share of sampled entries (row r, k-th entry) whose column is exactly one
-    more than row r-1's k-th column, over rows r-1, r of the same slice (one
-    device->host sync)."""
+    """(locality, narrow) from a sample of 256 slices (one device->host sync).
+
+    locality: share of sampled entries (row r, k-th entry, k < 8) whose
+    column is exactly one more than row r-1's k-th column, over rows r-1, r
+    of the same slice.  narrow: the sampled offsets c - r (first 32 entries
+    of each sampled row) take at most _SELL_CODES distinct values, so the
+    copy can likely store one-byte codes and a slot's gathers fall in a few
+    windows of x whatever the column order (bands, stencils with gaps)."""
     device = indices.device
     n_slices = n_rows // 64
     step = max(1, n_slices // _SELL_SAMPLE_SLICES)
@@ -355,25 +377,48 @@ def _sell_locality(indices, indptr, n_rows):
     cur = indices[(p1[:, None] + k).clamp(max=last)].to(torch.int64)
     hits = ((cur - prev == 1) & valid).sum()
     total = valid.sum().clamp(min=1)
-    return float((hits.double() / total.double()).item())
+    kk = torch.arange(_SELL_SAMPLE_OFFSETS, device=device)[None, :]
+    in_row = kk < (p2 - p1)[:, None]
+    off = indices[(p1[:, None] + kk).clamp(max=last)].to(torch.int64) - r[:, None]
+    off = off[in_row]
+    if off.numel() == 0:
+        stats = torch.stack([hits.double() / total.double(), torch.zeros((), dtype=torch.float64, device=device),
+                             torch.zeros((), dtype=torch.float64, device=device)])
+    else:
+        stats = torch.stack([hits.double() / total.double(), off.abs().max().double(),
+                             torch.tensor(float(torch.unique(off).numel()), dtype=torch.float64, device=device)])
+    locality, max_off, distinct = stats.cpu().tolist()
+    return locality, distinct <= _SELL_CODES and max_off <= 32767
 
 
-def _spmv_sell_locality(plan, indices, indptr, one_shot):
+def _sell_codes_possible(value_bytes):
+    """Whether a SELL copy could store one-byte offset codes (values of at
+    most 8 bytes, codes and offsets not switched off)."""
+    return (value_bytes <= 8 and os.environ.get("FLAGSPARSE_SELL_CODES") != "0"
+            and os.environ.get("FLAGSPARSE_SELL_DELTA") != "0")
+
+
+def _spmv_sell_locality(plan, indices, indptr, one_shot, codes_possible=True):
     """The sampled column locality when a prepared matrix may get a SELL-64
     copy, else None.  FLAGSPARSE_SPMV_SELL=0/1 forces it off / on (1.0);
     otherwise only for a kept prepared matrix (the copy costs more than one
     launch) whose rows are short (not the merge-path kernel), with at least
     _SELL_MIN_SLICES slices and a locality of at least
-    _SELL_MIN_LOCALITY_CODES.  _build_sell applies the bound that fits the
-    column storage, and the padding bound after the slot count."""
+    _SELL_MIN_LOCALITY_CODES, or few sampled offsets (then at least that
+    value is returned).  _build_sell applies the bound that fits the column
+    storage, and the padding bound after the slot count."""
     env = os.environ.get("FLAGSPARSE_SPMV_SELL")
     n_rows = int(plan.n_rows)
     if env is not None:
         return 1.0 if env == "1" and n_rows > 0 else None
     if one_shot or plan.kernel == _lib.FS_KERNEL_MERGE or n_rows < 64 * _SELL_MIN_SLICES:
         return None
-    locality = _sell_locality(indices, indptr, n_rows)
-    return locality if locality >= _SELL_MIN_LOCALITY_CODES else None
+    locality, narrow = _sell_locality(indices, indptr, n_rows)
+    # below the plain bound only offset codes can win: skip the offset pass
+    # (one launch and a sync) when the values rule codes out
+    if codes_possible and narrow:
+        return max(locality, _SELL_MIN_LOCALITY_CODES)
+    return locality if locality >= (_SELL_MIN_LOCALITY_CODES if codes_possible else _SELL_MIN_LOCALITY) else None
 
 
 def _sell_slice_ptr(indptr, n_rows, group):

@@ -337,7 +337,7 @@ int fs_spmv_csr_panels(const fs_csr_plan* plan, int n_panels,
  * CSR indptr (ptr_t).  With FS_SELL_C8, code_table holds 256 int32 offsets
  * (device memory; entry k is the offset of code k); otherwise it is ignored.
  * Rows may hold up to 2^31 - 1 entries.
- * None of the three synchronises `stream`.
+ * None of the four synchronises `stream`.
  */
 int fs_sell_slots(int ptr_t, int64_t n_rows, const void* indptr,
                   int64_t* slots_dev, hipStream_t stream);

@@ -411,8 +411,9 @@ def test_spmv_sell_not_chosen_without_locality_or_with_padding(device, monkeypat
     """Uniformly random columns (no locality) keep the CSR kernels.  Uneven
     rows: a stencil with 10% or 30% of its entries dropped (stored slots
     ~1.16 / ~1.30 x nnz, sampled locality ~0.50 / ~0.25) gets the copy with
-    offset codes (bounds 1.35 and 0.2) but not with int16 offsets (bounds
-    1.03 and 0.5); with 60% dropped it gets none."""
+    offset codes (padding bound 1.75, few offsets) but not with int16
+    offsets (bounds 1.03 and 0.5); with 60% dropped (~1.6 x nnz slots) it
+    still gets the copy with codes, with 75% dropped (~1.9 x) none."""
     for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS", "FLAGSPARSE_SELL_DELTA",
               "FLAGSPARSE_SELL_CODES"):
         monkeypatch.delenv(k, raising=False)
@@ -432,7 +433,46 @@ def test_spmv_sell_not_chosen_without_locality_or_with_padding(device, monkeypat
         assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell", frac
         monkeypatch.delenv("FLAGSPARSE_SELL_CODES")
     d, i, p, sh = _dropped(*stencil, 0.6, 9)
+    assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name == "sell"
+    d, i, p, sh = _dropped(*stencil, 0.75, 9)
     assert fs.prepare_spmv_csr(d, i, p, sh).kernel_name != "sell"
+
+
+def _band(n, half, keep, dtype, device, seed):
+    """Random in-band columns: each of the 2 * half + 1 diagonals kept with
+    probability `keep` per row."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    offs = torch.arange(-half, half + 1, device=device)
+    r = torch.arange(n, device=device).unsqueeze(1)
+    c = r + offs.unsqueeze(0)
+    m = (c >= 0) & (c < n) & (torch.rand(c.shape, device=device, generator=g) < keep)
+    indptr = torch.zeros(n + 1, dtype=torch.int64, device=device)
+    indptr[1:] = torch.cumsum(m.sum(1), 0)
+    cols = c[m].to(torch.int32)
+    data = torch.rand(cols.numel(), dtype=dtype, device=device, generator=g) - 0.5
+    return data, cols, indptr.to(torch.int32), (n, n)
+
+
+@pytest.mark.parametrize("half,keep", [(16, 0.8), (64, 0.2)])
+def test_spmv_sell_chosen_for_narrow_bands(device, monkeypatch, half, keep):
+    """Random in-band columns have little row-to-row locality (sampled 0.34 /
+    0.04) but few offsets: the copy with offset codes is chosen (stored slots
+    up to ~1.45 x nnz), and matches the oracle."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_PANELS", "FLAGSPARSE_SELL_DELTA",
+              "FLAGSPARSE_SELL_CODES"):
+        monkeypatch.delenv(k, raising=False)
+    d, i, p, sh = _band(1 << 18, half, keep, torch.float64, device, seed=half)
+    prep = fs.prepare_spmv_csr(d, i, p, sh)
+    assert prep.kernel_name == "sell" and prep._sell.cols.dtype == torch.uint8
+    x = S.vector(sh[1], torch.float64, device, seed=4)
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    gen = np.random.default_rng(5)
+    rows = sorted(set(gen.integers(0, sh[0], 2000).tolist()) | {0, 1, sh[0] - 1})
+    _sampled_rows_check(d, i, p, sh, x, y, rows, REL_TOL[torch.float64])
+    # complex128 keeps int16 offsets, whose bound needs locality: not chosen
+    dc = torch.complex(d, d)
+    assert fs.prepare_spmv_csr(dc, i, p, sh).kernel_name != "sell"
 
 
 @pytest.mark.parametrize("storage", ["int16", "int32"])
