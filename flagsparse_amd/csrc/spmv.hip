@@ -358,6 +358,86 @@ __global__ __launch_bounds__(256) void spmv_stream_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// K3t: row-block SpMV with a slot-order x gather, for blocks of 64 short rows.
+//
+// The load phase is K3's: the 256 threads stream the block's entries with
+// unit stride, but stage (column, value) pairs in LDS instead of products.
+// Then wave w takes rows 16w..16w+15 and lane l works on row 16w + (l & 15)
+// with sub-lane s = l >> 4, walking the row's entries s, s+4, s+8, ...  So
+// for each gather instruction the 16 lanes of one sub-lane hold the same
+// entry slot of 16 consecutive rows: on a stencil (or any matrix whose
+// neighbouring rows have neighbouring columns) those are 16 consecutive x
+// entries, where K3's entry-order gather spreads a wave over ~2 rows' worth
+// of scattered offsets.  Each row's four partial sums combine over lanes
+// l, l^16, l^32 in a fixed order: deterministic.
+// ---------------------------------------------------------------------------
+template <int SUBS, class V, class I, class P>
+__global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_blocks, int remap, int stage) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  constexpr int R = 64;             // rows per workgroup
+  constexpr int NT = 64 * SUBS;     // threads
+  constexpr int RPW = 64 / SUBS;    // rows per wave
+  constexpr int K = stream_items<A>() / NT;
+  // dynamic LDS: `stage` (= 64 x the longest row, <= stream_items) values,
+  // then as many column indices, then the 65 row offsets
+  extern __shared__ __align__(16) unsigned char t_lds[];
+  V* s_val = reinterpret_cast<V*>(t_lds);
+  I* s_col = reinterpret_cast<I*>(t_lds + (size_t)stage * sizeof(V));
+  int* s_off = reinterpret_cast<int*>(t_lds + (size_t)stage * (sizeof(V) + sizeof(I)));
+  const int t = threadIdx.x;
+  const int64_t blk = logical_block(remap, n_blocks);
+  if (blk < 0) return;  // whole workgroup
+  const int64_t rb0 = blk * R;
+  const int rows = n_rows - rb0 < R ? (int)(n_rows - rb0) : R;
+  const int64_t S = (int64_t)rowptr[rb0];
+  for (int k = t; k <= rows; k += NT) s_off[k] = (int)((int64_t)rowptr[rb0 + k] - S);  // rows + 1 offsets
+  const int cnt = (int)((int64_t)rowptr[rb0 + rows] - S);
+  V v[K];
+  I c[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = t + NT * k;
+    if (q < cnt) {
+      v[k] = load_stream(vals + S + q);  // A is read once: non-temporal
+      c[k] = __builtin_nontemporal_load(cols + S + q);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = t + NT * k;
+    if (q < cnt) {
+      s_col[q] = c[k];
+      s_val[q] = v[k];
+    }
+  }
+  __syncthreads();
+  const int lane = t & 63;
+  const int r = (t >> 6) * RPW + lane % RPW;
+  const int sub = lane / RPW;
+  A acc0 = T::zero(), acc1 = T::zero(), acc2 = T::zero(), acc3 = T::zero();
+  if (r < rows) {
+    const int a = s_off[r], b = s_off[r + 1];
+    for (int q = a + sub; q < b; q += 4 * SUBS) {  // up to four gathers in flight per lane
+      const bool h1 = q + SUBS < b, h2 = q + 2 * SUBS < b, h3 = q + 3 * SUBS < b;
+      const I c0 = s_col[q], c1 = h1 ? s_col[q + SUBS] : c0, c2 = h2 ? s_col[q + 2 * SUBS] : c0,
+              c3 = h3 ? s_col[q + 3 * SUBS] : c0;
+      const V x0 = x[c0], x1 = x[c1], x2 = x[c2], x3 = x[c3];
+      acc0 = T::fma(s_val[q], x0, acc0);
+      if (h1) acc1 = T::fma(s_val[q + SUBS], x1, acc1);
+      if (h2) acc2 = T::fma(s_val[q + 2 * SUBS], x2, acc2);
+      if (h3) acc3 = T::fma(s_val[q + 3 * SUBS], x3, acc3);
+    }
+  }
+  A acc = add(add(acc0, acc1), add(acc2, acc3));
+  if constexpr (SUBS >= 4) acc = add(acc, shfl(acc, lane ^ 16));
+  if constexpr (SUBS >= 2) acc = add(acc, shfl(acc, lane ^ 32));
+  if (sub == 0 && r < rows) store_stream(y + rb0 + r, T::out(acc));
+}
+
+// ---------------------------------------------------------------------------
 // K3b: entry-aligned streaming SpMV.  Block b owns the entry range
 // [b*C, (b+1)*C) (C = the LDS stage), so its value / index loads depend on
 // nothing and go out at once; the rows it owns (those whose last entry, or
@@ -822,6 +902,13 @@ __global__ __launch_bounds__(256) void merge_fixup_kernel(
 // Host dispatch.
 // ---------------------------------------------------------------------------
 // XCD-contiguous workgroup mapping (FLAGSPARSE_XCD_REMAP=0/1 for A/B).
+// K3t (slot-order gather) in place of K3 for blocks of 64 rows; off with
+// FLAGSPARSE_SPMV_STREAM_T=0 (A/B).
+inline bool stream_t_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_SPMV_STREAM_T");
+  return !(e && std::atoi(e) == 0);
+}
+
 inline int xcd_remap() {
   if (const char* e = std::getenv("FLAGSPARSE_XCD_REMAP")) return std::atoi(e) != 0;
   return 0;  // measured neutral (within 5%) on the stencil and uniform matrices
@@ -876,6 +963,20 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
     const int rpb = plan->rows_per_block;
     if (rpb < 32 || rpb > 256 || (rpb & (rpb - 1)) || (int64_t)plan->max_row * rpb > stream_items<Acc>())
       return fail(FS_E_INVALID, "fs_spmv_csr: rows_per_block does not fit the stream kernel");
+    if (stream_t_enabled() && (int64_t)plan->max_row * 64 <= stream_items<Acc>()) {
+      const int64_t blocks = ceil_div(n_rows, (int64_t)64);
+      const int remap = xcd_remap();
+      dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
+      const int stage = (int)std::max<int64_t>(64 * plan->max_row, 1);
+      const size_t lds = (size_t)stage * (sizeof(V) + sizeof(I)) + 65 * sizeof(int);
+      // four lanes per row: 16 rows per gather instruction.  One or two lanes
+      // per row (64 / 32 rows per instruction, 64- / 128-thread workgroups)
+      // measured slower on the f64 stencil: 0.176 / 0.150 against 0.136 ms.
+      hipLaunchKernelGGL((spmv_stream_t_kernel<4, V, I, P>), g, dim3(256), lds, stream, v, c, p, xv, yv, n_rows,
+                         blocks, remap, stage);
+      FS_CHECK_LAUNCH("spmv_stream_t_kernel");
+      return FS_OK;
+    }
     const int64_t blocks = ceil_div(n_rows, (int64_t)rpb);
     const int remap = xcd_remap();
     dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));

@@ -31,13 +31,20 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge", "stream", "nnzblock", "sell", "panel2", "panel3", "panel8",
-                        "panel16"])
+@pytest.fixture(params=["auto", "vector", "merge", "stream", "stream-entry-order", "nnzblock", "sell", "panel2",
+                        "panel3", "panel8", "panel16"])
 def kernel_choice(request, monkeypatch):
     """Kernel variant under test; panelN = merge path over N column panels;
-    sell = the SELL-64 copy, forced for every matrix."""
+    sell = the SELL-64 copy, forced for every matrix; stream = row blocks
+    with the slot-order gather (K3t) where rows fit, stream-entry-order =
+    the entry-order row-block kernel (K3)."""
     monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
     monkeypatch.delenv("FLAGSPARSE_SPMV_SELL", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SPMV_STREAM_T", raising=False)
+    if request.param == "stream-entry-order":
+        monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "stream")
+        monkeypatch.setenv("FLAGSPARSE_SPMV_STREAM_T", "0")
+        return request.param
     if request.param == "sell":
         monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
         monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
