@@ -42,6 +42,8 @@ EXPORTED_SYMBOLS = (
     "fs_version",
     "fs_csr_check_bytes",
     "fs_csr_check",
+    "fs_csr_check_analyze_bytes",
+    "fs_csr_check_analyze",
     "fs_csr_stats_bytes",
     "fs_csr_analyze",
     "fs_csr_partition",
@@ -117,6 +119,11 @@ def _declare(lib):
     lib.fs_csr_check_bytes.argtypes = []
     lib.fs_csr_check.restype = _i32
     lib.fs_csr_check.argtypes = [_vp, _i32, _vp, _i32, _i64, _i64, _vp, ctypes.POINTER(_i64), _vp]
+    lib.fs_csr_check_analyze_bytes.restype = _sz
+    lib.fs_csr_check_analyze_bytes.argtypes = []
+    lib.fs_csr_check_analyze.restype = _i32
+    lib.fs_csr_check_analyze.argtypes = [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _i64, _i32, _vp, ctypes.POINTER(_i64),
+                                         ctypes.POINTER(FsCsrPlan), _vp]
     lib.fs_csr_stats_bytes.restype = _sz
     lib.fs_csr_stats_bytes.argtypes = []
     lib.fs_csr_analyze.restype = _i32

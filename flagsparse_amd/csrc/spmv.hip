@@ -963,7 +963,10 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
     const int rpb = plan->rows_per_block;
     if (rpb < 32 || rpb > 256 || (rpb & (rpb - 1)) || (int64_t)plan->max_row * rpb > stream_items<Acc>())
       return fail(FS_E_INVALID, "fs_spmv_csr: rows_per_block does not fit the stream kernel");
-    if (stream_t_enabled() && (int64_t)plan->max_row * 64 <= stream_items<Acc>()) {
+    // (the dispatch counts work-items in 32 bits: beyond 2^32 threads, K3's
+    // larger row blocks run instead)
+    if (stream_t_enabled() && (int64_t)plan->max_row * 64 <= stream_items<Acc>() &&
+        ceil_div(n_rows, (int64_t)64) * 256 < (int64_t(1) << 32)) {
       const int64_t blocks = ceil_div(n_rows, (int64_t)64);
       const int remap = xcd_remap();
       dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
@@ -1183,12 +1186,8 @@ using namespace fs;
 
 extern "C" size_t fs_csr_stats_bytes(void) { return kStatsWords * sizeof(unsigned long long); }
 
-extern "C" int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t, int64_t n_rows,
-                              int64_t n_cols, int64_t nnz, int force_kernel, void* stats_dev,
-                              fs_csr_plan* plan, hipStream_t stream) {
-  if (!plan) return fail(FS_E_INVALID, "fs_csr_analyze: plan is null");
-  if (!valid_types(val_t, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_csr_analyze: bad type code");
-  if (n_rows < 0 || n_cols < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_csr_analyze: negative size");
+static void init_plan(fs_csr_plan* plan, int ptr_t, int idx_t, int val_t, int64_t n_rows, int64_t n_cols,
+                      int64_t nnz) {
   std::memset(plan, 0, sizeof(*plan));
   plan->n_rows = n_rows;
   plan->n_cols = n_cols;
@@ -1196,45 +1195,62 @@ extern "C" int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_
   plan->val_t = val_t;
   plan->idx_t = idx_t;
   plan->ptr_t = ptr_t;
-  if (n_rows > 0) {
-    if (!indptr || !stats_dev) return fail(FS_E_INVALID, "fs_csr_analyze: null pointer");
-    unsigned long long* st = static_cast<unsigned long long*>(stats_dev);
-    hipLaunchKernelGGL(stats_init_kernel, dim3(1), dim3(64), 0, stream, st);
-    FS_CHECK_LAUNCH("stats_init_kernel");
-    // Each workgroup ends with a handful of global atomics on shared addresses,
-    // which serialise in L2, so the grid is bounded: at least 2048 rows per
-    // workgroup (8 per lane), at most 1024 workgroups.  Measured on 4 M + 16.7 M
-    // rows (a power-law matrix and its 4-panel stacked copy): 256 / 512 / 1024 /
-    // 2048 / 4096 workgroups 173 / 113 / 104 / 135 / 177 us.
-    int64_t blocks = std::min<int64_t>(ceil_div(n_rows, 2048), 1024);
-    if (ptr_t == FS_I32)
-      hipLaunchKernelGGL((stats_kernel<int32_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
-                         static_cast<const int32_t*>(indptr), n_rows, st);
-    else
-      hipLaunchKernelGGL((stats_kernel<int64_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
-                         static_cast<const int64_t*>(indptr), n_rows, st);
-    FS_CHECK_LAUNCH("stats_kernel");
-    unsigned long long host[kStatsWords];
-    FS_CHECK_HIP(hipMemcpyAsync(host, st, sizeof(host), hipMemcpyDeviceToHost, stream));
-    FS_CHECK_HIP(hipStreamSynchronize(stream));
+}
+
+// Row-length statistics into st[kStatsWords] (no synchronisation).
+static int launch_stats(const void* indptr, int ptr_t, int64_t n_rows, unsigned long long* st, hipStream_t stream) {
+  hipLaunchKernelGGL(stats_init_kernel, dim3(1), dim3(64), 0, stream, st);
+  FS_CHECK_LAUNCH("stats_init_kernel");
+  // Each workgroup ends with a handful of global atomics on shared addresses,
+  // which serialise in L2, so the grid is bounded: at least 2048 rows per
+  // workgroup (8 per lane), at most 1024 workgroups.  Measured on 4 M + 16.7 M
+  // rows (a power-law matrix and its 4-panel stacked copy): 256 / 512 / 1024 /
+  // 2048 / 4096 workgroups 173 / 113 / 104 / 135 / 177 us.
+  int64_t blocks = std::min<int64_t>(ceil_div(n_rows, 2048), 1024);
+  if (ptr_t == FS_I32)
+    hipLaunchKernelGGL((stats_kernel<int32_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const int32_t*>(indptr), n_rows, st);
+  else
+    hipLaunchKernelGGL((stats_kernel<int64_t>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const int64_t*>(indptr), n_rows, st);
+  FS_CHECK_LAUNCH("stats_kernel");
+  return FS_OK;
+}
+
+static void finish_plan(fs_csr_plan* plan, const unsigned long long* host, int force_kernel) {
+  if (plan->n_rows > 0) {
     for (int b = 0; b < FS_HIST_BINS; ++b) plan->hist[b] = (int64_t)host[b];
     plan->max_row = (int64_t)host[FS_HIST_BINS];
     plan->min_row = (int64_t)host[FS_HIST_BINS + 1];
   }
   choose_spmv_kernel(plan, force_kernel);
+}
+
+extern "C" int fs_csr_analyze(const void* indptr, int ptr_t, int idx_t, int val_t, int64_t n_rows,
+                              int64_t n_cols, int64_t nnz, int force_kernel, void* stats_dev,
+                              fs_csr_plan* plan, hipStream_t stream) {
+  if (!plan) return fail(FS_E_INVALID, "fs_csr_analyze: plan is null");
+  if (!valid_types(val_t, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_csr_analyze: bad type code");
+  if (n_rows < 0 || n_cols < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_csr_analyze: negative size");
+  init_plan(plan, ptr_t, idx_t, val_t, n_rows, n_cols, nnz);
+  unsigned long long host[kStatsWords] = {};
+  if (n_rows > 0) {
+    if (!indptr || !stats_dev) return fail(FS_E_INVALID, "fs_csr_analyze: null pointer");
+    unsigned long long* st = static_cast<unsigned long long*>(stats_dev);
+    const int rc = launch_stats(indptr, ptr_t, n_rows, st, stream);
+    if (rc != FS_OK) return rc;
+    FS_CHECK_HIP(hipMemcpyAsync(host, st, sizeof(host), hipMemcpyDeviceToHost, stream));
+    FS_CHECK_HIP(hipStreamSynchronize(stream));
+  }
+  finish_plan(plan, host, force_kernel);
   return FS_OK;
 }
 
 extern "C" size_t fs_csr_check_bytes(void) { return 5 * sizeof(unsigned long long); }
 
-extern "C" int fs_csr_check(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows,
-                            int64_t nnz, void* check_dev, int64_t* out, hipStream_t stream) {
-  if (!indptr || !check_dev || !out) return fail(FS_E_INVALID, "fs_csr_check: null pointer");
-  if ((ptr_t != FS_I32 && ptr_t != FS_I64) || (idx_t != FS_I32 && idx_t != FS_I64))
-    return fail(FS_E_INVALID, "fs_csr_check: bad index type code");
-  if (n_rows < 0 || nnz < 0) return fail(FS_E_INVALID, "fs_csr_check: negative size");
-  if (nnz > 0 && !indices) return fail(FS_E_INVALID, "fs_csr_check: indices is null");
-  unsigned long long* ck = static_cast<unsigned long long*>(check_dev);
+// Structure-check kernels into ck[5] (no synchronisation).
+static int launch_check(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows, int64_t nnz,
+                        unsigned long long* ck, hipStream_t stream) {
   // enough workgroups to stream the indices at full rate; each ends with
   // three global atomics
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(std::max(n_rows, nnz), 1024), 2048));
@@ -1256,14 +1272,66 @@ extern "C" int fs_csr_check(const void* indptr, int ptr_t, const void* indices, 
   else if (idx_t == FS_I32) FS_CHECK_CASE(int64_t, int32_t);
   else FS_CHECK_CASE(int64_t, int64_t);
 #undef FS_CHECK_CASE
-  unsigned long long host[5];
-  FS_CHECK_HIP(hipMemcpyAsync(host, ck, sizeof(host), hipMemcpyDeviceToHost, stream));
-  FS_CHECK_HIP(hipStreamSynchronize(stream));
+  return FS_OK;
+}
+
+static void decode_check(const unsigned long long* host, int64_t nnz, int64_t* out) {
   out[0] = (int64_t)host[0];
   out[1] = (int64_t)host[1];
   out[2] = (int64_t)host[2];
   out[3] = nnz > 0 ? (int64_t)(host[3] ^ kSignFlip) : 0;
   out[4] = nnz > 0 ? (int64_t)(host[4] ^ kSignFlip) : -1;
+}
+
+static int check_args(const char* who, const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows,
+                      int64_t nnz, const void* ws, const int64_t* out) {
+  if (!indptr || !ws || !out) return fail(FS_E_INVALID, std::string(who) + ": null pointer");
+  if ((ptr_t != FS_I32 && ptr_t != FS_I64) || (idx_t != FS_I32 && idx_t != FS_I64))
+    return fail(FS_E_INVALID, std::string(who) + ": bad index type code");
+  if (n_rows < 0 || nnz < 0) return fail(FS_E_INVALID, std::string(who) + ": negative size");
+  if (nnz > 0 && !indices) return fail(FS_E_INVALID, std::string(who) + ": indices is null");
+  return FS_OK;
+}
+
+extern "C" int fs_csr_check(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows,
+                            int64_t nnz, void* check_dev, int64_t* out, hipStream_t stream) {
+  int rc = check_args("fs_csr_check", indptr, ptr_t, indices, idx_t, n_rows, nnz, check_dev, out);
+  if (rc != FS_OK) return rc;
+  unsigned long long* ck = static_cast<unsigned long long*>(check_dev);
+  rc = launch_check(indptr, ptr_t, indices, idx_t, n_rows, nnz, ck, stream);
+  if (rc != FS_OK) return rc;
+  unsigned long long host[5];
+  FS_CHECK_HIP(hipMemcpyAsync(host, ck, sizeof(host), hipMemcpyDeviceToHost, stream));
+  FS_CHECK_HIP(hipStreamSynchronize(stream));
+  decode_check(host, nnz, out);
+  return FS_OK;
+}
+
+extern "C" size_t fs_csr_check_analyze_bytes(void) { return (5 + kStatsWords) * sizeof(unsigned long long); }
+
+extern "C" int fs_csr_check_analyze(const void* indptr, int ptr_t, const void* indices, int idx_t, int val_t,
+                                    int64_t n_rows, int64_t n_cols, int64_t nnz, int force_kernel, void* ws,
+                                    int64_t* out, fs_csr_plan* plan, hipStream_t stream) {
+  int rc = check_args("fs_csr_check_analyze", indptr, ptr_t, indices, idx_t, n_rows, nnz, ws, out);
+  if (rc != FS_OK) return rc;
+  if (!plan) return fail(FS_E_INVALID, "fs_csr_check_analyze: plan is null");
+  if (!valid_types(val_t, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_csr_check_analyze: bad type code");
+  if (n_cols < 0) return fail(FS_E_INVALID, "fs_csr_check_analyze: negative size");
+  init_plan(plan, ptr_t, idx_t, val_t, n_rows, n_cols, nnz);
+  unsigned long long* ck = static_cast<unsigned long long*>(ws);
+  unsigned long long* st = ck + 5;
+  rc = launch_check(indptr, ptr_t, indices, idx_t, n_rows, nnz, ck, stream);
+  if (rc != FS_OK) return rc;
+  if (n_rows > 0) {
+    rc = launch_stats(indptr, ptr_t, n_rows, st, stream);
+    if (rc != FS_OK) return rc;
+  }
+  unsigned long long host[5 + kStatsWords] = {};
+  FS_CHECK_HIP(hipMemcpyAsync(host, ck, (n_rows > 0 ? 5 + kStatsWords : 5) * sizeof(unsigned long long),
+                              hipMemcpyDeviceToHost, stream));
+  FS_CHECK_HIP(hipStreamSynchronize(stream));
+  decode_check(host, nnz, out);
+  finish_plan(plan, host + 5, force_kernel);
   return FS_OK;
 }
 

@@ -106,34 +106,38 @@ __device__ inline T xor_shfl(T v, int mask) {
   return __shfl_xor(v, mask);
 }
 
-// L (8, 32 or 64) lanes per row, 64 / L rows per wave.
+// L (8, 32 or 64) lanes per row, 256 / L rows per workgroup per step; the
+// workgroups stride over the bucket (the trip count depends only on the
+// workgroup, so every lane of a group takes part in the reduction).
 template <class V, class I, class P, class R, int L>
 __global__ __launch_bounds__(256) void opt_rows_kernel(const V* __restrict__ vals, const I* __restrict__ cols,
                                                        const P* __restrict__ indptr, const V* __restrict__ x,
                                                        V* __restrict__ y, const R* __restrict__ rows,
                                                        int64_t n_bucket) {
-  const int lane = threadIdx.x & 63;
-  const int gl = lane % L;
-  const int64_t slot = ((int64_t)blockIdx.x * 256 + threadIdx.x) / L;
-  const bool in = slot < n_bucket;
-  const int64_t row = in ? (int64_t)rows[slot] : 0;
-  const int64_t start = in ? (int64_t)indptr[row] : 0;
-  const int64_t end = in ? (int64_t)indptr[row + 1] : 0;
-  V acc0 = V(0), acc1 = V(0), acc2 = V(0), acc3 = V(0);
-  int64_t k = start + gl;
-  for (; k + 3 * L < end; k += 4 * L) {
-    const I c0 = cols[k], c1 = cols[k + L], c2 = cols[k + 2 * L], c3 = cols[k + 3 * L];
-    const V a0 = vals[k], a1 = vals[k + L], a2 = vals[k + 2 * L], a3 = vals[k + 3 * L];
-    acc0 = __builtin_fma(a0, x[c0], acc0);
-    acc1 = __builtin_fma(a1, x[c1], acc1);
-    acc2 = __builtin_fma(a2, x[c2], acc2);
-    acc3 = __builtin_fma(a3, x[c3], acc3);
-  }
-  for (; k < end; k += L) acc0 = __builtin_fma(vals[k], x[cols[k]], acc0);
-  V s = (acc0 + acc1) + (acc2 + acc3);
+  constexpr int RPB = 256 / L;
+  const int gl = threadIdx.x % L;
+  for (int64_t base = (int64_t)blockIdx.x * RPB; base < n_bucket; base += (int64_t)gridDim.x * RPB) {
+    const int64_t slot = base + threadIdx.x / L;
+    const bool in = slot < n_bucket;
+    const int64_t row = in ? (int64_t)rows[slot] : 0;
+    const int64_t start = in ? (int64_t)indptr[row] : 0;
+    const int64_t end = in ? (int64_t)indptr[row + 1] : 0;
+    V acc0 = V(0), acc1 = V(0), acc2 = V(0), acc3 = V(0);
+    int64_t k = start + gl;
+    for (; k + 3 * L < end; k += 4 * L) {
+      const I c0 = cols[k], c1 = cols[k + L], c2 = cols[k + 2 * L], c3 = cols[k + 3 * L];
+      const V a0 = vals[k], a1 = vals[k + L], a2 = vals[k + 2 * L], a3 = vals[k + 3 * L];
+      acc0 = __builtin_fma(a0, x[c0], acc0);
+      acc1 = __builtin_fma(a1, x[c1], acc1);
+      acc2 = __builtin_fma(a2, x[c2], acc2);
+      acc3 = __builtin_fma(a3, x[c3], acc3);
+    }
+    for (; k < end; k += L) acc0 = __builtin_fma(vals[k], x[cols[k]], acc0);
+    V s = (acc0 + acc1) + (acc2 + acc3);
 #pragma unroll
-  for (int m = L / 2; m >= 1; m >>= 1) s += xor_shfl(s, m);
-  if (in && gl == 0) y[row] = s;
+    for (int m = L / 2; m >= 1; m >>= 1) s += xor_shfl(s, m);
+    if (in && gl == 0) y[row] = s;
+  }
 }
 
 // One 256-thread workgroup per row (the long-row tiers).
@@ -183,11 +187,11 @@ int launch_opt(const OptTiers& t, const void* vals, const void* cols, const void
     V* yv = static_cast<V*>(y);
     const int L = t.lanes[b];
     if (L == 256) {
-      if (n > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr_opt: grid too large");
+      if (n >= (int64_t(1) << 24)) return fail(FS_E_INVALID, "fs_spmv_csr_opt: too many long rows for one grid");
       hipLaunchKernelGGL((opt_block_kernel<V, I, P, R>), dim3((unsigned)n), dim3(256), 0, s, v, c, p, xv, yv, rb);
     } else {
-      const int64_t blocks = ceil_div(n * L, 256);
-      if (blocks > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmv_csr_opt: grid too large");
+      // at most 2^20 workgroups (the dispatch counts work-items in 32 bits)
+      const int64_t blocks = std::min<int64_t>(ceil_div(n * L, 256), int64_t(1) << 20);
       if (L == 8)
         hipLaunchKernelGGL((opt_rows_kernel<V, I, P, R, 8>), dim3((unsigned)blocks), dim3(256), 0, s, v, c, p, xv, yv, rb, n);
       else if (L == 32)

@@ -27,7 +27,7 @@ from ._common import (
     SUPPORTED_INDEX_DTYPES,
     _compute_dtype,
 )
-from ._csr import analyze_csr, transpose_csr
+from ._csr import CsrPlan, analyze_csr, transpose_csr
 
 SUPPORTED_SPMV_VALUE_DTYPES = (
     torch.float16,
@@ -93,7 +93,7 @@ class PreparedCsrSpmv:
         "block_nnz",
         "max_segments",
         "opt_max_segments",
-        "row_lengths",
+        "_row_lengths",
         "max_row_nnz",
         "opt_buckets",
         "supports_opt",
@@ -141,9 +141,7 @@ class PreparedCsrSpmv:
         self.block_nnz = block_nnz
         self.max_segments = max_segments
         self.opt_max_segments = opt_max_segments
-        if row_lengths is None:
-            row_lengths = kernel_indptr[1:] - kernel_indptr[:-1]
-        self.row_lengths = row_lengths
+        self._row_lengths = row_lengths  # computed on first access when None
         self.max_row_nnz = max_row_nnz
         self.opt_buckets = [] if opt_buckets is None else opt_buckets
         self.supports_opt = (
@@ -163,11 +161,25 @@ class PreparedCsrSpmv:
         self._opt = None  # row-length buckets of the use_opt path (built on first use)
         self._one_shot = False  # built for a single call: no column-panel copy
 
+    @property
+    def row_lengths(self):
+        """indptr[1:] - indptr[:-1] (spmv_csr.py:111-113), computed on first access."""
+        if self._row_lengths is None:
+            self._row_lengths = self.kernel_indptr[1:] - self.kernel_indptr[:-1]
+        return self._row_lengths
+
+    @row_lengths.setter
+    def row_lengths(self, value):
+        self._row_lengths = value
+
     # -- HIP plan (built lazily on first run, then cached) ------------------
-    def hip_plan(self):
+    def hip_plan(self, analysed=None):
+        """The analysis plan (built on first use, or taken from `analysed`,
+        a CsrPlan of this same matrix) plus the copies and partitions the
+        chosen kernel needs."""
         if self._plan is None:
             data = self.compute_data()
-            self._plan = analyze_csr(
+            self._plan = analysed if analysed is not None else analyze_csr(
                 data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols
             )
             p = self._plan.plan
@@ -599,46 +611,73 @@ def _transpose_csr_for_spmv(data, indices, indptr, shape):
     return transpose_csr(data, indices, indptr, shape, conj=False)
 
 
-def _check_structure(data, indices, indptr, n_cols, messages):
+def _check_structure(data, indices, indptr, n_cols, messages, analyze=False):
     """indptr / index checks in one native pass with one device->host sync
     (fs_csr_check).
 
     The reference checks indptr[0], indptr[-1], monotonicity and the column
     range with separate .item() syncs (spmv_csr.py:546-558); the checks and
     the order in which their errors are raised are kept.  Returns the column
-    range (lo, hi), or None when nnz == 0.
+    range (lo, hi), or None when nnz == 0.  With analyze=True the row-length
+    analysis runs in the same round trip (fs_csr_check_analyze) and the
+    result is (range, CsrPlan).
     """
     nnz = data.numel()
     if indptr.numel() == 0:
-        return None
+        return (None, None) if analyze else None
     lib = _lib.lib()
-    check = _lib.workspace(lib.fs_csr_check_bytes(), indptr.device)
     vals = (ctypes.c_int64 * 5)()
-    _lib.check(
-        lib.fs_csr_check(
-            _lib.ptr(indptr),
-            _lib.index_code(indptr.dtype),
-            _lib.ptr(indices) if nnz > 0 else None,
-            _lib.index_code(indices.dtype),
-            indptr.numel() - 1,
-            nnz,
-            _lib.ptr(check),
-            vals,
-            _lib.stream_handle(indptr.device),
-        ),
-        "fs_csr_check",
-    )
+    plan = None
+    if analyze:
+        ws = _lib.workspace(lib.fs_csr_check_analyze_bytes(), indptr.device)
+        raw = _lib.FsCsrPlan()
+        _lib.check(
+            lib.fs_csr_check_analyze(
+                _lib.ptr(indptr),
+                _lib.index_code(indptr.dtype),
+                _lib.ptr(indices) if nnz > 0 else None,
+                _lib.index_code(indices.dtype),
+                _lib.value_code(_compute_dtype(data.dtype)),
+                indptr.numel() - 1,
+                int(n_cols),
+                nnz,
+                -1,
+                _lib.ptr(ws),
+                vals,
+                raw,
+                _lib.stream_handle(indptr.device),
+            ),
+            "fs_csr_check_analyze",
+        )
+        plan = CsrPlan(raw, indptr.device)
+    else:
+        check = _lib.workspace(lib.fs_csr_check_bytes(), indptr.device)
+        _lib.check(
+            lib.fs_csr_check(
+                _lib.ptr(indptr),
+                _lib.index_code(indptr.dtype),
+                _lib.ptr(indices) if nnz > 0 else None,
+                _lib.index_code(indices.dtype),
+                indptr.numel() - 1,
+                nnz,
+                _lib.ptr(check),
+                vals,
+                _lib.stream_handle(indptr.device),
+            ),
+            "fs_csr_check",
+        )
     if vals[0] != 0:
         raise ValueError(messages["start"])
     if vals[1] != nnz:
         raise ValueError(messages["last"](vals[1]))
     if vals[2] != 0:
         raise ValueError(messages["monotone"])
+    col_range = None
     if nnz > 0:
         if vals[3] < 0 or vals[4] >= n_cols:
             raise IndexError("indices out of range for n_cols")
-        return vals[3], vals[4]
-    return None
+        col_range = (vals[3], vals[4])
+    return (col_range, plan) if analyze else col_range
 
 
 _SPMV_STRUCT_MESSAGES = {
@@ -648,8 +687,10 @@ _SPMV_STRUCT_MESSAGES = {
 }
 
 
-def _prepare_spmv_csr_matrix(data, indices, indptr, shape, index_fallback_policy="auto"):
-    """Validation of spmv_csr.py:518-572 (same order, types and messages)."""
+def _prepare_spmv_csr_matrix(data, indices, indptr, shape, index_fallback_policy="auto", analyze=False):
+    """Validation of spmv_csr.py:518-572 (same order, types and messages).
+    With analyze=True the row-length analysis shares the check's device
+    round trip and its plan is returned last."""
     _normalize_spmv_index_fallback_policy(index_fallback_policy)
     if not all(torch.is_tensor(t) for t in (data, indices, indptr)):
         raise TypeError("data, indices, indptr must all be torch.Tensor")
@@ -674,9 +715,11 @@ def _prepare_spmv_csr_matrix(data, indices, indptr, shape, index_fallback_policy
     data = data.contiguous()
     indices = indices.contiguous()
     indptr = indptr.contiguous()
+    if analyze:
+        _, plan = _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES, analyze=True)
+        return data, indices, indptr, n_rows, n_cols, None, plan
     _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
-    row_lengths = indptr[1:] - indptr[:-1]
-    return data, indices, indptr, n_rows, n_cols, row_lengths
+    return data, indices, indptr, n_rows, n_cols, None
 
 
 def _validate_spmv_x(x, prepared):
@@ -731,8 +774,8 @@ def _prepare_spmv(
         data, indices, indptr, shape = transpose_csr(
             data, indices, indptr, shape, conj=(op_code == SPMV_OP_CONJ_TRANS)
         )
-    data, indices, indptr, n_rows, n_cols, row_lengths = _prepare_spmv_csr_matrix(
-        data, indices, indptr, shape, index_fallback_policy=index_fallback_policy
+    data, indices, indptr, n_rows, n_cols, row_lengths, plan0 = _prepare_spmv_csr_matrix(
+        data, indices, indptr, shape, index_fallback_policy=index_fallback_policy, analyze=True
     )
     prepared = PreparedCsrSpmv(
         data=data,
@@ -753,7 +796,7 @@ def _prepare_spmv(
     )
     prepared._one_shot = bool(one_shot)
     if n_rows > 0:
-        plan = prepared.hip_plan()
+        plan = prepared.hip_plan(analysed=plan0)
         max_row = plan.max_row_nnz
     else:
         max_row = 0

@@ -118,6 +118,21 @@ int fs_csr_check(const void* indptr, int ptr_t, const void* indices, int idx_t,
                  hipStream_t stream);
 
 /*
+ * fs_csr_check and fs_csr_analyze in one device round trip: both passes are
+ * launched, then one read-back fills `out` (as fs_csr_check) and `plan` (as
+ * fs_csr_analyze) and synchronises `stream`.  `ws` holds
+ * fs_csr_check_analyze_bytes() bytes of device memory.  The plan is only
+ * meaningful when `out` shows a valid structure.  Used by the reference's
+ * prepare path (spmv_csr.py:546-558 checks, then 623-647 sizing), which
+ * every unprepared flagsparse_spmv_csr call runs.
+ */
+size_t fs_csr_check_analyze_bytes(void);
+int fs_csr_check_analyze(const void* indptr, int ptr_t, const void* indices, int idx_t,
+                         int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                         int force_kernel, void* ws, int64_t* out, fs_csr_plan* plan,
+                         hipStream_t stream);
+
+/*
  * Merge-path partition: for each tile t, the row coordinate where the
  * tile's merge path starts.  Writes plan->n_tiles+1 int64 into part_dev
  * (plan->part_bytes bytes).
