@@ -57,14 +57,14 @@ CONFIG_ORDER = [DEFAULT_CONFIG] + [c for c in CONFIGS if c != DEFAULT_CONFIG]
 # counts are in profiles/<kernel>_<workload>.md).  Reported as
 # roofline.traffic; configs not profiled with the current kernels report null.
 MEASURED_TRAFFIC = {
-    "c1_spmv_uniform4096_f32_i32": 0.747e6,
+    "c1_spmv_uniform4096_f32_i32": 0.755e6,
     "c2_spmv_stencil128_f64_i32": 583.5e6,
-    "c3_spmv_powerlaw4M_f32_i32": 1762.1e6,
-    "c3_spmv_powerlaw4M_f32_i64": 1761.1e6,
-    "c4_spmm_uniform1M_f32_i32_n64_non": 9177.3e6,
-    "c4_spmm_uniform1M_f32_i32_n64_trans": 9184.6e6,
-    "c5_spmm_rmat21_f32_i64_n256_non": 30702.7e6,
-    "c5_spmm_rmat21_c64_i64_n32_conj": 7198.5e6,
+    "c3_spmv_powerlaw4M_f32_i32": 1760.6e6,
+    "c3_spmv_powerlaw4M_f32_i64": 1761.2e6,
+    "c4_spmm_uniform1M_f32_i32_n64_non": 9265.1e6,
+    "c4_spmm_uniform1M_f32_i32_n64_trans": 9274.8e6,
+    "c5_spmm_rmat21_f32_i64_n256_non": 30700.3e6,
+    "c5_spmm_rmat21_c64_i64_n32_conj": 7229.2e6,
 }
 
 
@@ -276,11 +276,9 @@ def run_config(name, args):
             extra["n_panels"] = pan.n_panels
         bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
         flops = S.flops_spmv(nnz, complex_values)
-        kernel_name = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
-                       "panel": "spmv_panel_merge_kernel", "nnzblock": "spmv_nnzblock_kernel",
-                       "sell": "spmv_sell_kernel"}[prep.kernel_name]
-        if sell is not None and sell.layout == 1:
-            kernel_name = "spmv_sell_group_kernel"
+        from flagsparse_amd.spmv_csr import _spmv_kernel_symbol
+
+        kernel_name = _spmv_kernel_symbol(prep)
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         if cfg["gen"] == "stencil":
             extra["one_shot"] = _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for=(
@@ -421,11 +419,11 @@ def _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for, ste
     for _ in range(20):
         kern()
     k_ms = time_loop(kern, steps, stream)
-    names = {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "stream": "spmv_stream_kernel",
-             "nnzblock": "spmv_nnzblock_kernel", "panel": "spmv_panel_merge_kernel"}
+    from flagsparse_amd.spmv_csr import _spmv_kernel_symbol
+
     return {
         "ms_per_call": round(ms_call, 5),
-        "kernel": names.get(prep.kernel_name, prep.kernel_name),
+        "kernel": _spmv_kernel_symbol(prep),
         "kernel_ms": round(k_ms, 5),
         "achieved": round(bytes_alg_for / (k_ms * 1e-3) / 1e9, 2),
         "frac": round(bytes_alg_for / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -902,6 +902,22 @@ def _spmv_prepared_with_int32_indices(prepared, reason):
     return out
 
 
+def _spmv_kernel_symbol(prepared):
+    """Name of the kernel function a prepared matrix's SpMV launches (for
+    reports): mirrors the choice in fs_spmv_csr / fs_spmv_sell."""
+    name = prepared.kernel_name
+    if name == "sell":
+        return "spmv_sell_group_kernel" if prepared._sell.layout == _SELL_PAIR else "spmv_sell_kernel"
+    if name == "stream":
+        plan = prepared.hip_plan().plan
+        items = 16384 // (16 if prepared.compute_data().dtype.is_complex else 8)
+        t_ok = (os.environ.get("FLAGSPARSE_SPMV_STREAM_T", "1") != "0" and int(plan.max_row) * 64 <= items
+                and -(-int(plan.n_rows) // 64) * 256 < (1 << 32))
+        return "spmv_stream_t_kernel" if t_ok else "spmv_stream_kernel"
+    return {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "panel": "spmv_panel_merge_kernel",
+            "nnzblock": "spmv_nnzblock_kernel"}.get(name, name)
+
+
 class _SpmvOptBuckets:
     """Row ids of the use_opt path partitioned into the reference's row-length
     tiers (spmv_csr.py:136-161, 353-410), on the device, with the tier sizes
