@@ -69,9 +69,11 @@ __device__ inline T bcast_lane(const T& v, int src_lane) {
 }
 
 // VEC: 16-byte vector loads / stores of row-major slices; otherwise element
-// accesses at any strides.  (16-byte buffer loads with 32-bit offsets
-// measured within 1% of these: C4 1.264 / 1.275 ms, R-MAT complex64 N = 32
-// 1.447 / 1.400 ms.)
+// accesses at any strides.  Measured alternatives, not kept: 16-byte buffer
+// loads with 32-bit offsets (C4 1.264 / 1.275 ms, R-MAT complex64 N = 32
+// 1.447 / 1.400 ms), two gathers per batch instead of four (more waves per
+// SIMD; C4 1.33 ms against 1.26), a residency bound through
+// amdgpu_waves_per_eu (spills registers).
 template <class V, int LPR, int U, bool VEC, class I>
 __global__ __launch_bounds__(256) void spmm_group_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const void* __restrict__ rowptr_raw, int ptr64,
@@ -134,6 +136,7 @@ __global__ __launch_bounds__(256) void spmm_group_kernel(
   const I* colp = cols + n0;
   const V* valp = vals + n0;
   const V* Bl = B + col0_ld * sbn;
+  const uint32_t row_bytes = (uint32_t)(sbk * (int64_t)sizeof(V));
   // Entry chunks: LPR entries per group, one per lane; chunk c + 1 is loaded
   // while chunk c is walked.  Every global load below is unconditional, so
   // the compiler counts the ones in flight exactly and waits for a gather
@@ -200,11 +203,14 @@ __global__ __launch_bounds__(256) void spmm_group_kernel(
         cc = bcast_lane(cch, g * LPR + li);
         aa[u] = bcast_lane(vch, g * LPR + li);
       }
-      const V* p = Bl + (int64_t)cc * sbk;
       if constexpr (VEC) {
-        L4 q = *reinterpret_cast<const L4*>(p);
+        // one 32 x 32 + 64-bit multiply-add per gather (the host takes this
+        // path only when columns and the row stride in bytes fit 32 bits)
+        const char* pb = reinterpret_cast<const char*>(Bl) + (uint64_t)(uint32_t)cc * (uint64_t)row_bytes;
+        L4 q = *reinterpret_cast<const L4*>(pb);
         __builtin_memcpy(bb[u], &q, 16);
       } else {
+        const V* p = Bl + (int64_t)cc * sbk;
 #pragma unroll
         for (int k = 0; k < EPL; ++k) bb[u][k] = p[(k < valid ? k : 0) * sbn];
       }
@@ -376,8 +382,10 @@ int launch_spmm_group(const fs_csr_plan* plan, const void* vals, const void* col
   size_t lds = (size_t)4 * G * (size_t)sub_items * sizeof(uint16_t);
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_WG_CAP")) lds = std::max(lds, lds_pad_for_cap(std::atoi(e), 0));
   // vector path: every lane's B / C slice is EPL unit-stride elements, 16-byte aligned
+  // (and 32-bit gather offsets: column indices and B's row stride in bytes fit 32 bits)
   const bool vec = sbn == 1 && scn == 1 && (n_dense % EPL) == 0 && (sbk % EPL) == 0 && (scm % EPL) == 0 &&
-                   ((uintptr_t)B % 16) == 0 && ((uintptr_t)C % 16) == 0;
+                   ((uintptr_t)B % 16) == 0 && ((uintptr_t)C % 16) == 0 && plan->n_cols <= (int64_t(1) << 32) &&
+                   sbk * (int64_t)sizeof(V) < (int64_t(1) << 32);
   const int ptr64 = plan->ptr_t == FS_I64 ? 1 : 0;
   auto go = [&](auto icode) {
     using I = std::conditional_t<decltype(icode)::value, int64_t, int32_t>;
