@@ -59,8 +59,8 @@ CONFIG_ORDER = [DEFAULT_CONFIG] + [c for c in CONFIGS if c != DEFAULT_CONFIG]
 MEASURED_TRAFFIC = {
     "c1_spmv_uniform4096_f32_i32": 0.755e6,
     "c2_spmv_stencil128_f64_i32": 583.5e6,
-    "c3_spmv_powerlaw4M_f32_i32": 1760.6e6,
-    "c3_spmv_powerlaw4M_f32_i64": 1761.2e6,
+    "c3_spmv_powerlaw4M_f32_i32": 1989.0e6,
+    "c3_spmv_powerlaw4M_f32_i64": 1987.5e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9265.1e6,
     "c4_spmm_uniform1M_f32_i32_n64_trans": 9274.8e6,
     "c5_spmm_rmat21_f32_i64_n256_non": 30700.3e6,

@@ -686,63 +686,111 @@ __device__ inline void store_row(Y* y, int64_t row, typename VT<V>::acc v) {
     y[row] = VT<V>::out(v);
 }
 
-// One merge tile, processed by one wave (per-wave LDS slices passed in).
-template <class V, class I, class P, class Y>
-__device__ inline void merge_tile(const V* __restrict__ vals, const I* __restrict__ cols,
-                                  const P* __restrict__ rowptr, const V* __restrict__ x, Y* __restrict__ y,
-                                  const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
-                                  typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz,
-                                  int64_t t, unsigned* msk, typename VT<V>::acc* prod) {
+// Geometry of merge tile t: its first row r0 = part[t], its row ends
+// r0 .. r1-1, its first nnz n0, R row ends and Nz nnz.
+struct TileGeom {
+  int64_t r0, r1, n0;
+  int R, Nz;
+};
+__device__ inline TileGeom tile_geom(int64_t t, int64_t r0, int64_t r1, int64_t total) {
+  const int64_t d0 = t * kMergeTile;
+  const int64_t dend = d0 + kMergeTile < total ? d0 + kMergeTile : total;
+  TileGeom g;
+  g.r0 = r0;
+  g.r1 = r1;
+  g.n0 = d0 - r0;
+  g.R = (int)(r1 - r0);
+  g.Nz = (int)(dend - r1 - g.n0);
+  return g;
+}
+
+// The tile's own loads: values and columns of its nnz (coalesced, read
+// once: non-temporal, which keeps x in L2, power-law 0.608 -> 0.591 ms),
+// and the row pointers of its row ends (lane-striped), plus rowptr[r0].
+template <class V, class I, class P>
+__device__ inline void tile_loads(const V* __restrict__ vals, const I* __restrict__ cols,
+                                  const P* __restrict__ rowptr, const TileGeom& g, V (&av)[kMergeTile / 64],
+                                  I (&cv)[kMergeTile / 64], P (&rp)[kMergeTile / 64], P& rp0) {
+  constexpr int kIpt = kMergeTile / 64;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < kIpt; ++k) {
+    const int j = k * 64 + lane;
+    if (j < g.Nz) {  // lanes past the tile keep stale registers, never read
+      av[k] = load_stream(vals + g.n0 + j);
+      cv[k] = __builtin_nontemporal_load(cols + g.n0 + j);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kIpt; ++i) {
+    const int k = lane + 64 * i;
+    if (k < g.R) rp[i] = rowptr[g.r0 + 1 + k];
+  }
+  rp0 = g.R > 0 ? rowptr[g.r0] : P(0);
+}
+
+// tile_loads without branches, for the pipelined loop: lanes past the
+// tile's nnz re-read the matrix's last entry and lanes past its row ends the
+// last row pointer (n_rows_total = rows of the CSR), so every load is issued
+// and the compiler can count loads in flight exactly (a load skipped on
+// some path makes it wait for all of them).  Needs nnz >= 1.
+template <class V, class I, class P>
+__device__ inline void tile_loads_all(const V* __restrict__ vals, const I* __restrict__ cols,
+                                      const P* __restrict__ rowptr, const TileGeom& g, int64_t nnz,
+                                      int64_t n_rows_total, V (&av)[kMergeTile / 64], I (&cv)[kMergeTile / 64],
+                                      P (&rp)[kMergeTile / 64], P& rp0) {
+  constexpr int kIpt = kMergeTile / 64;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < kIpt; ++k) {
+    const int j = k * 64 + lane;
+    const int64_t e = j < g.Nz ? g.n0 + j : nnz - 1;
+    av[k] = load_stream(vals + e);
+    cv[k] = __builtin_nontemporal_load(cols + e);
+  }
+#pragma unroll
+  for (int i = 0; i < kIpt; ++i) {
+    const int k = lane + 64 * i;
+    rp[i] = rowptr[k < g.R ? g.r0 + 1 + k : n_rows_total];
+  }
+  rp0 = rowptr[g.r0];
+}
+
+// Everything after the x gathers of one tile: row-end mask, products in
+// LDS, per-lane walk, carry scan, row stores and head / tail fragments.
+template <class V, class P, class Y>
+__device__ inline void tile_finish(Y* __restrict__ y, typename VT<V>::acc* __restrict__ head,
+                                   typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t t,
+                                   const TileGeom& g, const V (&av)[kMergeTile / 64], const V (&xv)[kMergeTile / 64],
+                                   const P (&rp)[kMergeTile / 64], P rp0, unsigned* msk,
+                                   typename VT<V>::acc* prod) {
   using T = VT<V>;
   using A = typename T::acc;
   constexpr int kIpt = kMergeTile / 64;  // items per lane
   const int lane = threadIdx.x & 63;
-
-  const int64_t r0 = part[t];
-  const int64_t r1 = part[t + 1];
-  const int64_t d0 = t * kMergeTile;
-  const int64_t total = n_rows + nnz;
-  const int64_t dend = d0 + kMergeTile < total ? d0 + kMergeTile : total;
-  const int64_t n0 = d0 - r0;
-  const int R = (int)(r1 - r0);
-  const int Nz = (int)(dend - r1 - n0);
+  const int64_t r0 = g.r0;
+  const int R = g.R;
+  const int Nz = g.Nz;
   const int items = R + Nz;
-
-  // 1. products of the tile's nnz: coalesced loads, x gathers, LDS stage.
-  V av[kIpt];
-  I cv[kIpt];
-#pragma unroll
-  for (int k = 0; k < kIpt; ++k) {
-    const int j = k * 64 + lane;
-    cv[k] = 0;
-    if (j < Nz) {
-      av[k] = load_stream(vals + n0 + j);  // A is read once: keep x in L2 (power-law 0.608 -> 0.591 ms)
-      cv[k] = __builtin_nontemporal_load(cols + n0 + j);
-    }
-  }
-  // 2. row-end mask (one ds_or per row end).
+  // row-end mask (one ds_or per row end).
   if (lane < kMergeTile / 32) msk[lane] = 0u;
-  V xv[kIpt];
-#pragma unroll
-  for (int k = 0; k < kIpt; ++k)
-    if (k * 64 + lane < Nz) xv[k] = x[cv[k]];
   wave_sync();
 #pragma unroll
   for (int i = 0; i < kIpt; ++i) {
     const int k = lane + 64 * i;
     if (k < R) {
-      const int q = (int)((r0 + k) + (int64_t)rowptr[r0 + 1 + k] - d0);
+      const int q = (int)(k + (int64_t)rp[i] - g.n0);
       atomicOr(&msk[q >> 5], 1u << (q & 31));
     }
   }
-  const bool head_partial = R > 0 && (int64_t)rowptr[r0] < n0;
+  const bool head_partial = R > 0 && (int64_t)rp0 < g.n0;
 #pragma unroll
   for (int k = 0; k < kIpt; ++k) {
     const int j = k * 64 + lane;
     if (j < Nz) prod[prod_slot(j)] = T::mul(av[k], xv[k]);
   }
   wave_sync();
-  // 3. sequential walk of this lane's 8 items.  Row ends before the lane:
+  // sequential walk of this lane's 8 items.  Row ends before the lane:
   // popcounts of the 16 mask words, scanned over lanes 0..15 with DPP row
   // shifts (one 16-lane row), read back from lane d/32 by a permute.
   static_assert(kMergeTile / 32 == 16, "word scan covers one DPP row");
@@ -778,7 +826,7 @@ __device__ inline void merge_tile(const V* __restrict__ vals, const I* __restric
     }
   }
 
-  // 4. carry across lanes: inclusive segmented scan of lane tails (a lane
+  // carry across lanes: inclusive segmented scan of lane tails (a lane
   // with a row end starts a new segment), shifted to exclusive.
   const A incl = seg_scan(acc, ends > 0 ? 1 : 0);
   A carry_in = shfl(incl, lane > 0 ? lane - 1 : 0);
@@ -791,7 +839,92 @@ __device__ inline void merge_tile(const V* __restrict__ vals, const I* __restric
     else
       store_row<V>(y, row, v);
   }
-  if (lane == 63 && r1 < n_rows) tail[t] = incl;
+  if (lane == 63 && g.r1 < n_rows) tail[t] = incl;
+}
+
+// One merge tile, processed by one wave (per-wave LDS slices passed in).
+template <class V, class I, class P, class Y>
+__device__ inline void merge_tile(const V* __restrict__ vals, const I* __restrict__ cols,
+                                  const P* __restrict__ rowptr, const V* __restrict__ x, Y* __restrict__ y,
+                                  const int64_t* __restrict__ part, typename VT<V>::acc* __restrict__ head,
+                                  typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz,
+                                  int64_t t, unsigned* msk, typename VT<V>::acc* prod) {
+  constexpr int kIpt = kMergeTile / 64;
+  const int lane = threadIdx.x & 63;
+  const TileGeom g = tile_geom(t, part[t], part[t + 1], n_rows + nnz);
+  V av[kIpt];
+  I cv[kIpt];
+  P rp[kIpt];
+  P rp0;
+  tile_loads<V, I, P>(vals, cols, rowptr, g, av, cv, rp, rp0);
+  V xv[kIpt];
+#pragma unroll
+  for (int k = 0; k < kIpt; ++k)
+    if (k * 64 + lane < g.Nz) xv[k] = x[cv[k]];
+  tile_finish<V, P, Y>(y, head, tail, n_rows, t, g, av, xv, rp, rp0, msk, prod);
+}
+
+// A wave's run of merge tiles t0, t0 + stride, ... (< t_end), software
+// pipelined: the x gathers of tile i are issued first, then the loads of
+// tile i+1 (values, columns, row pointers) and the partition entries of
+// tile i+2, and only then does the wave wait for its gathers and finish
+// tile i.  Loads complete in issue order, so the wait for the gathers does
+// not wait for the prefetch: the HBM latency of the next tile's A overlaps
+// the L2 latency of this tile's gathers, where one tile per wave pays both
+// in turn.
+template <class V, class I, class P, class Y>
+__device__ inline void merge_tiles_pipelined(const V* __restrict__ vals, const I* __restrict__ cols,
+                                             const P* __restrict__ rowptr, const V* __restrict__ x,
+                                             Y* __restrict__ y, const int64_t* __restrict__ part,
+                                             typename VT<V>::acc* __restrict__ head,
+                                             typename VT<V>::acc* __restrict__ tail, int64_t n_rows, int64_t nnz,
+                                             int64_t t0, int64_t stride, int64_t t_end, unsigned* msk,
+                                             typename VT<V>::acc* prod) {
+  constexpr int kIpt = kMergeTile / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t total = n_rows + nnz;
+  if (t0 >= t_end) return;
+  TileGeom g = tile_geom(t0, part[t0], part[t0 + 1], total);
+  V av[kIpt];
+  I cv[kIpt];
+  P rp[kIpt];
+  P rp0;
+  tile_loads_all<V, I, P>(vals, cols, rowptr, g, nnz, n_rows, av, cv, rp, rp0);
+  int64_t t = t0;
+  int64_t tn = t0 + stride;
+  // partition entries of the next tile (the current one again past the end,
+  // so that the loop body always issues the same loads)
+  int64_t pn0 = part[tn < t_end ? tn : t0], pn1 = part[(tn < t_end ? tn : t0) + 1];
+  while (true) {
+    V xv[kIpt];
+#pragma unroll
+    for (int k = 0; k < kIpt; ++k) xv[k] = x[cv[k]];  // every column is valid (lanes past the tile repeat one)
+    const bool more = tn < t_end;
+    const int64_t tl = more ? tn : t;  // tile whose loads are issued now
+    const TileGeom gn = tile_geom(tl, pn0, pn1, total);
+    V avn[kIpt];
+    I cvn[kIpt];
+    P rpn[kIpt];
+    P rp0n;
+    tile_loads_all<V, I, P>(vals, cols, rowptr, gn, nnz, n_rows, avn, cvn, rpn, rp0n);
+    const int64_t tnn = tn + stride < t_end ? tn + stride : tl;
+    const int64_t pnn0 = part[tnn], pnn1 = part[tnn + 1];
+    tile_finish<V, P, Y>(y, head, tail, n_rows, t, g, av, xv, rp, rp0, msk, prod);
+    if (!more) break;
+    wave_sync();  // this tile's LDS reads are done before the next tile's writes
+    g = gn;
+#pragma unroll
+    for (int k = 0; k < kIpt; ++k) {
+      av[k] = avn[k];
+      cv[k] = cvn[k];
+      rp[k] = rpn[k];
+    }
+    rp0 = rp0n;
+    t = tn;
+    tn += stride;
+    pn0 = pnn0;
+    pn1 = pnn1;
+  }
 }
 
 template <class V, class I, class P>
@@ -862,6 +995,37 @@ __global__ __launch_bounds__(256) void spmv_panel_merge_kernel(
   merge_tile<V, I, P, A>(vals, cols, rowptr, x, y, part, head, tail, n_rows, nnz, t, s_mask[w], s_prod[w]);
 }
 
+// K2p, persistent and pipelined: for n_panels dividing 8 (panel p on XCDs
+// p, p + n_panels, ...), a fixed grid of workgroups whose waves each walk
+// a strided run of their panel's tiles with merge_tiles_pipelined.  Wave
+// slot ws of the XCD's W waves takes tiles T0 + (ws + i W) G + s of panel p
+// (G XCDs per panel, s = this XCD's index among them), so the waves of a
+// panel sweep its tiles front to back together.
+template <class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_panel_pipe_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, typename VT<V>::acc* __restrict__ y, const int64_t* __restrict__ part,
+    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail, const PanelTable tab,
+    int n_panels, int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+  using A = typename VT<V>::acc;
+  __shared__ unsigned s_mask[kMergeWaves][kMergeTile / 32];
+  __shared__ A s_prod[kMergeWaves][kMergeTile + kMergeTile / 8];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int xcd = (int)(blockIdx.x % kXcds);
+  const int64_t slot = blockIdx.x / kXcds;
+  const int64_t n_slots = gridDim.x / kXcds;
+  const int G = kXcds / n_panels;
+  const int p = xcd % n_panels;
+  const int s = xcd / n_panels;
+  const int64_t T0 = tab.first[p] * kMergeWaves;
+  const int64_t T1 = tab.first[p + 1] * kMergeWaves < n_tiles ? tab.first[p + 1] * kMergeWaves : n_tiles;
+  const int64_t ws = slot * kMergeWaves + w;
+  const int64_t t0 = T0 + ws * G + s;
+  const int64_t stride = n_slots * kMergeWaves * G;
+  merge_tiles_pipelined<V, I, P, A>(vals, cols, rowptr, x, y, part, head, tail, n_rows, nnz, t0, stride, T1,
+                                    s_mask[w], s_prod[w]);
+}
+
 // y[r] = sum over panels p (in order) of partial[p * n_rows + r], rounded once.
 template <class V>
 __global__ __launch_bounds__(256) void panel_reduce_kernel(const typename VT<V>::acc* __restrict__ partial,
@@ -906,6 +1070,14 @@ __global__ __launch_bounds__(256) void merge_fixup_kernel(
 // FLAGSPARSE_SPMV_STREAM_T=0 (A/B).
 inline bool stream_t_enabled() {
   const char* e = std::getenv("FLAGSPARSE_SPMV_STREAM_T");
+  return !(e && std::atoi(e) == 0);
+}
+
+// Persistent, software-pipelined K2p (spmv_panel_pipe_kernel) when the
+// panel count divides the XCD count; FLAGSPARSE_PANEL_PIPE=0 runs one tile
+// per wave instead (A/B).
+inline bool panel_pipe_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_PANEL_PIPE");
   return !(e && std::atoi(e) == 0);
 }
 
@@ -1101,10 +1273,34 @@ int launch_spmv_panels(const fs_csr_plan* plan, int n_panels, const int64_t* pan
   const size_t static_lds = sizeof(unsigned) * kMergeWaves * (kMergeTile / 32) +
                             sizeof(typename VT<V>::acc) * kMergeWaves * (kMergeTile + kMergeTile / 8);
   const size_t lds_pad = lds_pad_for_cap(cap, static_lds);
-  hipLaunchKernelGGL((spmv_panel_merge_kernel<V, I, P>), dim3((unsigned)(per_xcd * kXcds)), dim3(256), lds_pad, stream,
-                     static_cast<const V*>(vals), static_cast<const I*>(cols), p, static_cast<const V*>(x), partial,
-                     static_cast<const int64_t*>(part), head, tail, tab, n_panels, plan->n_rows, plan->nnz, n_tiles);
-  FS_CHECK_LAUNCH("spmv_panel_merge_kernel");
+  if (kXcds % n_panels == 0 && plan->nnz > 0 && panel_pipe_enabled()) {
+    // persistent: as many workgroups per CU as can be resident at once (at
+    // most `cap`), on every CU of each XCD.  The kernel takes 120 VGPRs (4
+    // waves per SIMD).  Power-law 4M, 4 panels: 0.581 -> 0.570 ms against
+    // one tile per wave; forcing 5 / 6 waves per SIMD (spills) 0.597 /
+    // 0.633; 2 / 3 / 4 workgroups per CU 0.571 / 0.582 / 0.571.  The x
+    // gathers' L2 request rate bounds it, not the latency the pipeline hides.
+    auto launch = [&](auto kern) -> int {
+      int per_cu = 0;
+      FS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds_pad));
+      if (cap > 0) per_cu = std::min(per_cu, cap);
+      const int64_t wgs = std::max<int64_t>(1, (int64_t)(device_cus() / kXcds) * std::max(per_cu, 1));
+      hipLaunchKernelGGL(kern, dim3((unsigned)(std::min(wgs, per_xcd) * kXcds)), dim3(256), lds_pad, stream,
+                         static_cast<const V*>(vals), static_cast<const I*>(cols), p, static_cast<const V*>(x), partial,
+                         static_cast<const int64_t*>(part), head, tail, tab, n_panels, plan->n_rows, plan->nnz,
+                         n_tiles);
+      return FS_OK;
+    };
+    const int rc = launch(spmv_panel_pipe_kernel<V, I, P>);
+    if (rc != FS_OK) return rc;
+    FS_CHECK_LAUNCH("spmv_panel_pipe_kernel");
+  } else {
+    hipLaunchKernelGGL((spmv_panel_merge_kernel<V, I, P>), dim3((unsigned)(per_xcd * kXcds)), dim3(256), lds_pad,
+                       stream, static_cast<const V*>(vals), static_cast<const I*>(cols), p, static_cast<const V*>(x),
+                       partial, static_cast<const int64_t*>(part), head, tail, tab, n_panels, plan->n_rows,
+                       plan->nnz, n_tiles);
+    FS_CHECK_LAUNCH("spmv_panel_merge_kernel");
+  }
   hipLaunchKernelGGL((merge_fixup_kernel<V, P, A>), dim3((unsigned)ceil_div(n_tiles, 256)), dim3(256), 0, stream, p,
                      static_cast<const int64_t*>(part), head, tail, partial, n_tiles, (int64_t)kMergeTile);
   FS_CHECK_LAUNCH("merge_fixup_kernel");

@@ -914,7 +914,12 @@ def _spmv_kernel_symbol(prepared):
         t_ok = (os.environ.get("FLAGSPARSE_SPMV_STREAM_T", "1") != "0" and int(plan.max_row) * 64 <= items
                 and -(-int(plan.n_rows) // 64) * 256 < (1 << 32))
         return "spmv_stream_t_kernel" if t_ok else "spmv_stream_kernel"
-    return {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel", "panel": "spmv_panel_merge_kernel",
+    if name == "panel":
+        pc = prepared._panels
+        pipe = (8 % pc.n_panels == 0 and int(pc.plan.plan.nnz) > 0
+                and os.environ.get("FLAGSPARSE_PANEL_PIPE", "1") != "0")
+        return "spmv_panel_pipe_kernel" if pipe else "spmv_panel_merge_kernel"
+    return {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel",
             "nnzblock": "spmv_nnzblock_kernel"}.get(name, name)
 
 

@@ -32,15 +32,18 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(params=["auto", "vector", "merge", "stream", "stream-entry-order", "nnzblock", "sell", "panel2",
-                        "panel3", "panel8", "panel16"])
+                        "panel3", "panel4", "panel4-tile", "panel8", "panel16"])
 def kernel_choice(request, monkeypatch):
     """Kernel variant under test; panelN = merge path over N column panels;
+    panelN-tile = the same with one tile per wave instead of the persistent
+    pipelined panel kernel (which runs when N divides 8);
     sell = the SELL-64 copy, forced for every matrix; stream = row blocks
     with the slot-order gather (K3t) where rows fit, stream-entry-order =
     the entry-order row-block kernel (K3)."""
     monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS", raising=False)
     monkeypatch.delenv("FLAGSPARSE_SPMV_SELL", raising=False)
     monkeypatch.delenv("FLAGSPARSE_SPMV_STREAM_T", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_PANEL_PIPE", raising=False)
     if request.param == "stream-entry-order":
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "stream")
         monkeypatch.setenv("FLAGSPARSE_SPMV_STREAM_T", "0")
@@ -50,7 +53,9 @@ def kernel_choice(request, monkeypatch):
         monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "1")
     elif request.param.startswith("panel"):
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
-        monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", request.param[len("panel"):])
+        monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", request.param[len("panel"):].split("-")[0])
+        if request.param.endswith("-tile"):
+            monkeypatch.setenv("FLAGSPARSE_PANEL_PIPE", "0")
     elif request.param != "auto":
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", request.param)
     else:
