@@ -793,3 +793,32 @@ def test_spmv_sell_codes_padding_never_multiplied(device, monkeypatch, dtype):
     assert int(prep._sell.table[0]) == 0
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert torch.equal(y, lengths.to(dtype))
+
+
+@pytest.mark.parametrize("n_panels", [2, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
+def test_panel_pipelined_walk_matches_one_tile_per_wave(device, monkeypatch, n_panels, dtype):
+    """The persistent pipelined panel kernel, held to one workgroup per CU so
+    every wave walks many tiles (prefetch, register rotation, the repeated
+    last tile), gives the same bits as one tile per wave (the per-tile
+    arithmetic is the same) and matches the oracle on sampled rows."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_PANEL_PIPE"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", str(n_panels))
+    data, indices, indptr, sh = S.powerlaw(300000, dtype, torch.int32, device, seed=11, clip=20000)
+    x = S.vector(sh[1], dtype, device, seed=5)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    assert prep.kernel_name == "panel"
+    assert spmv_mod._spmv_kernel_symbol(prep) == "spmv_panel_pipe_kernel"
+    monkeypatch.setenv("FLAGSPARSE_PANEL_WG_CAP", "1")
+    y_pipe = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert torch.equal(y_pipe, fs.flagsparse_spmv_csr(x=x, prepared=prep))
+    monkeypatch.delenv("FLAGSPARSE_PANEL_WG_CAP")
+    assert torch.equal(y_pipe, fs.flagsparse_spmv_csr(x=x, prepared=prep))
+    monkeypatch.setenv("FLAGSPARSE_PANEL_PIPE", "0")
+    assert spmv_mod._spmv_kernel_symbol(prep) == "spmv_panel_merge_kernel"
+    y_tile = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert torch.equal(y_pipe, y_tile)
+    gen = np.random.default_rng(2)
+    rows = sorted(set(gen.integers(0, sh[0], 2000).tolist()) | {0, sh[0] - 1})
+    _sampled_rows_check(data, indices, indptr, sh, x, y_pipe, rows, REL_TOL[dtype])
