@@ -416,6 +416,19 @@ __global__ __launch_bounds__(256) void transpose_gather_packed_kernel(const uint
   t_cols[k] = (OI)w.y;
 }
 
+// Sorted packed (value, row) words out to the transposed arrays (coalesced).
+template <class V, class OI>
+__global__ __launch_bounds__(256) void unpack_kernel(const uint2* __restrict__ packed, int64_t nnz,
+                                                     V* __restrict__ t_vals, OI* __restrict__ t_cols) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= nnz) return;
+  const uint2 w = packed[k];
+  V v;
+  __builtin_memcpy(&v, &w.x, 4);
+  t_vals[k] = v;  // real 4-byte values only: conj is the identity
+  t_cols[k] = (OI)w.y;
+}
+
 template <class K, class OP>
 __global__ __launch_bounds__(256) void colptr_kernel(const K* __restrict__ keys, int64_t nnz, int64_t n_cols,
                                                      OP* __restrict__ colptr) {
@@ -445,11 +458,14 @@ struct Layout {
   int64_t n_sub, n_counts, n_partials;
   size_t off_keys_a, off_keys_b, off_pos_a, off_pos_b, off_rowid, off_counts, off_partials, total;
   size_t off_prow = 0, off_tile_rows = 0;
+  bool payload = false;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz) {
+// payload = true sizes the position slots for 8-byte words (the transpose
+// carries packed (value, row) words through the sort instead of positions).
+Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz, bool payload = false) {
   Layout L{};
   L.key_bytes = (n_cols > (int64_t)0xffffffffLL) ? 8 : 4;
   L.pos_bytes = (nnz > (int64_t)0xffffffffLL) ? 8 : 4;
@@ -460,12 +476,14 @@ Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz) {
   size_t o = 0;
   L.off_keys_a = o; o = align256(o + L.key_bytes * nnz);
   L.off_keys_b = o; o = align256(o + L.key_bytes * nnz);
-  L.off_pos_a = o; o = align256(o + L.pos_bytes * nnz);
-  L.off_pos_b = o; o = align256(o + L.pos_bytes * nnz);
+  const size_t slot = payload ? 8 : L.pos_bytes;
+  L.off_pos_a = o; o = align256(o + slot * nnz);
+  L.off_pos_b = o; o = align256(o + slot * nnz);
   L.off_rowid = o; o = align256(o + L.rowid_bytes * nnz);
   L.off_counts = o; o = align256(o + sizeof(int64_t) * L.n_counts);
   L.off_partials = o; o = align256(o + sizeof(int64_t) * (L.n_partials + 1));
   L.total = o;
+  L.payload = payload;
   (void)n_rows;
   return L;
 }
@@ -490,7 +508,7 @@ int key_bits(int64_t n_cols) {
 
 template <class K, class Pos>
 int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, int64_t nnz, int64_t n_cols,
-                    const K** sorted_keys, const Pos** perm, hipStream_t s) {
+                    const K** sorted_keys, const Pos** perm, hipStream_t s, const Pos* pos_init = nullptr) {
   K* ka = reinterpret_cast<K*>(ws + L.off_keys_a);
   K* kb = reinterpret_cast<K*>(ws + L.off_keys_b);
   Pos* pa = reinterpret_cast<Pos*>(ws + L.off_pos_a);
@@ -501,7 +519,7 @@ int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, i
   const unsigned blocks = (unsigned)ceil_div(L.n_sub, kWavesPerBlock);
   const void* kin = cols;
   int kind = col_kind;
-  const Pos* pin = nullptr;  // identity on the first pass
+  const Pos* pin = pos_init;  // null: positions 0, 1, ... on the first pass
   K* kout = ka;
   Pos* pout = pa;
   if (passes == 0) {
@@ -539,11 +557,43 @@ __global__ __launch_bounds__(256) void iota_kernel(Pos* __restrict__ p, int64_t 
   if (k < n) p[k] = (Pos)k;
 }
 
+// Packed payload through the sort (4-byte values with 4-byte output
+// indices): the (value, row) words ride through every scatter pass in
+// place of positions, so no random permutation gather follows the sort.
+// FLAGSPARSE_TRANSPOSE_PAYLOAD=0 sorts positions and gathers instead (A/B).
+inline bool transpose_payload_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_PAYLOAD");
+  return !(e && std::atoi(e) == 0);
+}
+
 template <class V, class P, class OI, class OP, class K, class Pos>
 int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
                     const void* vals, const void* cols, const void* indptr, int conj, void* t_vals, void* t_cols,
                     void* t_indptr, hipStream_t s) {
   const K* keys = nullptr;
+  const unsigned expand_blocks = (unsigned)ceil_div(nnz, kExpandTile);
+  if constexpr (sizeof(V) == 4 && sizeof(OI) == 4) {
+    if (L.payload) {
+      uint2* packed = reinterpret_cast<uint2*>(ws + L.off_rowid);
+      hipLaunchKernelGGL((expand_pack_kernel<P, V, OI>), dim3(expand_blocks), dim3(256), 0, s,
+                         static_cast<const P*>(indptr), n_rows, nnz, static_cast<const V*>(vals), packed);
+      FS_CHECK_LAUNCH("expand_pack_kernel");
+      const uint64_t* sorted = nullptr;
+      int rc = radix_sort_cols<K, uint64_t>(L, ws, cols, idx_t == FS_I32 ? 0 : 1, nnz, n_cols, &keys, &sorted, s,
+                                            reinterpret_cast<const uint64_t*>(packed));
+      if (rc != FS_OK) return rc;
+      if (sorted == nullptr) sorted = reinterpret_cast<const uint64_t*>(packed);  // one column: order unchanged
+      hipLaunchKernelGGL((unpack_kernel<V, OI>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s,
+                         reinterpret_cast<const uint2*>(sorted), nnz, static_cast<V*>(t_vals),
+                         static_cast<OI*>(t_cols));
+      FS_CHECK_LAUNCH("unpack_kernel");
+      hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
+                         n_cols, static_cast<OP*>(t_indptr));
+      FS_CHECK_LAUNCH("colptr_kernel");
+      (void)conj;
+      return FS_OK;
+    }
+  }
   const Pos* perm = nullptr;
   int rc = radix_sort_cols<K, Pos>(L, ws, cols, idx_t == FS_I32 ? 0 : 1, nnz, n_cols, &keys, &perm, s);
   if (rc != FS_OK) return rc;
@@ -553,7 +603,6 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
     FS_CHECK_LAUNCH("iota_kernel");
     perm = pa;
   }
-  const unsigned expand_blocks = (unsigned)ceil_div(nnz, kExpandTile);
   if constexpr (sizeof(V) == 4 && sizeof(OI) == 4) {
     // the rowid slot holds 8 bytes per entry: room for the packed words
     uint2* packed = reinterpret_cast<uint2*>(ws + L.off_rowid);
@@ -997,7 +1046,7 @@ using namespace fs;
 
 extern "C" size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t nnz) {
   if (nnz <= 0) return 0;
-  return make_layout(n_rows, n_cols, nnz).total;
+  return make_layout(n_rows, n_cols, nnz, true).total;
 }
 
 extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, int out_ptr_t, int64_t n_rows,
@@ -1022,7 +1071,7 @@ extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, 
   }
   if (!vals || !cols || !indptr || !t_vals || !t_cols) return fail(FS_E_INVALID, "fs_csr_transpose: null pointer");
   if (n_rows == 0 || n_cols == 0) return fail(FS_E_INVALID, "fs_csr_transpose: nnz > 0 with an empty dimension");
-  const Layout L = make_layout(n_rows, n_cols, nnz);
+  const Layout L = make_layout(n_rows, n_cols, nnz, transpose_payload_enabled());
   if (!ws || ws_bytes < L.total) return fail(FS_E_WORKSPACE, "fs_csr_transpose: workspace too small");
   char* w = static_cast<char*>(ws);
   switch (val_t) {
