@@ -320,37 +320,56 @@ __device__ inline int64_t row_of_entry(const P* __restrict__ rowptr, int64_t lo,
   return lo;
 }
 
-// Call with all 256 threads (contains a barrier).
+// Row ids of the tile's entries into s_row (call with all 256 threads; it
+// contains barriers).  The rows that start inside the tile are marked at
+// their first entry (row + 1; the row pointer is read with unit stride, 256
+// rows at a time, and empty rows start nowhere), then an inclusive max-scan
+// over the tile fills every entry with the last row that started at or
+// before it, seeded with the row of the tile's first entry.  No thread walks
+// rows one dependent load at a time.
 template <class P, class RT>
 __device__ inline void expand_tile_rows(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz, int64_t base,
                                         RT* s_row) {
-  // rows of the tile's first and last entries bound every thread's search
   __shared__ int64_t s_bounds[2];
-  const int64_t last = (base + kExpandTile < nnz ? base + kExpandTile : nnz) - 1;
-  if (threadIdx.x == 0) s_bounds[0] = row_of_entry<P>(rowptr, 0, n_rows - 1, base);
-  if (threadIdx.x == 64) s_bounds[1] = row_of_entry<P>(rowptr, 0, n_rows - 1, last);
+  __shared__ RT s_wmax[4];
+  const int tid = threadIdx.x;
+  const int64_t end = base + kExpandTile < nnz ? base + kExpandTile : nnz;
+  if (tid == 0) s_bounds[0] = row_of_entry<P>(rowptr, 0, n_rows - 1, base);
+  if (tid == 64) s_bounds[1] = row_of_entry<P>(rowptr, 0, n_rows - 1, end - 1);
+  for (int j = tid; j < kExpandTile; j += 256) s_row[expand_slot(j)] = 0;
   __syncthreads();
-  const int64_t e0 = base + (int64_t)threadIdx.x * kExpandItems;
-  if (e0 >= nnz) return;
-  int64_t lo = s_bounds[0], hi = s_bounds[1];  // first row whose end exceeds e0
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if ((int64_t)rowptr[mid + 1] <= e0)
-      lo = mid + 1;
-    else
-      hi = mid;
+  const int64_t rlo = s_bounds[0], rhi = s_bounds[1];
+  // rows rlo+1 .. rhi start inside the tile (after entry base) unless empty
+  for (int64_t r = rlo + 1 + tid; r <= rhi; r += 256) {
+    const int64_t st = (int64_t)rowptr[r];
+    if ((int64_t)rowptr[r + 1] > st) s_row[expand_slot((int)(st - base))] = (RT)(r + 1);
   }
-  int64_t row = lo;
-  int64_t rend = (int64_t)rowptr[row + 1];
+  __syncthreads();
+  // inclusive max-scan: 16 consecutive entries per thread, then across
+  // threads (wave shuffles, then the 4 wave totals)
+  RT v[kExpandItems];
+  RT run = 0;
+#pragma unroll
   for (int k = 0; k < kExpandItems; ++k) {
-    const int64_t e = e0 + k;
-    if (e >= nnz) break;
-    while (rend <= e) {
-      ++row;
-      rend = (int64_t)rowptr[row + 1];
-    }
-    s_row[expand_slot((int)threadIdx.x * kExpandItems + k)] = (RT)row;
+    const RT m = s_row[expand_slot(tid * kExpandItems + k)];
+    run = m > run ? m : run;
+    v[k] = run;
   }
+  RT incl = run;
+  const int lane = tid & 63;
+  for (int off = 1; off < 64; off <<= 1) {
+    const RT y = __shfl_up(incl, off);
+    if (lane >= off && y > incl) incl = y;
+  }
+  if (lane == 63) s_wmax[tid >> 6] = incl;
+  __syncthreads();
+  RT carry = (RT)(rlo + 1);
+  for (int w = 0; w < (tid >> 6); ++w) carry = s_wmax[w] > carry ? s_wmax[w] : carry;
+  const RT prev = __shfl_up(incl, 1);
+  if (lane > 0 && prev > carry) carry = prev;
+#pragma unroll
+  for (int k = 0; k < kExpandItems; ++k)
+    s_row[expand_slot(tid * kExpandItems + k)] = (v[k] > carry ? v[k] : carry) - (RT)1;
 }
 
 template <class P, class OI>
