@@ -406,7 +406,7 @@ __global__ __launch_bounds__(256) void transpose_gather_kernel(const V* __restri
 template <class P, class V, class OI>
 __global__ __launch_bounds__(256) void expand_pack_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz,
                                                           const V* __restrict__ vals, uint2* __restrict__ packed) {
-  static_assert(sizeof(V) == 4 && sizeof(OI) == 4, "packs a 4-byte value with a 4-byte row index");
+  static_assert(sizeof(V) == 4, "packs a 4-byte value with a 4-byte row index (rows below 2^32)");
   __shared__ unsigned s_row[kExpandTile + kExpandTile / 16];
   __shared__ unsigned s_val[kExpandTile + kExpandTile / 16];
   const int64_t base = (int64_t)blockIdx.x * kExpandTile;
@@ -433,6 +433,43 @@ __global__ __launch_bounds__(256) void transpose_gather_packed_kernel(const uint
   __builtin_memcpy(&v, &w.x, 4);
   t_vals[k] = v;  // real 4-byte values only: conj is the identity
   t_cols[k] = (OI)w.y;
+}
+
+// 8-byte values (f64, complex64) with row ids below 2^32: (value, row) in
+// one 16-byte word, so the permutation gather is one random 16-byte read per
+// entry instead of an 8-byte value read and an 8-byte row id read.
+template <class P, class V>
+__global__ __launch_bounds__(256) void expand_pack16_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t nnz,
+                                                            const V* __restrict__ vals, uint4* __restrict__ packed) {
+  static_assert(sizeof(V) == 8, "packs an 8-byte value with a 4-byte row index");
+  __shared__ unsigned s_row[kExpandTile + kExpandTile / 16];
+  const int64_t base = (int64_t)blockIdx.x * kExpandTile;
+  expand_tile_rows<P, unsigned>(rowptr, n_rows, nnz, base, s_row);
+  __syncthreads();
+  for (int j = threadIdx.x; j < kExpandTile; j += 256) {
+    const int64_t e = base + j;
+    if (e < nnz) {
+      uint2 v;
+      __builtin_memcpy(&v, &vals[e], 8);
+      packed[e] = make_uint4(v.x, v.y, s_row[expand_slot(j)], 0u);
+    }
+  }
+}
+
+template <class V, class OI, class Pos>
+__global__ __launch_bounds__(256) void transpose_gather_packed16_kernel(const uint4* __restrict__ packed,
+                                                                        const Pos* __restrict__ perm, int64_t nnz,
+                                                                        int conj, V* __restrict__ t_vals,
+                                                                        OI* __restrict__ t_cols) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= nnz) return;
+  const uint4 w = packed[(int64_t)perm[k]];
+  const uint2 vb = make_uint2(w.x, w.y);
+  V v;
+  __builtin_memcpy(&v, &vb, 8);
+  if (conj) v = VT<V>::conj(v);
+  t_vals[k] = v;
+  t_cols[k] = (OI)w.z;
 }
 
 // Sorted packed (value, row) words out to the transposed arrays (coalesced).
@@ -488,7 +525,7 @@ Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz, bool payload = f
   Layout L{};
   L.key_bytes = (n_cols > (int64_t)0xffffffffLL) ? 8 : 4;
   L.pos_bytes = (nnz > (int64_t)0xffffffffLL) ? 8 : 4;
-  L.rowid_bytes = 8;  // sized for the widest output index type
+  L.rowid_bytes = payload ? 16 : 8;  // the widest output index, or a packed 16-byte (value, row) word
   L.n_sub = ceil_div(nnz, kSub);
   L.n_counts = (int64_t)kDigits * L.n_sub;
   L.n_partials = ceil_div(L.n_counts, kScanTile);
@@ -576,10 +613,17 @@ __global__ __launch_bounds__(256) void iota_kernel(Pos* __restrict__ p, int64_t 
   if (k < n) p[k] = (Pos)k;
 }
 
-// Packed payload through the sort (4-byte values with 4-byte output
-// indices): the (value, row) words ride through every scatter pass in
+// Packed payload through the sort (4-byte values, row ids below 2^32,
+// widened on the way out for 8-byte output indices): the (value, row) words ride through every scatter pass in
 // place of positions, so no random permutation gather follows the sort.
 // FLAGSPARSE_TRANSPOSE_PAYLOAD=0 sorts positions and gathers instead (A/B).
+// 16-byte (value, row) words for the gather of 8-byte values;
+// FLAGSPARSE_TRANSPOSE_PACK16=0 gathers value and row id separately (A/B).
+inline bool transpose_pack16_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_PACK16");
+  return !(e && std::atoi(e) == 0);
+}
+
 inline bool transpose_payload_enabled() {
   const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_PAYLOAD");
   return !(e && std::atoi(e) == 0);
@@ -591,8 +635,8 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
                     void* t_indptr, hipStream_t s) {
   const K* keys = nullptr;
   const unsigned expand_blocks = (unsigned)ceil_div(nnz, kExpandTile);
-  if constexpr (sizeof(V) == 4 && sizeof(OI) == 4) {
-    if (L.payload) {
+  if constexpr (sizeof(V) == 4) {
+    if (L.payload && n_rows <= (int64_t)0xffffffffLL) {
       uint2* packed = reinterpret_cast<uint2*>(ws + L.off_rowid);
       hipLaunchKernelGGL((expand_pack_kernel<P, V, OI>), dim3(expand_blocks), dim3(256), 0, s,
                          static_cast<const P*>(indptr), n_rows, nnz, static_cast<const V*>(vals), packed);
@@ -633,6 +677,22 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
     FS_CHECK_LAUNCH("transpose_gather_packed_kernel");
     (void)conj;
   } else {
+    if constexpr (sizeof(V) == 8) {
+      if (n_rows <= (int64_t)0xffffffffLL && L.payload && transpose_pack16_enabled()) {
+        // the payload layout's rowid slot holds 16 bytes per entry
+        uint4* packed = reinterpret_cast<uint4*>(ws + L.off_rowid);
+        hipLaunchKernelGGL((expand_pack16_kernel<P, V>), dim3(expand_blocks), dim3(256), 0, s,
+                           static_cast<const P*>(indptr), n_rows, nnz, static_cast<const V*>(vals), packed);
+        FS_CHECK_LAUNCH("expand_pack16_kernel");
+        hipLaunchKernelGGL((transpose_gather_packed16_kernel<V, OI, Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256),
+                           0, s, packed, perm, nnz, conj, static_cast<V*>(t_vals), static_cast<OI*>(t_cols));
+        FS_CHECK_LAUNCH("transpose_gather_packed16_kernel");
+        hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
+                           n_cols, static_cast<OP*>(t_indptr));
+        FS_CHECK_LAUNCH("colptr_kernel");
+        return FS_OK;
+      }
+    }
     OI* rowid = reinterpret_cast<OI*>(ws + L.off_rowid);
     hipLaunchKernelGGL((expand_rows_kernel<P, OI>), dim3(expand_blocks), dim3(256), 0, s,
                        static_cast<const P*>(indptr), n_rows, nnz, rowid);
