@@ -62,9 +62,9 @@ MEASURED_TRAFFIC = {
     "c3_spmv_powerlaw4M_f32_i32": 1989.0e6,
     "c3_spmv_powerlaw4M_f32_i64": 1987.5e6,
     "c4_spmm_uniform1M_f32_i32_n64_non": 9265.1e6,
-    "c4_spmm_uniform1M_f32_i32_n64_trans": 9274.8e6,
+    "c4_spmm_uniform1M_f32_i32_n64_trans": 9274.4e6,
     "c5_spmm_rmat21_f32_i64_n256_non": 30700.3e6,
-    "c5_spmm_rmat21_c64_i64_n32_conj": 7229.2e6,
+    "c5_spmm_rmat21_c64_i64_n32_conj": 7227.6e6,
 }
 
 
