@@ -942,6 +942,24 @@ __global__ __launch_bounds__(256) void spmv_merge_kernel(
   merge_tile<V, I, P, V>(vals, cols, rowptr, x, y, part, head, tail, n_rows, nnz, t, s_mask[w], s_prod[w]);
 }
 
+// K2, persistent and pipelined: a fixed grid whose waves each walk tiles
+// w, w + W, ... (W = waves in the grid) with merge_tiles_pipelined.
+template <class V, class I, class P>
+__global__ __launch_bounds__(256) void spmv_merge_pipe_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, const int64_t* __restrict__ part,
+    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail,
+    int64_t n_rows, int64_t nnz, int64_t n_tiles) {
+  using A = typename VT<V>::acc;
+  __shared__ unsigned s_mask[kMergeWaves][kMergeTile / 32];
+  __shared__ A s_prod[kMergeWaves][kMergeTile + kMergeTile / 8];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int64_t t0 = (int64_t)blockIdx.x * kMergeWaves + w;
+  const int64_t stride = (int64_t)gridDim.x * kMergeWaves;
+  merge_tiles_pipelined<V, I, P, V>(vals, cols, rowptr, x, y, part, head, tail, n_rows, nnz, t0, stride, n_tiles,
+                                    s_mask[w], s_prod[w]);
+}
+
 // ---------------------------------------------------------------------------
 // K2p: merge-path SpMV over a column-panelled matrix.  The stacked CSR holds
 // panel p's entries (columns [p*width, (p+1)*width)) as rows p*n + r, so the
@@ -1070,6 +1088,14 @@ __global__ __launch_bounds__(256) void merge_fixup_kernel(
 // FLAGSPARSE_SPMV_STREAM_T=0 (A/B).
 inline bool stream_t_enabled() {
   const char* e = std::getenv("FLAGSPARSE_SPMV_STREAM_T");
+  return !(e && std::atoi(e) == 0);
+}
+
+// Persistent, software-pipelined K2 (spmv_merge_pipe_kernel): power-law 4M
+// without panels 0.998 -> 0.974 ms (f32 / i32), 1.020 -> 1.010 (i64).
+// FLAGSPARSE_MERGE_PIPE=0 runs one tile per wave (A/B).
+inline bool merge_pipe_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_MERGE_PIPE");
   return !(e && std::atoi(e) == 0);
 }
 
@@ -1203,9 +1229,18 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
   A* head = static_cast<A*>(carry);
   A* tail = head + n_tiles;
   const int64_t blocks = ceil_div(n_tiles, kMergeWaves);
-  hipLaunchKernelGGL((spmv_merge_kernel<V, I, P>), dim3((unsigned)blocks), dim3(256), 0, stream, v, c, p,
-                     xv, yv, static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
-  FS_CHECK_LAUNCH("spmv_merge_kernel");
+  if (plan->nnz > 0 && merge_pipe_enabled()) {
+    int per_cu = 0;
+    FS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, spmv_merge_pipe_kernel<V, I, P>, 256, 0));
+    const int64_t wgs = std::min<int64_t>(blocks, (int64_t)device_cus() * std::max(per_cu, 1));
+    hipLaunchKernelGGL((spmv_merge_pipe_kernel<V, I, P>), dim3((unsigned)wgs), dim3(256), 0, stream, v, c, p, xv, yv,
+                       static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
+    FS_CHECK_LAUNCH("spmv_merge_pipe_kernel");
+  } else {
+    hipLaunchKernelGGL((spmv_merge_kernel<V, I, P>), dim3((unsigned)blocks), dim3(256), 0, stream, v, c, p,
+                       xv, yv, static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
+    FS_CHECK_LAUNCH("spmv_merge_kernel");
+  }
   hipLaunchKernelGGL((merge_fixup_kernel<V, P>), dim3((unsigned)ceil_div(n_tiles, 256)), dim3(256), 0,
                      stream, p, static_cast<const int64_t*>(part), head, tail, yv, n_tiles,
                      (int64_t)kMergeTile);

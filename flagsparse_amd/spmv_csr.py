@@ -919,7 +919,10 @@ def _spmv_kernel_symbol(prepared):
         pipe = (8 % pc.n_panels == 0 and int(pc.plan.plan.nnz) > 0
                 and os.environ.get("FLAGSPARSE_PANEL_PIPE", "1") != "0")
         return "spmv_panel_pipe_kernel" if pipe else "spmv_panel_merge_kernel"
-    return {"vector": "spmv_vector_kernel", "merge": "spmv_merge_kernel",
+    if name == "merge":
+        pipe = (int(prepared.hip_plan().plan.nnz) > 0 and os.environ.get("FLAGSPARSE_MERGE_PIPE", "1") != "0")
+        return "spmv_merge_pipe_kernel" if pipe else "spmv_merge_kernel"
+    return {"vector": "spmv_vector_kernel",
             "nnzblock": "spmv_nnzblock_kernel"}.get(name, name)
 
 

@@ -31,10 +31,12 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge", "stream", "stream-entry-order", "nnzblock", "sell", "panel2",
+@pytest.fixture(params=["auto", "vector", "merge", "merge-tile", "stream", "stream-entry-order", "nnzblock", "sell", "panel2",
                         "panel3", "panel4", "panel4-tile", "panel8", "panel16"])
 def kernel_choice(request, monkeypatch):
     """Kernel variant under test; panelN = merge path over N column panels;
+    merge-tile = the merge path with one tile per wave instead of the
+    persistent pipelined walk;
     panelN-tile = the same with one tile per wave instead of the persistent
     pipelined panel kernel (which runs when N divides 8);
     sell = the SELL-64 copy, forced for every matrix; stream = row blocks
@@ -44,6 +46,11 @@ def kernel_choice(request, monkeypatch):
     monkeypatch.delenv("FLAGSPARSE_SPMV_SELL", raising=False)
     monkeypatch.delenv("FLAGSPARSE_SPMV_STREAM_T", raising=False)
     monkeypatch.delenv("FLAGSPARSE_PANEL_PIPE", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_MERGE_PIPE", raising=False)
+    if request.param == "merge-tile":
+        monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
+        monkeypatch.setenv("FLAGSPARSE_MERGE_PIPE", "0")
+        return request.param
     if request.param == "stream-entry-order":
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "stream")
         monkeypatch.setenv("FLAGSPARSE_SPMV_STREAM_T", "0")
