@@ -371,7 +371,42 @@ __global__ __launch_bounds__(256) void spmv_stream_kernel(
 // of scattered offsets.  Each row's four partial sums combine over lanes
 // l, l^16, l^32 in a fixed order: deterministic.
 // ---------------------------------------------------------------------------
-template <int SUBS, class V, class I, class P>
+// LDS layout of K3t for a stage of `stage` entries: values, then column
+// indices (16-byte aligned), then the 65 row offsets.  With direct-to-LDS
+// staging (DL) each array starts at the 16-byte boundary at or below the
+// block's first entry and ends at one at or above its last, so it holds up
+// to two 16-byte chunks more.
+struct StreamTLayout {
+  size_t col_off, off_off, total;
+};
+__host__ __device__ inline StreamTLayout stream_t_layout(int stage, size_t vsz, size_t isz, bool dl) {
+  const size_t nv = (size_t)stage + (dl ? 2 * (16 / vsz) : 0);
+  const size_t ni = (size_t)stage + (dl ? 2 * (16 / isz) : 0);
+  StreamTLayout L;
+  L.col_off = (nv * vsz + 15) & ~(size_t)15;
+  L.off_off = (L.col_off + ni * isz + 15) & ~(size_t)15;
+  L.total = L.off_off + 65 * sizeof(int);
+  return L;
+}
+
+// Copy 16-byte chunks [0, n) of g into LDS (chunk c to dst + 16 c) with
+// direct global-to-LDS loads: wave w of NW takes chunks (k NW + w) 64 + lane.
+// The data never passes through VGPRs and no LDS store is issued.
+template <int NW, int KC>
+__device__ inline void lds_copy16(const unsigned char* g, unsigned char* dst, int n) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int c0 = (k * NW + w) * 64;  // wave-uniform
+    if (c0 >= n) break;
+    if (c0 + lane < n)
+      __builtin_amdgcn_global_load_lds((const void*)(g + (size_t)(c0 + lane) * 16),
+                                       (__attribute__((address_space(3))) void*)(dst + (size_t)c0 * 16), 16, 0, 0);
+  }
+}
+
+template <int SUBS, class V, class I, class P, bool DL>
 __global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
     const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_blocks, int remap, int stage) {
@@ -381,12 +416,11 @@ __global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
   constexpr int NT = 64 * SUBS;     // threads
   constexpr int RPW = 64 / SUBS;    // rows per wave
   constexpr int K = stream_items<A>() / NT;
-  // dynamic LDS: `stage` (= 64 x the longest row, <= stream_items) values,
-  // then as many column indices, then the 65 row offsets
   extern __shared__ __align__(16) unsigned char t_lds[];
+  const StreamTLayout L = stream_t_layout(stage, sizeof(V), sizeof(I), DL);
   V* s_val = reinterpret_cast<V*>(t_lds);
-  I* s_col = reinterpret_cast<I*>(t_lds + (size_t)stage * sizeof(V));
-  int* s_off = reinterpret_cast<int*>(t_lds + (size_t)stage * (sizeof(V) + sizeof(I)));
+  I* s_col = reinterpret_cast<I*>(t_lds + L.col_off);
+  int* s_off = reinterpret_cast<int*>(t_lds + L.off_off);
   const int t = threadIdx.x;
   const int64_t blk = logical_block(remap, n_blocks);
   if (blk < 0) return;  // whole workgroup
@@ -395,22 +429,43 @@ __global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
   const int64_t S = (int64_t)rowptr[rb0];
   for (int k = t; k <= rows; k += NT) s_off[k] = (int)((int64_t)rowptr[rb0 + k] - S);  // rows + 1 offsets
   const int cnt = (int)((int64_t)rowptr[rb0 + rows] - S);
-  V v[K];
-  I c[K];
+  // entry q of the block (0 <= q < cnt) sits at s_val[q + ov], s_col[q + oi]
+  int ov = 0, oi = 0;
+  if constexpr (DL) {
+    // Each array is copied from the 16-byte boundary at or below entry S to
+    // the one at or above S + cnt: a 16-byte aligned load never crosses a
+    // page, so reading the rest of a granule that holds a valid entry is safe.
+    constexpr int EV = 16 / (int)sizeof(V);
+    constexpr int EI = 16 / (int)sizeof(I);
+    const int64_t Sv = S & ~(int64_t)(EV - 1);
+    const int64_t Si = S & ~(int64_t)(EI - 1);
+    ov = (int)(S - Sv);
+    oi = (int)(S - Si);
+    constexpr int KV = (stream_items<A>() + 2 * EV + NT * EV - 1) / (NT * EV);
+    constexpr int KI = (stream_items<A>() + 2 * EI + NT * EI - 1) / (NT * EI);
+    lds_copy16<SUBS, KV>(reinterpret_cast<const unsigned char*>(vals + Sv), reinterpret_cast<unsigned char*>(s_val),
+                         (ov + cnt + EV - 1) / EV);
+    lds_copy16<SUBS, KI>(reinterpret_cast<const unsigned char*>(cols + Si), reinterpret_cast<unsigned char*>(s_col),
+                         (oi + cnt + EI - 1) / EI);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS copies have landed
+  } else {
+    V v[K];
+    I c[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int q = t + NT * k;
-    if (q < cnt) {
-      v[k] = load_stream(vals + S + q);  // A is read once: non-temporal
-      c[k] = __builtin_nontemporal_load(cols + S + q);
+    for (int k = 0; k < K; ++k) {
+      const int q = t + NT * k;
+      if (q < cnt) {
+        v[k] = load_stream(vals + S + q);  // A is read once: non-temporal
+        c[k] = __builtin_nontemporal_load(cols + S + q);
+      }
     }
-  }
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int q = t + NT * k;
-    if (q < cnt) {
-      s_col[q] = c[k];
-      s_val[q] = v[k];
+    for (int k = 0; k < K; ++k) {
+      const int q = t + NT * k;
+      if (q < cnt) {
+        s_col[q] = c[k];
+        s_val[q] = v[k];
+      }
     }
   }
   __syncthreads();
@@ -420,15 +475,17 @@ __global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
   A acc0 = T::zero(), acc1 = T::zero(), acc2 = T::zero(), acc3 = T::zero();
   if (r < rows) {
     const int a = s_off[r], b = s_off[r + 1];
+    const I* sc = s_col + oi;
+    const V* sv = s_val + ov;
     for (int q = a + sub; q < b; q += 4 * SUBS) {  // up to four gathers in flight per lane
       const bool h1 = q + SUBS < b, h2 = q + 2 * SUBS < b, h3 = q + 3 * SUBS < b;
-      const I c0 = s_col[q], c1 = h1 ? s_col[q + SUBS] : c0, c2 = h2 ? s_col[q + 2 * SUBS] : c0,
-              c3 = h3 ? s_col[q + 3 * SUBS] : c0;
+      const I c0 = sc[q], c1 = h1 ? sc[q + SUBS] : c0, c2 = h2 ? sc[q + 2 * SUBS] : c0,
+              c3 = h3 ? sc[q + 3 * SUBS] : c0;
       const V x0 = x[c0], x1 = x[c1], x2 = x[c2], x3 = x[c3];
-      acc0 = T::fma(s_val[q], x0, acc0);
-      if (h1) acc1 = T::fma(s_val[q + SUBS], x1, acc1);
-      if (h2) acc2 = T::fma(s_val[q + 2 * SUBS], x2, acc2);
-      if (h3) acc3 = T::fma(s_val[q + 3 * SUBS], x3, acc3);
+      acc0 = T::fma(sv[q], x0, acc0);
+      if (h1) acc1 = T::fma(sv[q + SUBS], x1, acc1);
+      if (h2) acc2 = T::fma(sv[q + 2 * SUBS], x2, acc2);
+      if (h3) acc3 = T::fma(sv[q + 3 * SUBS], x3, acc3);
     }
   }
   A acc = add(add(acc0, acc1), add(acc2, acc3));
@@ -1107,6 +1164,16 @@ inline bool panel_pipe_enabled() {
   return !(e && std::atoi(e) == 0);
 }
 
+// Direct global-to-LDS staging in K3t (kernel ms, staged through VGPRs ->
+// direct): 27-point stencil f64 0.1364 -> 0.1249, f32 0.103 -> 0.086, f64 /
+// int64 0.167 -> 0.156; 2M x 2M with 16 random columns per row f64 0.482 ->
+// 0.496, f32 0.325 -> 0.338 (their x gathers bound them).
+// FLAGSPARSE_SPMV_STREAM_T_DL=0 stages through VGPRs (A/B).
+inline bool stream_t_dl_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_SPMV_STREAM_T_DL");
+  return !(e && std::atoi(e) == 0);
+}
+
 inline int xcd_remap() {
   if (const char* e = std::getenv("FLAGSPARSE_XCD_REMAP")) return std::atoi(e) != 0;
   return 0;  // measured neutral (within 5%) on the stencil and uniform matrices
@@ -1169,12 +1236,18 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
       const int remap = xcd_remap();
       dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
       const int stage = (int)std::max<int64_t>(64 * plan->max_row, 1);
-      const size_t lds = (size_t)stage * (sizeof(V) + sizeof(I)) + 65 * sizeof(int);
+      // direct-to-LDS staging needs 16-byte aligned value / index arrays
+      const bool dl = stream_t_dl_enabled() && ((uintptr_t)v % 16) == 0 && ((uintptr_t)c % 16) == 0;
+      const size_t lds = stream_t_layout(stage, sizeof(V), sizeof(I), dl).total;
       // four lanes per row: 16 rows per gather instruction.  One or two lanes
       // per row (64 / 32 rows per instruction, 64- / 128-thread workgroups)
       // measured slower on the f64 stencil: 0.176 / 0.150 against 0.136 ms.
-      hipLaunchKernelGGL((spmv_stream_t_kernel<4, V, I, P>), g, dim3(256), lds, stream, v, c, p, xv, yv, n_rows,
-                         blocks, remap, stage);
+      if (dl)
+        hipLaunchKernelGGL((spmv_stream_t_kernel<4, V, I, P, true>), g, dim3(256), lds, stream, v, c, p, xv, yv,
+                           n_rows, blocks, remap, stage);
+      else
+        hipLaunchKernelGGL((spmv_stream_t_kernel<4, V, I, P, false>), g, dim3(256), lds, stream, v, c, p, xv, yv,
+                           n_rows, blocks, remap, stage);
       FS_CHECK_LAUNCH("spmv_stream_t_kernel");
       return FS_OK;
     }

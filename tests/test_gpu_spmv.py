@@ -31,10 +31,12 @@ from tests._helpers import (
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "vector", "merge", "merge-tile", "stream", "stream-entry-order", "nnzblock", "sell", "panel2",
+@pytest.fixture(params=["auto", "vector", "merge", "merge-tile", "stream", "stream-vgpr-stage", "stream-entry-order", "nnzblock", "sell", "panel2",
                         "panel3", "panel4", "panel4-tile", "panel8", "panel16"])
 def kernel_choice(request, monkeypatch):
     """Kernel variant under test; panelN = merge path over N column panels;
+    stream-vgpr-stage = K3t staging its block through registers instead of
+    direct global-to-LDS loads;
     merge-tile = the merge path with one tile per wave instead of the
     persistent pipelined walk;
     panelN-tile = the same with one tile per wave instead of the persistent
@@ -47,6 +49,11 @@ def kernel_choice(request, monkeypatch):
     monkeypatch.delenv("FLAGSPARSE_SPMV_STREAM_T", raising=False)
     monkeypatch.delenv("FLAGSPARSE_PANEL_PIPE", raising=False)
     monkeypatch.delenv("FLAGSPARSE_MERGE_PIPE", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SPMV_STREAM_T_DL", raising=False)
+    if request.param == "stream-vgpr-stage":
+        monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "stream")
+        monkeypatch.setenv("FLAGSPARSE_SPMV_STREAM_T_DL", "0")
+        return request.param
     if request.param == "merge-tile":
         monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
         monkeypatch.setenv("FLAGSPARSE_MERGE_PIPE", "0")
@@ -829,3 +836,28 @@ def test_panel_pipelined_walk_matches_one_tile_per_wave(device, monkeypatch, n_p
     gen = np.random.default_rng(2)
     rows = sorted(set(gen.integers(0, sh[0], 2000).tolist()) | {0, sh[0] - 1})
     _sampled_rows_check(data, indices, indptr, sh, x, y_pipe, rows, REL_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
+def test_stream_t_misaligned_arrays_match(device, monkeypatch, dtype):
+    """Value / index arrays that are not 16-byte aligned (views one element
+    into a buffer) take K3t's register-staged path; aligned copies take the
+    direct-to-LDS path; both give the same bits."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_STREAM_T_DL"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "0")
+    data, indices, indptr, sh = S.stencil27(24, dtype, torch.int32, device, seed=9)
+    x = S.vector(sh[1], dtype, device, seed=4)
+    y = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh, return_meta=True)
+    y, meta = y
+    assert meta["kernel"] == "stream"
+    dbuf = torch.empty(data.numel() + 1, dtype=dtype, device=device)
+    ibuf = torch.empty(indices.numel() + 1, dtype=indices.dtype, device=device)
+    dbuf[1:] = data
+    ibuf[1:] = indices
+    d_view, i_view = dbuf[1:], ibuf[1:]
+    assert d_view.data_ptr() % 16 != 0 and i_view.data_ptr() % 16 != 0
+    y_mis = fs.flagsparse_spmv_csr(d_view, i_view, indptr, x, sh)
+    assert torch.equal(y, y_mis)
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
+    assert rel_err(np_(y), ref) <= REL_TOL[dtype]
