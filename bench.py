@@ -57,7 +57,7 @@ CONFIG_ORDER = [DEFAULT_CONFIG] + [c for c in CONFIGS if c != DEFAULT_CONFIG]
 # counts are in profiles/<kernel>_<workload>.md).  Reported as
 # roofline.traffic; configs not profiled with the current kernels report null.
 MEASURED_TRAFFIC = {
-    "c1_spmv_uniform4096_f32_i32": 0.8e6,
+    "c1_spmv_uniform4096_f32_i32": 0.755e6,
     "c2_spmv_stencil128_f64_i32": 583.5e6,
     "c3_spmv_powerlaw4M_f32_i32": 1989.0e6,
     "c3_spmv_powerlaw4M_f32_i64": 1987.5e6,
