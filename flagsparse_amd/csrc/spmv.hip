@@ -31,14 +31,12 @@ __global__ void stats_init_kernel(unsigned long long* stats) {
   if (k < kStatsWords) stats[k] = (k == FS_HIST_BINS + 1) ? ~0ull : 0ull;
 }
 
-template <class P>
-__global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr,
-                                                    int64_t n_rows,
-                                                    unsigned long long* stats) {
-  __shared__ unsigned int s_hist[FS_HIST_BINS];
-  if (threadIdx.x < FS_HIST_BINS) s_hist[threadIdx.x] = 0;
-  __syncthreads();
-  unsigned long long vmax = 0, vmin = ~0ull;
+// Row-length statistics of the rows this thread's wave visits: LDS
+// histogram by bit length, max / min length, and (COUNT_BAD) the rows whose
+// pointer decreases.
+template <class P, bool COUNT_BAD>
+__device__ inline void stats_rows(const P* __restrict__ rowptr, int64_t n_rows, unsigned int* s_hist,
+                                  unsigned long long& vmax, unsigned long long& vmin, unsigned long long& bad) {
   static_assert(FS_HIST_BINS <= 32, "bins are grouped with 5 ballots");
   // Whole waves run every iteration (the bound is wave-uniform), so the
   // ballots below see every active lane.
@@ -49,18 +47,19 @@ __global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr
   // the kernel latency-bound (88 us for 4 M rows).
   constexpr int kStatsUnroll = 8;
   for (int64_t r0 = first; r0 < n_rows; r0 += kStatsUnroll * stride) {
-    unsigned long long lens[kStatsUnroll];
+    int64_t lens[kStatsUnroll];
     bool valids[kStatsUnroll];
 #pragma unroll
     for (int u = 0; u < kStatsUnroll; ++u) {
       const int64_t r = r0 + u * stride + (threadIdx.x & 63);
       valids[u] = r < n_rows;
-      lens[u] = valids[u] ? (unsigned long long)(rowptr[r + 1] - rowptr[r]) : 0ull;
+      lens[u] = valids[u] ? (int64_t)rowptr[r + 1] - (int64_t)rowptr[r] : 0;
     }
 #pragma unroll
     for (int u = 0; u < kStatsUnroll; ++u) {
       const bool valid = valids[u];
-      const unsigned long long len = lens[u];
+      if constexpr (COUNT_BAD) bad += (valid && lens[u] < 0) ? 1ull : 0ull;
+      const unsigned long long len = (unsigned long long)lens[u];
       int bin = len == 0 ? 0 : (64 - __clzll(len));
       bin = bin < FS_HIST_BINS ? bin : FS_HIST_BINS - 1;
       // lanes with the same bin: one of them adds the group's count
@@ -80,10 +79,15 @@ __global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr
       }
     }
   }
-  // Max / min over the workgroup first (wave butterflies, then 4 partials in
-  // LDS), so each workgroup issues one global atomic per statistic: a global
-  // atomic per thread on one address serialises in L2.  Integer max / min /
-  // count are order independent, so the result is deterministic.
+}
+
+// Max / min over the workgroup first (wave butterflies, then 4 partials in
+// LDS), so each workgroup issues one global atomic per statistic: a global
+// atomic per thread on one address serialises in L2.  Integer max / min /
+// count are order independent, so the result is deterministic.  All
+// threads call it (it has a barrier); s_hist must be complete.
+__device__ inline void stats_flush(unsigned long long vmax, unsigned long long vmin, const unsigned int* s_hist,
+                                   unsigned long long* stats) {
   __shared__ unsigned long long s_max[4], s_min[4];
   for (int off = 32; off > 0; off >>= 1) {
     const unsigned long long omax = __shfl_xor(vmax, off);
@@ -107,6 +111,19 @@ __global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr
   }
   if (threadIdx.x < FS_HIST_BINS && s_hist[threadIdx.x])
     atomicAdd(&stats[threadIdx.x], (unsigned long long)s_hist[threadIdx.x]);
+}
+
+template <class P>
+__global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr,
+                                                    int64_t n_rows,
+                                                    unsigned long long* stats) {
+  __shared__ unsigned int s_hist[FS_HIST_BINS];
+  if (threadIdx.x < FS_HIST_BINS) s_hist[threadIdx.x] = 0;
+  __syncthreads();
+  unsigned long long vmax = 0, vmin = ~0ull, bad = 0;
+  stats_rows<P, false>(rowptr, n_rows, s_hist, vmax, vmin, bad);
+  __syncthreads();
+  stats_flush(vmax, vmin, s_hist, stats);
 }
 
 // ---------------------------------------------------------------------------
@@ -135,18 +152,14 @@ __device__ inline void check_range(I c, unsigned long long& lo, unsigned long lo
   hi = v > hi ? v : hi;
 }
 
-// VEC: the indices are 16-byte aligned and read as 16-byte vectors, four per
-// lane in flight (64 bytes; 4-byte loads left the pass at 3.3 TB/s).
-template <class P, class I, bool VEC>
-__global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr, int64_t n_rows,
-                                                    const I* __restrict__ cols, int64_t nnz,
-                                                    unsigned long long* check) {
+// VEC: the indices are 16-byte aligned and read as 16-byte vectors, eight
+// per lane in flight (128 bytes; 4-byte loads left the pass at 3.3 TB/s).
+// Min / max column over this thread's share of the indices.
+template <class I, bool VEC>
+__device__ inline void check_cols(const I* __restrict__ cols, int64_t nnz, unsigned long long& lo,
+                                  unsigned long long& hi) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  unsigned long long bad = 0;
-  for (int64_t r = tid; r < n_rows; r += stride)
-    bad += __builtin_nontemporal_load(rowptr + r + 1) < __builtin_nontemporal_load(rowptr + r) ? 1ull : 0ull;
-  unsigned long long lo = ~0ull, hi = 0;
   int64_t done = 0;  // leading entries covered by the vector loop
   if constexpr (VEC) {
     constexpr int W = 16 / sizeof(I);
@@ -154,12 +167,12 @@ __global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr
     const vec_t* cv = reinterpret_cast<const vec_t*>(cols);
     const int64_t nv = nnz / W;
     int64_t k = tid;
-    for (; k + 3 * stride < nv; k += 4 * stride) {
-      vec_t c[4];
+    for (; k + 7 * stride < nv; k += 8 * stride) {
+      vec_t c[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) c[u] = __builtin_nontemporal_load(cv + k + u * stride);
+      for (int u = 0; u < 8; ++u) c[u] = __builtin_nontemporal_load(cv + k + u * stride);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int w = 0; w < W; ++w) check_range<I>(c[u][w], lo, hi);
     }
@@ -171,6 +184,12 @@ __global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr
     done = nv * W;
   }
   for (int64_t k = done + tid; k < nnz; k += stride) check_range<I>(__builtin_nontemporal_load(cols + k), lo, hi);
+}
+
+// Workgroup reduction of (bad rows, min, max column), then one global atomic
+// each.  All threads call it (it has a barrier).
+__device__ inline void check_flush(unsigned long long bad, unsigned long long lo, unsigned long long hi, int64_t nnz,
+                                   unsigned long long* check) {
   for (int off = 32; off > 0; off >>= 1) {
     bad += __shfl_xor(bad, off);
     const unsigned long long olo = __shfl_xor(lo, off), ohi = __shfl_xor(hi, off);
@@ -196,6 +215,40 @@ __global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr
       atomicMax(&check[4], hi);
     }
   }
+}
+
+// VEC: the indices are 16-byte aligned and read as 16-byte vectors, eight
+// per lane in flight (128 bytes; 4-byte loads left the pass at 3.3 TB/s).
+template <class P, class I, bool VEC>
+__global__ __launch_bounds__(256) void check_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                                    const I* __restrict__ cols, int64_t nnz,
+                                                    unsigned long long* check) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long bad = 0;
+  for (int64_t r = tid; r < n_rows; r += stride)
+    bad += __builtin_nontemporal_load(rowptr + r + 1) < __builtin_nontemporal_load(rowptr + r) ? 1ull : 0ull;
+  unsigned long long lo = ~0ull, hi = 0;
+  check_cols<I, VEC>(cols, nnz, lo, hi);
+  check_flush(bad, lo, hi, nnz, check);
+}
+
+// Structure check and row-length statistics in one pass (the row pointer is
+// read once, for both): check words as check_kernel, statistics as
+// stats_kernel.
+template <class P, class I, bool VEC>
+__global__ __launch_bounds__(256) void check_stats_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                                          const I* __restrict__ cols, int64_t nnz,
+                                                          unsigned long long* check, unsigned long long* stats) {
+  __shared__ unsigned int s_hist[FS_HIST_BINS];
+  if (threadIdx.x < FS_HIST_BINS) s_hist[threadIdx.x] = 0;
+  __syncthreads();
+  unsigned long long vmax = 0, vmin = ~0ull, bad = 0;
+  stats_rows<P, true>(rowptr, n_rows, s_hist, vmax, vmin, bad);
+  unsigned long long lo = ~0ull, hi = 0;
+  check_cols<I, VEC>(cols, nnz, lo, hi);
+  check_flush(bad, lo, hi, nnz, check);  // its barrier also completes s_hist
+  if (n_rows > 0) stats_flush(vmax, vmin, s_hist, stats);
 }
 
 // ---------------------------------------------------------------------------
@@ -1555,9 +1608,14 @@ extern "C" size_t fs_csr_check_bytes(void) { return 5 * sizeof(unsigned long lon
 // Structure-check kernels into ck[5] (no synchronisation).
 static int launch_check(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows, int64_t nnz,
                         unsigned long long* ck, hipStream_t stream) {
-  // enough workgroups to stream the indices at full rate; each ends with
-  // three global atomics
-  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(std::max(n_rows, nnz), 1024), 2048));
+  // enough workgroups to stream the indices at full rate (eight 16-byte
+  // loads in flight per lane); each ends with three global atomics on shared
+  // addresses, which serialise in L2.  27-point stencil (223 MB of columns),
+  // kernel us at 2048 / 1024 / 512 / 256 workgroups: 67.4 / 55.3 / 46.8 /
+  // 49.3.  FLAGSPARSE_CHECK_BLOCKS overrides (A/B).
+  int64_t cap_blocks = 512;
+  if (const char* e = std::getenv("FLAGSPARSE_CHECK_BLOCKS")) cap_blocks = std::max(1, std::atoi(e));
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(std::max(n_rows, nnz), 1024), cap_blocks));
 #define FS_CHECK_CASE(P, I)                                                                                   \
   do {                                                                                                        \
     hipLaunchKernelGGL((check_init_kernel<P>), dim3(1), dim3(64), 0, stream, static_cast<const P*>(indptr),   \
@@ -1576,6 +1634,35 @@ static int launch_check(const void* indptr, int ptr_t, const void* indices, int 
   else if (idx_t == FS_I32) FS_CHECK_CASE(int64_t, int32_t);
   else FS_CHECK_CASE(int64_t, int64_t);
 #undef FS_CHECK_CASE
+  return FS_OK;
+}
+
+// Structure check and statistics in one kernel (fs_csr_check_analyze).
+static int launch_check_stats(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows,
+                              int64_t nnz, unsigned long long* ck, unsigned long long* st, hipStream_t stream) {
+  int64_t cap_blocks = 512;  // as launch_check
+  if (const char* e = std::getenv("FLAGSPARSE_CHECK_BLOCKS")) cap_blocks = std::max(1, std::atoi(e));
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(std::max(n_rows, nnz), 1024), cap_blocks));
+  hipLaunchKernelGGL(stats_init_kernel, dim3(1), dim3(64), 0, stream, st);
+  FS_CHECK_LAUNCH("stats_init_kernel");
+#define FS_CHECK_STATS_CASE(P, I)                                                                             \
+  do {                                                                                                        \
+    hipLaunchKernelGGL((check_init_kernel<P>), dim3(1), dim3(64), 0, stream, static_cast<const P*>(indptr),   \
+                       n_rows, ck);                                                                           \
+    FS_CHECK_LAUNCH("check_init_kernel");                                                                     \
+    if (reinterpret_cast<uintptr_t>(indices) % 16 == 0)                                                       \
+      hipLaunchKernelGGL((check_stats_kernel<P, I, true>), dim3((unsigned)blocks), dim3(256), 0, stream,      \
+                         static_cast<const P*>(indptr), n_rows, static_cast<const I*>(indices), nnz, ck, st); \
+    else                                                                                                      \
+      hipLaunchKernelGGL((check_stats_kernel<P, I, false>), dim3((unsigned)blocks), dim3(256), 0, stream,     \
+                         static_cast<const P*>(indptr), n_rows, static_cast<const I*>(indices), nnz, ck, st); \
+    FS_CHECK_LAUNCH("check_stats_kernel");                                                                    \
+  } while (0)
+  if (ptr_t == FS_I32 && idx_t == FS_I32) FS_CHECK_STATS_CASE(int32_t, int32_t);
+  else if (ptr_t == FS_I32) FS_CHECK_STATS_CASE(int32_t, int64_t);
+  else if (idx_t == FS_I32) FS_CHECK_STATS_CASE(int64_t, int32_t);
+  else FS_CHECK_STATS_CASE(int64_t, int64_t);
+#undef FS_CHECK_STATS_CASE
   return FS_OK;
 }
 
@@ -1624,12 +1711,8 @@ extern "C" int fs_csr_check_analyze(const void* indptr, int ptr_t, const void* i
   init_plan(plan, ptr_t, idx_t, val_t, n_rows, n_cols, nnz);
   unsigned long long* ck = static_cast<unsigned long long*>(ws);
   unsigned long long* st = ck + 5;
-  rc = launch_check(indptr, ptr_t, indices, idx_t, n_rows, nnz, ck, stream);
+  rc = launch_check_stats(indptr, ptr_t, indices, idx_t, n_rows, nnz, ck, st, stream);
   if (rc != FS_OK) return rc;
-  if (n_rows > 0) {
-    rc = launch_stats(indptr, ptr_t, n_rows, st, stream);
-    if (rc != FS_OK) return rc;
-  }
   unsigned long long host[5 + kStatsWords] = {};
   FS_CHECK_HIP(hipMemcpyAsync(host, ck, (n_rows > 0 ? 5 + kStatsWords : 5) * sizeof(unsigned long long),
                               hipMemcpyDeviceToHost, stream));
