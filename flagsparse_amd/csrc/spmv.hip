@@ -459,15 +459,18 @@ __device__ inline void lds_copy16(const unsigned char* g, unsigned char* dst, in
   }
 }
 
+// SUBS lanes per row (4, 8, 16, 32 or 64): a 256-thread workgroup owns
+// 256 / SUBS rows, so rows of up to stream_items / (256 / SUBS) entries fit
+// the stage (f64: 32 entries at 4 lanes per row, 512 at 64).
 template <int SUBS, class V, class I, class P, bool DL>
-__global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
+__global__ __launch_bounds__(256) void spmv_stream_t_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
     const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_blocks, int remap, int stage) {
   using T = VT<V>;
   using A = typename T::acc;
-  constexpr int R = 64;             // rows per workgroup
-  constexpr int NT = 64 * SUBS;     // threads
+  constexpr int NT = 256;           // threads
   constexpr int RPW = 64 / SUBS;    // rows per wave
+  constexpr int R = 4 * RPW;        // rows per workgroup
   constexpr int K = stream_items<A>() / NT;
   extern __shared__ __align__(16) unsigned char t_lds[];
   const StreamTLayout L = stream_t_layout(stage, sizeof(V), sizeof(I), DL);
@@ -496,9 +499,9 @@ __global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
     oi = (int)(S - Si);
     constexpr int KV = (stream_items<A>() + 2 * EV + NT * EV - 1) / (NT * EV);
     constexpr int KI = (stream_items<A>() + 2 * EI + NT * EI - 1) / (NT * EI);
-    lds_copy16<SUBS, KV>(reinterpret_cast<const unsigned char*>(vals + Sv), reinterpret_cast<unsigned char*>(s_val),
+    lds_copy16<NT / 64, KV>(reinterpret_cast<const unsigned char*>(vals + Sv), reinterpret_cast<unsigned char*>(s_val),
                          (ov + cnt + EV - 1) / EV);
-    lds_copy16<SUBS, KI>(reinterpret_cast<const unsigned char*>(cols + Si), reinterpret_cast<unsigned char*>(s_col),
+    lds_copy16<NT / 64, KI>(reinterpret_cast<const unsigned char*>(cols + Si), reinterpret_cast<unsigned char*>(s_col),
                          (oi + cnt + EI - 1) / EI);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS copies have landed
   } else {
@@ -542,8 +545,8 @@ __global__ __launch_bounds__(64 * SUBS) void spmv_stream_t_kernel(
     }
   }
   A acc = add(add(acc0, acc1), add(acc2, acc3));
-  if constexpr (SUBS >= 4) acc = add(acc, shfl(acc, lane ^ 16));
-  if constexpr (SUBS >= 2) acc = add(acc, shfl(acc, lane ^ 32));
+#pragma unroll
+  for (int off = RPW; off < 64; off <<= 1) acc = add(acc, shfl(acc, lane ^ off));  // fixed order
   if (sub == 0 && r < rows) store_stream(y + rb0 + r, T::out(acc));
 }
 
@@ -1227,6 +1230,13 @@ inline bool stream_t_dl_enabled() {
   return !(e && std::atoi(e) == 0);
 }
 
+// K3t with eight lanes per row (32-row workgroups) for rows too long for
+// four lanes; FLAGSPARSE_SPMV_STREAM_T_WIDE=0 runs K3 there instead (A/B).
+inline bool stream_t_wide_enabled() {
+  const char* e = std::getenv("FLAGSPARSE_SPMV_STREAM_T_WIDE");
+  return !(e && std::atoi(e) == 0);
+}
+
 inline int xcd_remap() {
   if (const char* e = std::getenv("FLAGSPARSE_XCD_REMAP")) return std::atoi(e) != 0;
   return 0;  // measured neutral (within 5%) on the stencil and uniform matrices
@@ -1283,24 +1293,36 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
       return fail(FS_E_INVALID, "fs_spmv_csr: rows_per_block does not fit the stream kernel");
     // (the dispatch counts work-items in 32 bits: beyond 2^32 threads, K3's
     // larger row blocks run instead)
-    if (stream_t_enabled() && (int64_t)plan->max_row * 64 <= stream_items<Acc>() &&
-        ceil_div(n_rows, (int64_t)64) * 256 < (int64_t(1) << 32)) {
-      const int64_t blocks = ceil_div(n_rows, (int64_t)64);
+    // four lanes per row (64 rows per workgroup) when 64 rows fit the stage,
+    // else eight (32 rows): the rows the stream plan admits (f64: up to 64
+    // entries) all fit one or the other.
+    const int subs = (int64_t)plan->max_row * 64 <= stream_items<Acc>() ? 4
+                   : ((int64_t)plan->max_row * 32 <= stream_items<Acc>() && stream_t_wide_enabled()) ? 8 : 0;
+    const int64_t rows_per_wg = subs ? 256 / subs : 1;
+    if (stream_t_enabled() && subs && ceil_div(n_rows, rows_per_wg) * 256 < (int64_t(1) << 32)) {
+      const int64_t blocks = ceil_div(n_rows, rows_per_wg);
       const int remap = xcd_remap();
       dim3 g((unsigned)(remap ? ceil_div(blocks, kXcds) * kXcds : blocks));
-      const int stage = (int)std::max<int64_t>(64 * plan->max_row, 1);
+      const int stage = (int)std::max<int64_t>(rows_per_wg * plan->max_row, 1);
       // direct-to-LDS staging needs 16-byte aligned value / index arrays
       const bool dl = stream_t_dl_enabled() && ((uintptr_t)v % 16) == 0 && ((uintptr_t)c % 16) == 0;
       const size_t lds = stream_t_layout(stage, sizeof(V), sizeof(I), dl).total;
       // four lanes per row: 16 rows per gather instruction.  One or two lanes
       // per row (64 / 32 rows per instruction, 64- / 128-thread workgroups)
       // measured slower on the f64 stencil: 0.176 / 0.150 against 0.136 ms.
-      if (dl)
-        hipLaunchKernelGGL((spmv_stream_t_kernel<4, V, I, P, true>), g, dim3(256), lds, stream, v, c, p, xv, yv,
-                           n_rows, blocks, remap, stage);
-      else
-        hipLaunchKernelGGL((spmv_stream_t_kernel<4, V, I, P, false>), g, dim3(256), lds, stream, v, c, p, xv, yv,
-                           n_rows, blocks, remap, stage);
+      auto launch = [&](auto sc, auto dc) {
+        hipLaunchKernelGGL((spmv_stream_t_kernel<decltype(sc)::value, V, I, P, decltype(dc)::value>), g, dim3(256),
+                           lds, stream, v, c, p, xv, yv, n_rows, blocks, remap, stage);
+      };
+      using S4 = std::integral_constant<int, 4>;
+      using S8 = std::integral_constant<int, 8>;
+      if (subs == 4) {
+        if (dl) launch(S4{}, std::true_type{});
+        else launch(S4{}, std::false_type{});
+      } else {
+        if (dl) launch(S8{}, std::true_type{});
+        else launch(S8{}, std::false_type{});
+      }
       FS_CHECK_LAUNCH("spmv_stream_t_kernel");
       return FS_OK;
     }

@@ -911,8 +911,10 @@ def _spmv_kernel_symbol(prepared):
     if name == "stream":
         plan = prepared.hip_plan().plan
         items = 16384 // (16 if prepared.compute_data().dtype.is_complex else 8)
-        t_ok = (os.environ.get("FLAGSPARSE_SPMV_STREAM_T", "1") != "0" and int(plan.max_row) * 64 <= items
-                and -(-int(plan.n_rows) // 64) * 256 < (1 << 32))
+        wide = os.environ.get("FLAGSPARSE_SPMV_STREAM_T_WIDE", "1") != "0"
+        rows = 64 if int(plan.max_row) * 64 <= items else (32 if wide and int(plan.max_row) * 32 <= items else 0)
+        t_ok = (os.environ.get("FLAGSPARSE_SPMV_STREAM_T", "1") != "0" and rows > 0
+                and -(-int(plan.n_rows) // rows) * 256 < (1 << 32))
         return "spmv_stream_t_kernel" if t_ok else "spmv_stream_kernel"
     if name == "panel":
         pc = prepared._panels

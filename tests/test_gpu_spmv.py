@@ -861,3 +861,27 @@ def test_stream_t_misaligned_arrays_match(device, monkeypatch, dtype):
     assert torch.equal(y, y_mis)
     ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
     assert rel_err(np_(y), ref) <= REL_TOL[dtype]
+
+
+@pytest.mark.parametrize("per_row", [33, 48, 64])
+@pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+def test_stream_t_eight_lanes_per_row(device, monkeypatch, per_row, dtype, index_dtype):
+    """Rows of 33-64 entries (too long for four lanes per row in a 64-row
+    block): K3t with eight lanes per row and 32-row blocks, against the oracle,
+    and against the entry-order row-block kernel K3 within rounding."""
+    for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_STREAM_T_WIDE",
+              "FLAGSPARSE_SPMV_STREAM_T"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "0")
+    data, indices, indptr, sh = S.uniform_rows(3001, 2500, per_row, dtype, index_dtype, device, seed=per_row)
+    x = S.vector(sh[1], dtype, device, seed=6)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
+    if per_row * 32 <= (1024 if dtype.is_complex else 2048):
+        assert spmv_mod._spmv_kernel_symbol(prep) == "spmv_stream_t_kernel"
+    y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
+    assert rel_err(np_(y), ref) <= REL_TOL[dtype]
+    monkeypatch.setenv("FLAGSPARSE_SPMV_STREAM_T_WIDE", "0")
+    y3 = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert rel_err(np_(y3), ref) <= REL_TOL[dtype]
