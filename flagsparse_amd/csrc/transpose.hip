@@ -485,14 +485,35 @@ __global__ __launch_bounds__(256) void unpack_kernel(const uint2* __restrict__ p
   t_cols[k] = (OI)w.y;
 }
 
+// colptr[c] = first position whose key is >= c.  Thread k owns positions
+// [kW, kW + W) (one 16-byte load of its keys, plus the key before them) and
+// writes the pointers of the columns that start there; the thread at nnz
+// writes the trailing ones.
 template <class K, class OP>
 __global__ __launch_bounds__(256) void colptr_kernel(const K* __restrict__ keys, int64_t nnz, int64_t n_cols,
                                                      OP* __restrict__ colptr) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k > nnz) return;
-  const int64_t prev = k > 0 ? (int64_t)keys[k - 1] : -1;
-  const int64_t cur = k < nnz ? (int64_t)keys[k] : n_cols;
-  for (int64_t c = prev + 1; c <= cur; ++c) colptr[c] = (OP)k;
+  constexpr int W = 16 / (int)sizeof(K);
+  const int64_t k0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * W;
+  if (k0 > nnz) return;
+  K kv[W];
+  if (k0 + W <= nnz && ((uintptr_t)keys % 16) == 0) {
+    typedef K vec_t __attribute__((ext_vector_type(W)));
+    const vec_t v = *reinterpret_cast<const vec_t*>(keys + k0);
+#pragma unroll
+    for (int w = 0; w < W; ++w) kv[w] = v[w];
+  } else {
+#pragma unroll
+    for (int w = 0; w < W; ++w) kv[w] = k0 + w < nnz ? keys[k0 + w] : (K)0;
+  }
+  int64_t prev = k0 > 0 ? (int64_t)keys[k0 - 1] : -1;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const int64_t k = k0 + w;
+    if (k > nnz) break;
+    const int64_t cur = k < nnz ? (int64_t)kv[w] : n_cols;
+    for (int64_t c = prev + 1; c <= cur; ++c) colptr[c] = (OP)k;
+    prev = cur;
+  }
 }
 
 template <class OP>
@@ -650,7 +671,7 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
                          reinterpret_cast<const uint2*>(sorted), nnz, static_cast<V*>(t_vals),
                          static_cast<OI*>(t_cols));
       FS_CHECK_LAUNCH("unpack_kernel");
-      hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
+      hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(ceil_div(nnz + 1, 16 / (int64_t)sizeof(K)), 256)), dim3(256), 0, s, keys, nnz,
                          n_cols, static_cast<OP*>(t_indptr));
       FS_CHECK_LAUNCH("colptr_kernel");
       (void)conj;
@@ -687,7 +708,7 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
         hipLaunchKernelGGL((transpose_gather_packed16_kernel<V, OI, Pos>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256),
                            0, s, packed, perm, nnz, conj, static_cast<V*>(t_vals), static_cast<OI*>(t_cols));
         FS_CHECK_LAUNCH("transpose_gather_packed16_kernel");
-        hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
+        hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(ceil_div(nnz + 1, 16 / (int64_t)sizeof(K)), 256)), dim3(256), 0, s, keys, nnz,
                            n_cols, static_cast<OP*>(t_indptr));
         FS_CHECK_LAUNCH("colptr_kernel");
         return FS_OK;
@@ -702,7 +723,7 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
                        static_cast<OI*>(t_cols));
     FS_CHECK_LAUNCH("transpose_gather_kernel");
   }
-  hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(nnz + 1, 256)), dim3(256), 0, s, keys, nnz,
+  hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(ceil_div(nnz + 1, 16 / (int64_t)sizeof(K)), 256)), dim3(256), 0, s, keys, nnz,
                      n_cols, static_cast<OP*>(t_indptr));
   FS_CHECK_LAUNCH("colptr_kernel");
   return FS_OK;
