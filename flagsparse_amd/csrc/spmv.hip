@@ -1242,6 +1242,32 @@ inline int xcd_remap() {
   return 0;  // measured neutral (within 5%) on the stencil and uniform matrices
 }
 
+// Resident workgroups per CU of kernel `kern` at 256 threads and `lds`
+// bytes of dynamic LDS, cached per (kernel, device, lds) so that the
+// persistent launches do not query the runtime on every call.
+template <class F>
+inline int resident_per_cu(F kern, size_t lds) {
+  struct Entry {
+    const void* k;
+    int dev;
+    size_t lds;
+    int n;
+  };
+  static thread_local Entry cache[16];
+  static thread_local int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  const void* key = reinterpret_cast<const void*>(kern);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == key && cache[i].dev == dev && cache[i].lds == lds) return cache[i].n;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess || n <= 0) n = 1;
+  Entry e{key, dev, lds, n};
+  if (used < 16) cache[used++] = e;
+  else cache[(dev < 0 ? 0 : dev) % 16] = e;
+  return n;
+}
+
 // Compute units of the current device (cached per device id).
 inline int device_cus() {
   static int cached[64] = {0};
@@ -1378,8 +1404,7 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
   A* tail = head + n_tiles;
   const int64_t blocks = ceil_div(n_tiles, kMergeWaves);
   if (plan->nnz > 0 && merge_pipe_enabled()) {
-    int per_cu = 0;
-    FS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, spmv_merge_pipe_kernel<V, I, P>, 256, 0));
+    const int per_cu = resident_per_cu(spmv_merge_pipe_kernel<V, I, P>, 0);
     const int64_t wgs = std::min<int64_t>(blocks, (int64_t)device_cus() * std::max(per_cu, 1));
     hipLaunchKernelGGL((spmv_merge_pipe_kernel<V, I, P>), dim3((unsigned)wgs), dim3(256), 0, stream, v, c, p, xv, yv,
                        static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
@@ -1464,8 +1489,7 @@ int launch_spmv_panels(const fs_csr_plan* plan, int n_panels, const int64_t* pan
     // 0.633; 2 / 3 / 4 workgroups per CU 0.571 / 0.582 / 0.571.  The x
     // gathers' L2 request rate bounds it, not the latency the pipeline hides.
     auto launch = [&](auto kern) -> int {
-      int per_cu = 0;
-      FS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds_pad));
+      int per_cu = resident_per_cu(kern, lds_pad);
       if (cap > 0) per_cu = std::min(per_cu, cap);
       const int64_t wgs = std::max<int64_t>(1, (int64_t)(device_cus() / kXcds) * std::max(per_cu, 1));
       hipLaunchKernelGGL(kern, dim3((unsigned)(std::min(wgs, per_xcd) * kXcds)), dim3(256), lds_pad, stream,
