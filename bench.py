@@ -443,6 +443,52 @@ def copy_calibration(args):
     print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "launches": max(1, args.steps)}))
 
 
+def gather_floor(args):
+    """The SpMM configs' B-row gathers alone (fs_diag_gather_rows): the same
+    rows in the same order as the SpMM kernel reads them, with nothing else in
+    flight.  One JSON line per config: the gather time next to the SpMM
+    kernel time from run_config."""
+    import torch
+
+    from flagsparse_amd import _lib
+    from flagsparse_amd import synthetic as S
+
+    device = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(device)
+    lib = _lib.lib()
+    names = [args.config] if args.config else [n for n in CONFIG_ORDER if CONFIGS[n]["op_kind"] == "spmm"]
+    for name in names:
+        cfg = CONFIGS[name]
+        if cfg["op_kind"] != "spmm":
+            continue
+        data, indices, indptr, shape = generate(cfg, device)
+        if cfg["op"] != "non":
+            from flagsparse_amd import _csr
+
+            data, indices, indptr, shape = _csr.transpose_csr(data, indices, indptr, shape, conj=cfg["op"] == "conj")
+        n_dense = cfg["n"]
+        B = S.dense(shape[1], n_dense, data.dtype, device, seed=13)
+        row_bytes = n_dense * data.element_size()
+        chk = torch.zeros(1, dtype=torch.int32, device=device)
+        call = lambda: lib.fs_diag_gather_rows(  # noqa: E731
+            _lib.index_code(indices.dtype), _lib.ptr(B), shape[1], row_bytes, _lib.ptr(indices), indices.numel(),
+            _lib.ptr(chk), _lib.stream_handle(device))
+        _lib.check(call(), "fs_diag_gather_rows")
+        for _ in range(max(1, args.warmup)):
+            call()
+        ms = time_loop(call, args.steps, stream)
+        gathered = indices.numel() * row_bytes
+        spmm = run_config(name, argparse.Namespace(**{**vars(args), "no_cpu": True}))
+        print(json.dumps({
+            "workload": name, "gather_floor_ms": round(ms, 5), "rows_gathered": int(indices.numel()),
+            "row_bytes": row_bytes, "gathered_GBps": round(gathered / ms / 1e6, 1),
+            "spmm_kernel": spmm["roofline"]["kernel"], "spmm_kernel_ms": spmm["roofline"]["kernel_ms"],
+            "spmm_over_floor": round(spmm["roofline"]["kernel_ms"] / ms, 3),
+        }), flush=True)
+        del data, indices, indptr, B
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -454,6 +500,8 @@ def main():
     ap.add_argument("--traffic-bytes", type=float, default=None,
                     help="HBM bytes per launch measured with rocprofv3 FETCH_SIZE+WRITE_SIZE (scaled)")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--gather-floor", action="store_true",
+                    help="time the SpMM configs' B-row gathers alone (fs_diag_gather_rows) beside the SpMM kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -467,6 +515,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args)
+        return
+    if args.gather_floor:
+        gather_floor(args)
         return
     if args.config:
         print(json.dumps(run_config(args.config, args)), flush=True)

@@ -71,6 +71,7 @@ EXPORTED_SYMBOLS = (
     "fs_sell_max_offset",
     "fs_csr_to_sell",
     "fs_spmv_sell",
+    "fs_diag_gather_rows",
 )
 
 
@@ -185,6 +186,8 @@ def _declare(lib):
     lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_sell.restype = _i32
     lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.fs_diag_gather_rows.restype = _i32
+    lib.fs_diag_gather_rows.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _vp]
 
 
 def load_library(path=None):

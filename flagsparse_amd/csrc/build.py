@@ -22,7 +22,7 @@ REPO = os.path.dirname(PKG)
 OUT = os.path.join(PKG, "libflagsparse_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["abi.cpp", "spmv.hip", "spmv_opt.hip", "spmm.hip", "spmm_group.hip", "transpose.hip", "sell.hip"]
+SOURCES = ["abi.cpp", "spmv.hip", "spmv_opt.hip", "spmm.hip", "spmm_group.hip", "transpose.hip", "sell.hip", "diag.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

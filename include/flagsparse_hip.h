@@ -369,6 +369,17 @@ int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_row
                  const int32_t* code_table, const int64_t* slice_ptr,
                  const void* indptr, const void* x, void* y, hipStream_t stream);
 
+/* ---- Diagnostic (no counterpart in the reference) -------------------------
+ * fs_diag_gather_rows gathers the rows idx[0..n_idx) of a row-major B of
+ * n_b_rows rows of row_bytes bytes (a power of two in [16, 1024]; B 16-byte
+ * aligned; every idx value in [0, n_b_rows)) with nothing else in flight, and
+ * XORs the loaded words into *checksum (one uint32 of device memory).  It
+ * measures the gather floor an SpMM with the same column order cannot beat
+ * (bench.py --gather-floor).  Does not synchronise `stream`.
+ */
+int fs_diag_gather_rows(int idx_t, const void* B, int64_t n_b_rows, int64_t row_bytes,
+                        const void* idx, int64_t n_idx, void* checksum, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
