@@ -443,11 +443,67 @@ def copy_calibration(args):
     print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "launches": max(1, args.steps)}))
 
 
+def _gather_floor_spmv(name, cfg, args, lib, device, stream):
+    """SpMV: the x gathers alone, in the order the prepared kernel reads them
+    (panel by panel for a column-panelled matrix, one launch per panel, so a
+    launch's footprint is one x slice as in the panel kernel), and in plain
+    CSR order in one launch."""
+    import torch
+
+    import flagsparse_amd as fs
+    from flagsparse_amd import _lib
+    from flagsparse_amd import synthetic as S
+
+    data, indices, indptr, shape = generate(cfg, device)
+    prep = fs.prepare_spmv_csr(data, indices, indptr, shape)
+    x = S.vector(shape[1], data.dtype, device, seed=11)
+    esz = x.element_size()
+    chk = torch.zeros(1, dtype=torch.int32, device=device)
+    sh = _lib.stream_handle(device)
+
+    def launcher(idx_t, base_ptr, isz, lo, hi):
+        return lambda: lib.fs_diag_gather_rows(idx_t, _lib.ptr(x), shape[1], esz, base_ptr + lo * isz, hi - lo,
+                                               _lib.ptr(chk), sh)
+
+    calls = []
+    pan = prep._panels
+    if pan is not None:
+        pn = [int(pan.panel_nnz[q]) for q in range(pan.n_panels + 1)]
+        isz = pan.indices.element_size()
+        calls = [launcher(_lib.index_code(pan.indices.dtype), pan.indices.data_ptr(), isz, pn[q], pn[q + 1])
+                 for q in range(pan.n_panels) if pn[q + 1] > pn[q]]
+    plain = launcher(_lib.index_code(indices.dtype), indices.data_ptr(), indices.element_size(), 0, indices.numel())
+
+    def seq():
+        for c in calls:
+            _lib.check(c(), "fs_diag_gather_rows")
+
+    _lib.check(plain(), "fs_diag_gather_rows")
+    for _ in range(max(1, args.warmup)):
+        seq()
+        plain()
+    ms_panels = time_loop(seq, args.steps, stream) if calls else None
+    ms_plain = time_loop(plain, args.steps, stream)
+    spmv = run_config(name, argparse.Namespace(**{**vars(args), "no_cpu": True}))
+    floor = ms_panels if ms_panels is not None else ms_plain
+    print(json.dumps({
+        "workload": name, "gather_floor_ms": round(floor, 5),
+        "gather_floor_order": "panel by panel" if ms_panels is not None else "CSR order",
+        "gather_csr_order_ms": round(ms_plain, 5), "entries_gathered": int(indices.numel()), "entry_bytes": esz,
+        "gathers_per_ns": round(indices.numel() / floor / 1e6, 1),
+        "spmv_kernel": spmv["roofline"]["kernel"], "spmv_kernel_ms": spmv["roofline"]["kernel_ms"],
+        "spmv_over_floor": round(spmv["roofline"]["kernel_ms"] / floor, 3),
+    }), flush=True)
+    del data, indices, indptr, prep, x
+    torch.cuda.empty_cache()
+
+
 def gather_floor(args):
-    """The SpMM configs' B-row gathers alone (fs_diag_gather_rows): the same
-    rows in the same order as the SpMM kernel reads them, with nothing else in
-    flight.  One JSON line per config: the gather time next to the SpMM
-    kernel time from run_config."""
+    """The gathers alone (fs_diag_gather_rows): for the SpMM configs the same
+    B rows in the same order as the SpMM kernel reads them, for the
+    power-law SpMV configs the x entries; nothing else in flight.  One JSON
+    line per config: the gather time next to the kernel time from
+    run_config."""
     import torch
 
     from flagsparse_amd import _lib
@@ -456,10 +512,12 @@ def gather_floor(args):
     device = torch.device("cuda:0")
     stream = torch.cuda.current_stream(device)
     lib = _lib.lib()
-    names = [args.config] if args.config else [n for n in CONFIG_ORDER if CONFIGS[n]["op_kind"] == "spmm"]
+    names = [args.config] if args.config else [n for n in CONFIG_ORDER if CONFIGS[n]["gen"] in ("powerlaw",)
+                                                 or CONFIGS[n]["op_kind"] == "spmm"]
     for name in names:
         cfg = CONFIGS[name]
-        if cfg["op_kind"] != "spmm":
+        if cfg["op_kind"] == "spmv":
+            _gather_floor_spmv(name, cfg, args, lib, device, stream)
             continue
         data, indices, indptr, shape = generate(cfg, device)
         if cfg["op"] != "non":
@@ -501,7 +559,7 @@ def main():
                     help="HBM bytes per launch measured with rocprofv3 FETCH_SIZE+WRITE_SIZE (scaled)")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--gather-floor", action="store_true",
-                    help="time the SpMM configs' B-row gathers alone (fs_diag_gather_rows) beside the SpMM kernel")
+                    help="time the SpMM / power-law SpMV configs' gathers alone (fs_diag_gather_rows) beside the kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(

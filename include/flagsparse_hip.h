@@ -371,8 +371,9 @@ int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_row
 
 /* ---- Diagnostic (no counterpart in the reference) -------------------------
  * fs_diag_gather_rows gathers the rows idx[0..n_idx) of a row-major B of
- * n_b_rows rows of row_bytes bytes (a power of two in [16, 1024]; B 16-byte
- * aligned; every idx value in [0, n_b_rows)) with nothing else in flight, and
+ * n_b_rows rows of row_bytes bytes (a power of two in [4, 1024]; B aligned to
+ * min(row_bytes, 16) bytes; every idx value in [0, n_b_rows); rows of 4 or 8
+ * bytes are SpMV x entries) with nothing else in flight, and
  * XORs the loaded words into *checksum (one uint32 of device memory).  It
  * measures the gather floor an SpMM with the same column order cannot beat
  * (bench.py --gather-floor).  Does not synchronise `stream`.

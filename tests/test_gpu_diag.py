@@ -10,14 +10,14 @@ from flagsparse_amd import _lib
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("row_bytes", [16, 64, 256, 1024])
+@pytest.mark.parametrize("row_bytes", [4, 8, 16, 64, 256, 1024])
 @pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64], ids=["i32", "i64"])
 def test_gather_rows_checksum(device, row_bytes, idx_dtype):
     g = torch.Generator(device="cpu").manual_seed(row_bytes)
     n_rows = 5000
     words = row_bytes // 4
     B = torch.randint(0, 2**31 - 1, (n_rows, words), generator=g, dtype=torch.int32)
-    group = 64 // (row_bytes // 16)
+    group = 64 // (row_bytes // 16) if row_bytes >= 16 else 64
     n_idx = 8 * group * 37  # whole batches: no index is repeated past the end
     idx = torch.randint(0, n_rows, (n_idx,), generator=g, dtype=torch.int64)
     expect = np.bitwise_xor.reduce(B[idx].numpy().view(np.uint32).reshape(-1))
@@ -36,7 +36,7 @@ def test_gather_rows_rejects_bad_row_bytes(device):
     B = torch.zeros(4, 8, dtype=torch.int32, device=device)
     idx = torch.zeros(4, dtype=torch.int32, device=device)
     chk = torch.zeros(1, dtype=torch.int32, device=device)
-    rc = _lib.lib().fs_diag_gather_rows(_lib.index_code(torch.int32), _lib.ptr(B), 4, 24, _lib.ptr(idx), 4,
+    rc = _lib.lib().fs_diag_gather_rows(_lib.index_code(torch.int32), _lib.ptr(B), 4, 12, _lib.ptr(idx), 4,
                                         _lib.ptr(chk), _lib.stream_handle(device))
     assert rc != 0
     assert b"row_bytes" in _lib.lib().fs_last_error()
