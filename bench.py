@@ -27,6 +27,7 @@ the fp64 oracle.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -35,6 +36,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+SAMPLE_MIN_FRAC = 0.01  # cpu_baseline / accuracy sample: at least 1% of nnz
 SETTLE_S = 0.2  # untimed back-to-back steps before the warm-up (clock ramp)
 METRIC = "effective HBM GB/s (% of peak) + GFLOP/s for CSR SpMV/SpMM, 1 MI355X"
 
@@ -52,20 +54,39 @@ CONFIGS = {
 DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 CONFIG_ORDER = [DEFAULT_CONFIG] + [c for c in CONFIGS if c != DEFAULT_CONFIG]
 
-# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE and
-# WRITE_SIZE passes scaled by a 1 GiB copy calibration (the commands and raw
-# counts are in profiles/<kernel>_<workload>.md).  Reported as
-# roofline.traffic; configs not profiled with the current kernels report null.
-MEASURED_TRAFFIC = {
-    "c1_spmv_uniform4096_f32_i32": 0.755e6,
-    "c2_spmv_stencil128_f64_i32": 583.5e6,
-    "c3_spmv_powerlaw4M_f32_i32": 1989.0e6,
-    "c3_spmv_powerlaw4M_f32_i64": 1987.5e6,
-    "c4_spmm_uniform1M_f32_i32_n64_non": 9265.1e6,
-    "c4_spmm_uniform1M_f32_i32_n64_trans": 9274.4e6,
-    "c5_spmm_rmat21_f32_i64_n256_non": 30700.3e6,
-    "c5_spmm_rmat21_c64_i64_n32_conj": 7227.6e6,
-}
+PROFILES_DIR = os.path.join(ROOT, "profiles")
+
+
+def profile_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload`, from the committed
+    rocprofv3 summary profiles/<kernel>_<...>.md whose header reads
+    "# <kernel> — <workload>" and whose table ends in a "| total | ... MB"
+    row (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration).
+
+    Returns (bytes or None, note).  A summary of the workload for another
+    kernel is stale (the kernel changed since it was measured): its figure
+    is not reported, the note says which kernel it covered."""
+    stale = None
+    try:
+        names = sorted(os.listdir(PROFILES_DIR))
+    except OSError:
+        return None, "no profiles/ directory"
+    for fn in names:
+        if not fn.endswith(".md"):
+            continue
+        with open(os.path.join(PROFILES_DIR, fn)) as f:
+            text = f.read()
+        m = re.match(r"# (\S+) \u2014 (\S+)", text)
+        if not m or m.group(2) != workload:
+            continue
+        t = re.search(r"^\| total \|[^\n]*?([0-9][0-9,]*\.?[0-9]*) MB", text, re.M)
+        if t is None:
+            continue
+        if m.group(1) != kernel:
+            stale = f"profiles/{fn} measured {m.group(1)}, not {kernel}: traffic not reported"
+            continue
+        return float(t.group(1).replace(",", "")) * 1e6, f"profiles/{fn}"
+    return None, stale or f"no FETCH_SIZE/WRITE_SIZE summary for {kernel} on {workload} under profiles/"
 
 
 def _dtypes(torch):
@@ -122,6 +143,7 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz, g
     the GPU output `gpu_out` on the sampled rows against the fp64 oracle
     (the reference's normwise metric, spmm_csr.py:95-103)."""
     import numpy as np
+    import torch
 
     from oracle import cpu_baseline as CB
 
@@ -129,7 +151,6 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz, g
     i = indices.cpu().numpy()
     p = indptr.cpu().numpy().astype(np.int64)
     R = rhs.cpu().numpy()
-    n_rows = shape[0]
     op = cfg["op"]
     if cfg["op_kind"] == "spmm" and op != "non":
         # A^T / A^H once (not timed), then rows of it: same sample policy as op=non.
@@ -138,22 +159,21 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz, g
         A = sp.csr_matrix((d, i, p), shape=shape)
         A = (A.conj() if op == "conj" else A).T.tocsr()
         d, i, p, shape = A.data, A.indices, A.indptr.astype(np.int64), A.shape
-        n_rows = shape[0]
         op = "non"
     budget = 1e8 if cfg["op_kind"] == "spmv" else 5e7 / max(1, R.shape[1] if R.ndim == 2 else 1)
-    rows = n_rows
-    if p[-1] > budget:
-        rows = int(np.searchsorted(p, budget))
-        rows = max(1, min(rows, n_rows))
-    nnz_s = int(p[rows])
-    secs, reps = CB.time_scipy(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R, op=op, min_seconds=2.0)
+    target = max(budget, SAMPLE_MIN_FRAC * float(p[-1]))
+    rows_sel, ds, is_, ps = strided_row_sample(d, i, p, target)
+    nnz_s = int(ps[-1])
+    n_s = int(rows_sel.size)
+    secs, reps = CB.time_scipy(ds, is_, ps, (n_s, shape[1]), R, op=op, min_seconds=2.0)
     frac = nnz_s / max(1, full_nnz)
     value = full_bytes * frac / secs / 1e9
     info = CB.host_info()
     # the other CPU path the reference compares against: torch.sparse.mm on a
     # CPU CSR tensor, all torch threads, same sample (1 s budget)
-    t_secs, t_reps, t_threads = CB.time_torch_cpu(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R,
-                                                  min_seconds=1.0)
+    t_secs, t_reps, t_threads = CB.time_torch_cpu(ds, is_, ps, (n_s, shape[1]), R, min_seconds=1.0)
+    stride = int(rows_sel[1] - rows_sel[0]) if n_s > 1 else 1
+    sample = f"every {stride}-th row of the same matrix ({n_s} rows, {nnz_s} of {full_nnz} nnz = {100.0 * frac:.2f}%)"
     torch_leg = {
         "value": round(full_bytes * frac / t_secs / 1e9, 3),
         "unit": "GB/s",
@@ -167,12 +187,36 @@ def cpu_baseline(cfg, data, indices, indptr, shape, rhs, full_bytes, full_nnz, g
         "kind": "port",
         "sample": (
             f"scipy.sparse csr_matrix @ {'x' if R.ndim == 1 else 'B'} (the reference's CPU path), native dtype, "
-            f"rows [0,{rows}) of the same matrix ({nnz_s} of {full_nnz} nnz), median of {reps} runs "
-            f"({secs * 1e3:.2f} ms each); value = full algorithmic bytes x sampled nnz fraction / time; "
-            f"host {info['model']}, {info['affinity']} cores visible"
+            f"{sample}, median of {reps} runs ({secs * 1e3:.2f} ms each); value = full algorithmic bytes x "
+            f"sampled nnz fraction / time; host {info['model']}, {info['affinity']} cores visible"
         ),
         "torch_sparse_mm": torch_leg,
-    }, _accuracy(d[:nnz_s], i[:nnz_s], p[: rows + 1], (rows, shape[1]), R, gpu_out[:rows])
+    }, _accuracy(ds, is_, ps, (n_s, shape[1]), R, gpu_out[torch.from_numpy(rows_sel).to(gpu_out.device)])
+
+
+def strided_row_sample(d, i, p, target_nnz):
+    """Rows 0, k, 2k, ... of a CSR matrix, k the largest stride whose sample
+    holds at least `target_nnz` entries (all rows when the matrix has fewer):
+    the sample spreads over the whole row range instead of a leading prefix
+    (which on a graph is its hub rows).  Returns (row ids, data, indices,
+    indptr) of the sampled sub-matrix, same columns."""
+    import numpy as np
+
+    n_rows = p.size - 1
+    total = float(p[-1])
+    if total <= target_nnz or n_rows <= 1:
+        rows = np.arange(n_rows, dtype=np.int64)
+    else:
+        lens = np.diff(p)
+        k = max(1, int(total // max(1.0, target_nnz)))
+        while k > 1 and float(lens[::k].sum()) < target_nnz:
+            k = max(1, k * 3 // 4) if k > 4 else k - 1
+        rows = np.arange(0, n_rows, k, dtype=np.int64)
+    lens = (p[rows + 1] - p[rows]).astype(np.int64)
+    ps = np.zeros(rows.size + 1, dtype=np.int64)
+    np.cumsum(lens, out=ps[1:])
+    take = np.repeat(p[rows] - ps[:-1], lens) + np.arange(int(ps[-1]), dtype=np.int64)
+    return rows, d[take], i[take], ps
 
 
 def _accuracy(d, i, p, shape, R, out_rows):
@@ -276,9 +320,6 @@ def run_config(name, args):
             extra["n_panels"] = pan.n_panels
         bytes_alg = S.bytes_spmv(nnz, prep.n_rows, prep.n_cols, vb, ib, pb)
         flops = S.flops_spmv(nnz, complex_values)
-        from flagsparse_amd.spmv_csr import _spmv_kernel_symbol
-
-        kernel_name = _spmv_kernel_symbol(prep)
         extra.update(kernel_variant=prep.kernel_name, max_row_nnz=plan.max_row_nnz, analysis_ms=round(analysis_ms, 3))
         if cfg["gen"] == "stencil":
             extra["one_shot"] = _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for=(
@@ -315,9 +356,6 @@ def run_config(name, args):
         kernel_call = lambda: lib.fs_spmm_csr(*args_abi)  # noqa: E731
         bytes_alg = S.bytes_spmm(nnz, m, k, n_dense, vb, ib, pb)
         flops = S.flops_spmm(nnz, n_dense, complex_values)
-        from flagsparse_amd.spmm_csr import _spmm_kernel_name
-
-        kernel_name = _spmm_kernel_name(plan, data.dtype, n_dense)
         extra.update(max_row_nnz=plan.csr.max_row_nnz, analysis_ms=round(analysis_ms, 3), n_dense=n_dense)
         if op != "non":
             # Public call including the per-call transpose (reference semantics).
@@ -340,8 +378,13 @@ def run_config(name, args):
     rc = kernel_call()
     if rc != 0:
         raise RuntimeError(lib.fs_last_error().decode())
+    kernel_name = _lib.last_kernel()  # the main kernel that launch ran
     kernel_ms = time_loop(kernel_call, args.steps, stream)
 
+    if args.traffic_bytes is not None:
+        traffic, traffic_note = args.traffic_bytes, "--traffic-bytes"
+    else:
+        traffic, traffic_note = profile_traffic(name, kernel_name)
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
     achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
     dtype_name = {"f32": "f32 (fp64 accumulate)", "f64": "f64", "c64": "c64 (fp64 accumulate)"}[cfg["dtype"]]
@@ -379,7 +422,8 @@ def run_config(name, args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": args.traffic_bytes if args.traffic_bytes is not None else MEASURED_TRAFFIC.get(name),
+            "traffic": traffic,
+            "traffic_source": traffic_note,
         },
         "extra": dict(extra, generate_s=round(gen_s, 2)),
     }
@@ -418,12 +462,11 @@ def _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for, ste
     kern = lambda: lib.fs_spmv_csr(*abi)  # noqa: E731
     for _ in range(20):
         kern()
+    kernel_name = _lib.last_kernel()
     k_ms = time_loop(kern, steps, stream)
-    from flagsparse_amd.spmv_csr import _spmv_kernel_symbol
-
     return {
         "ms_per_call": round(ms_call, 5),
-        "kernel": _spmv_kernel_symbol(prep),
+        "kernel": kernel_name,
         "kernel_ms": round(k_ms, 5),
         "achieved": round(bytes_alg_for / (k_ms * 1e-3) / 1e9, 2),
         "frac": round(bytes_alg_for / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -441,6 +484,13 @@ def copy_calibration(args):
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "launches": max(1, args.steps)}))
+
+
+def _diag_check(rc):
+    if rc != 0:
+        from flagsparse_amd import _lib
+
+        raise RuntimeError("fs_diag_gather_rows: " + _lib.diag_lib().fs_last_error().decode())
 
 
 def _gather_floor_spmv(name, cfg, args, lib, device, stream):
@@ -476,9 +526,9 @@ def _gather_floor_spmv(name, cfg, args, lib, device, stream):
 
     def seq():
         for c in calls:
-            _lib.check(c(), "fs_diag_gather_rows")
+            _diag_check(c())
 
-    _lib.check(plain(), "fs_diag_gather_rows")
+    _diag_check(plain())
     for _ in range(max(1, args.warmup)):
         seq()
         plain()
@@ -511,7 +561,7 @@ def gather_floor(args):
 
     device = torch.device("cuda:0")
     stream = torch.cuda.current_stream(device)
-    lib = _lib.lib()
+    lib = _lib.diag_lib()
     names = [args.config] if args.config else [n for n in CONFIG_ORDER if CONFIGS[n]["gen"] in ("powerlaw",)
                                                  or CONFIGS[n]["op_kind"] == "spmm"]
     for name in names:
@@ -531,7 +581,7 @@ def gather_floor(args):
         call = lambda: lib.fs_diag_gather_rows(  # noqa: E731
             _lib.index_code(indices.dtype), _lib.ptr(B), shape[1], row_bytes, _lib.ptr(indices), indices.numel(),
             _lib.ptr(chk), _lib.stream_handle(device))
-        _lib.check(call(), "fs_diag_gather_rows")
+        _diag_check(call())
         for _ in range(max(1, args.warmup)):
             call()
         ms = time_loop(call, args.steps, stream)
@@ -588,11 +638,41 @@ def main():
     for name in CONFIG_ORDER:
         print(f"bench: {name}", file=sys.stderr, flush=True)
         entries.append(run_config(name, args))
+        # the full entry on its own line; the last line carries the summary
+        print(json.dumps({"bench_config_detail": entries[-1]}), flush=True)
         gc.collect()
         torch.cuda.empty_cache()
-    line = dict(entries[0])
-    line["configs"] = entries
-    print(json.dumps(line), flush=True)
+    line = {k: v for k, v in entries[0].items() if k not in ("extra",)}
+    line["configs"] = [compact_entry(e) for e in entries]
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+
+
+def compact_entry(e):
+    """The figures of one config that the summary line keeps (a few hundred
+    bytes each, so the last line of a full run stays near 4 KB)."""
+    r = e["roofline"]
+    out = {
+        "workload": e["config"]["workload"],
+        "value": e["value"],
+        "ms_per_step": e["ms_per_step"],
+        "kernel": r["kernel"],
+        "kernel_ms": r["kernel_ms"],
+        "frac": r["frac"],
+        "traffic": r["traffic"],
+    }
+    x = e.get("extra", {})
+    if "ms_with_transpose" in x:
+        out["ms_with_transpose"] = x["ms_with_transpose"]
+    if "one_shot" in x:
+        out["one_shot_ms"] = x["one_shot"]["ms_per_call"]
+        out["one_shot_kernel_ms"] = x["one_shot"]["kernel_ms"]
+    if "cpu_baseline" in e:
+        out["cpu_GBps"] = e["cpu_baseline"]["value"]
+        out["cpu_torch_GBps"] = e["cpu_baseline"]["torch_sparse_mm"]["value"]
+    if "accuracy" in e:
+        out["max_rel_err"] = e["accuracy"]["max_rel_err"]
+        out["acc_pass"] = e["accuracy"]["pass"]
+    return out
 
 
 if __name__ == "__main__":

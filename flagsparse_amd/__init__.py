@@ -16,6 +16,12 @@ from ._common import (
     _INDEX_LIMIT_INT32,
     _tolerance_for_dtype,
 )
+from .benchmarks import (
+    benchmark_spmm_case,
+    benchmark_spmm_opt_alg2_case,
+    benchmark_spmm_opt_case,
+    benchmark_spmv_case,
+)
 from .coo import coo_to_csr_for_spmv, flagsparse_spmv_coo_tocsr, prepare_spmv_coo_tocsr
 from .spmm_opt import (
     PreparedCsrSpmmOpt,
@@ -64,6 +70,10 @@ from .alpha_spmm import (
 )
 
 __all__ = [
+    "benchmark_spmv_case",
+    "benchmark_spmm_case",
+    "benchmark_spmm_opt_case",
+    "benchmark_spmm_opt_alg2_case",
     "SUPPORTED_VALUE_DTYPES",
     "SUPPORTED_INDEX_DTYPES",
     "flagsparse_spmv_csr",

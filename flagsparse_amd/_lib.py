@@ -39,6 +39,7 @@ KERNEL_NAMES = {
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTED_SYMBOLS = (
     "fs_last_error",
+    "fs_last_kernel",
     "fs_version",
     "fs_csr_check_bytes",
     "fs_csr_check",
@@ -71,7 +72,6 @@ EXPORTED_SYMBOLS = (
     "fs_sell_max_offset",
     "fs_csr_to_sell",
     "fs_spmv_sell",
-    "fs_diag_gather_rows",
 )
 
 
@@ -186,8 +186,8 @@ def _declare(lib):
     lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_sell.restype = _i32
     lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
-    lib.fs_diag_gather_rows.restype = _i32
-    lib.fs_diag_gather_rows.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _vp]
+    lib.fs_last_kernel.restype = ctypes.c_char_p
+    lib.fs_last_kernel.argtypes = []
 
 
 def load_library(path=None):
@@ -210,6 +210,35 @@ def load_library(path=None):
 
 def lib():
     return load_library()
+
+
+DIAG_LIB_PATH = os.path.join(_HERE, "libflagsparse_diag.so")
+_diag = None
+
+
+def diag_lib():
+    """The measurement-only library (libflagsparse_diag.so, declared in
+    flagsparse_amd/csrc/flagsparse_diag.h): bench.py's gather-floor
+    diagnostic.  Not part of the operator path or its C ABI."""
+    global _diag
+    if _diag is None:
+        if not os.path.exists(DIAG_LIB_PATH):
+            raise HipLibraryError(f"libflagsparse_diag.so not found at {DIAG_LIB_PATH}; build with "
+                                  "`python -m flagsparse_amd.csrc.build`")
+        d = ctypes.CDLL(DIAG_LIB_PATH, mode=ctypes.RTLD_LOCAL)
+        d.fs_last_error.restype = ctypes.c_char_p
+        d.fs_last_error.argtypes = []
+        d.fs_diag_gather_rows.restype = ctypes.c_int32
+        d.fs_diag_gather_rows.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+        _diag = d
+    return _diag
+
+
+def last_kernel():
+    """Name of the main kernel the calling thread's latest SpMV / SpMM launch
+    ran, as the C side recorded it at the launch (fs_last_kernel)."""
+    return lib().fs_last_kernel().decode()
 
 
 def check(rc, what):

@@ -9,7 +9,10 @@ namespace fs {
 
 namespace {
 thread_local std::string g_last_error;
+thread_local const char* g_last_kernel = "";
 }
+
+void note_kernel(const char* name) { g_last_kernel = name; }
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -31,5 +34,7 @@ bool valid_types(int val_t, int idx_t, int ptr_t) {
 }  // namespace fs
 
 extern "C" const char* fs_last_error(void) { return fs::g_last_error.c_str(); }
+
+extern "C" const char* fs_last_kernel(void) { return fs::g_last_kernel; }
 
 extern "C" const char* fs_version(void) { return "flagsparse_hip 0.1.0 (gfx950)"; }

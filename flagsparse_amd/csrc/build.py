@@ -22,7 +22,11 @@ REPO = os.path.dirname(PKG)
 OUT = os.path.join(PKG, "libflagsparse_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["abi.cpp", "spmv.hip", "spmv_opt.hip", "spmm.hip", "spmm_group.hip", "transpose.hip", "sell.hip", "diag.hip"]
+SOURCES = ["abi.cpp", "spmv.hip", "spmv_opt.hip", "spmm.hip", "spmm_group.hip", "transpose.hip", "sell.hip"]
+# the measurement-only library (bench.py --gather-floor), with its own copy of
+# the error reporting
+DIAG_OUT = os.path.join(PKG, "libflagsparse_diag.so")
+DIAG_SOURCES = ["abi.cpp", "diag.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -56,23 +60,29 @@ def _compile(src, extra):
     return obj, res.stderr
 
 
-def build(verbose=False, extra_flags=None):
-    """Compile every HIP source for gfx950 and link the shared library."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    extra = list(extra_flags or [])
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
-        results = list(ex.map(lambda s: _compile(s, extra), SOURCES))
-    objs = [r[0] for r in results]
-    if verbose:
-        for _, err in results:
-            if err.strip():
-                print(err, file=sys.stderr)
-    tmp = OUT + ".tmp"
+def _link(objs, out):
+    tmp = out + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
+
+
+def build(verbose=False, extra_flags=None):
+    """Compile every HIP source for gfx950 and link the shared libraries
+    (the operator library and the measurement-only diagnostic library)."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    extra = list(extra_flags or [])
+    srcs = list(dict.fromkeys(SOURCES + DIAG_SOURCES))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        results = dict(zip(srcs, ex.map(lambda s: _compile(s, extra), srcs)))
+    if verbose:
+        for _, err in results.values():
+            if err.strip():
+                print(err, file=sys.stderr)
+    _link([results[s][0] for s in SOURCES], OUT)
+    _link([results[s][0] for s in DIAG_SOURCES], DIAG_OUT)
     return OUT
 
 

@@ -8,6 +8,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stdint.h>
 
 #include <algorithm>
@@ -199,21 +201,26 @@ __device__ inline int shfl(int v, int src) { return __builtin_amdgcn_ds_bpermute
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_hip(hipError_t e, const char* what);
+// Records the main kernel of the calling thread's latest hot-path launch
+// (see fs_last_kernel()).
+void note_kernel(const char* name);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // LDS bytes per CU of the current device (cached per device id).
+// (The caches below are relaxed atomics: concurrent host threads may each
+// query the device once and store the same value.)
 inline size_t lds_per_cu() {
-  static size_t cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 163840;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || n <= 0)
-      n = 163840;
-    cached[dev] = (size_t)n;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || v <= 0)
+      v = 163840;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return (size_t)v;
 }
 
 // Dynamic LDS bytes that leave room for at most `wg_per_cu` workgroups per
@@ -240,4 +247,13 @@ bool valid_types(int val_t, int idx_t, int ptr_t);
   do {                                                      \
     int _rc = ::fs::check_hip(hipGetLastError(), name);     \
     if (_rc != FS_OK) return _rc;                           \
+  } while (0)
+
+// FS_CHECK_LAUNCH for the main kernel of an entry point: also records its
+// name for fs_last_kernel().
+#define FS_CHECK_MAIN_LAUNCH(name)                          \
+  do {                                                      \
+    int _rc = ::fs::check_hip(hipGetLastError(), name);     \
+    if (_rc != FS_OK) return _rc;                           \
+    ::fs::note_kernel(name);                                \
   } while (0)

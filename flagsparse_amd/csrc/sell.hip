@@ -393,7 +393,7 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
         else go(gc, std::integral_constant<int, 8>{});
       };
       by_up(std::integral_constant<int, 2>{});
-      FS_CHECK_LAUNCH("spmv_sell_group_kernel");
+      FS_CHECK_MAIN_LAUNCH("spmv_sell_group_kernel");
       return FS_OK;
     }
   }
@@ -409,7 +409,7 @@ int spmv_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
   if (u <= 4) go(std::integral_constant<int, 4>{});
   else if (u <= 8) go(std::integral_constant<int, 8>{});
   else go(std::integral_constant<int, 16>{});
-  FS_CHECK_LAUNCH("spmv_sell_kernel");
+  FS_CHECK_MAIN_LAUNCH("spmv_sell_kernel");
   return FS_OK;
 }
 

@@ -367,7 +367,7 @@ int launch_spmm_vec(const fs_csr_plan* plan, const void* vals, const void* cols,
   else if (i64) go(T1{}, F1{});
   else if (p64) go(F1{}, T1{});
   else go(F1{}, F1{});
-  FS_CHECK_LAUNCH("spmm_merge_kernel");
+  FS_CHECK_MAIN_LAUNCH("spmm_merge_kernel");
   const int64_t fix_cols = ceil_div(n_dense, 64) < 64 ? ceil_div(n_dense, 64) : 64;
   hipLaunchKernelGGL((spmm_fixup_kernel<V>), dim3((unsigned)blocks, (unsigned)fix_cols), dim3(256), 0, stream,
                      indptr, plan->ptr_t == FS_I64 ? 1 : 0, part, head, tail, static_cast<V*>(C), ldc, n_dense,

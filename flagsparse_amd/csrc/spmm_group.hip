@@ -400,7 +400,7 @@ int launch_spmm_group(const fs_csr_plan* plan, const void* vals, const void* col
   };
   if (plan->idx_t == FS_I64) go(std::true_type{});
   else go(std::false_type{});
-  FS_CHECK_LAUNCH("spmm_group_kernel");
+  FS_CHECK_MAIN_LAUNCH("spmm_group_kernel");
   const int64_t fix_blocks = ceil_div(n_sub, 4);
   const int64_t fix_cols = ceil_div(n_dense, 64) < 64 ? ceil_div(n_dense, 64) : 64;
   hipLaunchKernelGGL((spmm_group_fixup_kernel<V>), dim3((unsigned)fix_blocks, (unsigned)fix_cols), dim3(256), 0,

@@ -1268,17 +1268,18 @@ inline int resident_per_cu(F kern, size_t lds) {
   return n;
 }
 
-// Compute units of the current device (cached per device id).
+// Compute units of the current device (cached per device id; relaxed
+// atomics, so concurrent host threads at most query the device twice).
 inline int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 template <class V, class I, class P>
@@ -1309,7 +1310,7 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
       case 64: hipLaunchKernelGGL((spmv_vector_kernel<64, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
       default: return fail(FS_E_INVALID, "fs_spmv_csr: vec_width must be a power of two in [2, 64]");
     }
-    FS_CHECK_LAUNCH("spmv_vector_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_vector_kernel");
     return FS_OK;
   }
   if (plan->kernel == FS_KERNEL_STREAM) {
@@ -1349,7 +1350,7 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
         if (dl) launch(S8{}, std::true_type{});
         else launch(S8{}, std::false_type{});
       }
-      FS_CHECK_LAUNCH("spmv_stream_t_kernel");
+      FS_CHECK_MAIN_LAUNCH("spmv_stream_t_kernel");
       return FS_OK;
     }
     const int64_t blocks = ceil_div(n_rows, (int64_t)rpb);
@@ -1361,7 +1362,7 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
       case 4: hipLaunchKernelGGL((spmv_stream_kernel<4, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
       default: hipLaunchKernelGGL((spmv_stream_kernel<8, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, n_rows, blocks, remap); break;
     }
-    FS_CHECK_LAUNCH("spmv_stream_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_stream_kernel");
     return FS_OK;
   }
   if (plan->kernel == FS_KERNEL_NNZBLOCK) {
@@ -1386,7 +1387,7 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
       case 32: hipLaunchKernelGGL((spmv_nnzblock_kernel<32, V, I, P>), g, dim3(256), 0, stream, v, c, p, xv, yv, pt, head, tail, n_rows, plan->nnz); break;
       default: return fail(FS_E_INVALID, "fs_spmv_csr: entry-block threads per row must be a power of two in [1, 32]");
     }
-    FS_CHECK_LAUNCH("spmv_nnzblock_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_nnzblock_kernel");
     hipLaunchKernelGGL((nnz_fixup_kernel<V, P>), dim3((unsigned)ceil_div(n_blocks, 256)), dim3(256), 0, stream, p, pt,
                        head, tail, yv, n_blocks, (int64_t)C);
     FS_CHECK_LAUNCH("nnz_fixup_kernel");
@@ -1408,11 +1409,11 @@ int launch_spmv(const fs_csr_plan* plan, const void* vals, const void* cols, con
     const int64_t wgs = std::min<int64_t>(blocks, (int64_t)device_cus() * std::max(per_cu, 1));
     hipLaunchKernelGGL((spmv_merge_pipe_kernel<V, I, P>), dim3((unsigned)wgs), dim3(256), 0, stream, v, c, p, xv, yv,
                        static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
-    FS_CHECK_LAUNCH("spmv_merge_pipe_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_merge_pipe_kernel");
   } else {
     hipLaunchKernelGGL((spmv_merge_kernel<V, I, P>), dim3((unsigned)blocks), dim3(256), 0, stream, v, c, p,
                        xv, yv, static_cast<const int64_t*>(part), head, tail, n_rows, plan->nnz, n_tiles);
-    FS_CHECK_LAUNCH("spmv_merge_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_merge_kernel");
   }
   hipLaunchKernelGGL((merge_fixup_kernel<V, P>), dim3((unsigned)ceil_div(n_tiles, 256)), dim3(256), 0,
                      stream, p, static_cast<const int64_t*>(part), head, tail, yv, n_tiles,
@@ -1500,13 +1501,13 @@ int launch_spmv_panels(const fs_csr_plan* plan, int n_panels, const int64_t* pan
     };
     const int rc = launch(spmv_panel_pipe_kernel<V, I, P>);
     if (rc != FS_OK) return rc;
-    FS_CHECK_LAUNCH("spmv_panel_pipe_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_panel_pipe_kernel");
   } else {
     hipLaunchKernelGGL((spmv_panel_merge_kernel<V, I, P>), dim3((unsigned)(per_xcd * kXcds)), dim3(256), lds_pad,
                        stream, static_cast<const V*>(vals), static_cast<const I*>(cols), p, static_cast<const V*>(x),
                        partial, static_cast<const int64_t*>(part), head, tail, tab, n_panels, plan->n_rows,
                        plan->nnz, n_tiles);
-    FS_CHECK_LAUNCH("spmv_panel_merge_kernel");
+    FS_CHECK_MAIN_LAUNCH("spmv_panel_merge_kernel");
   }
   hipLaunchKernelGGL((merge_fixup_kernel<V, P, A>), dim3((unsigned)ceil_div(n_tiles, 256)), dim3(256), 0, stream, p,
                      static_cast<const int64_t*>(part), head, tail, partial, n_tiles, (int64_t)kMergeTile);
@@ -1830,31 +1831,43 @@ extern "C" int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void
 // its own copy of the array until the process ends; its address on a device
 // comes from hipGetSymbolAddress on the first call there, with that device
 // current, and is kept per device.  The kernels write every fragment the
-// fix-up reads, so nothing needs clearing between calls.  Calls that
-// overlap on one GPU (other streams, other host threads) share the array
-// and race.
+// fix-up reads, so nothing needs clearing between calls.  Calls on one GPU
+// from several streams or host threads are ordered on the GPU: each call
+// that uses the array records an event on its stream, and a call on another
+// stream waits for the previous call's event before its kernels run.  (Under
+// stream capture the wait and the record are skipped, and a caller that
+// replays captured calls on several streams at once must order them itself.)
 // ---------------------------------------------------------------------------
 constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;       // recorded after the latest call's kernels
+  hipStream_t last = nullptr;      // the stream of that call
+  bool used = false;
+};
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
+ScratchSlot g_scratch[kMaxDevices];
 }  // namespace
 
-static int scratch_for_current_device(void** out) {
+// Set-up on the first call on a device (with it current): the array's device
+// address and the ordering event.  Called with g_scratch_mu held.
+static int scratch_for_current_device(ScratchSlot** out) {
   int dev = 0;
   FS_CHECK_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= kMaxDevices) return fail(FS_E_INVALID, "fs_spmv_csr_noalloc: device id out of range");
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[dev] == nullptr) {
+  ScratchSlot& s = g_scratch[dev];
+  if (s.ptr == nullptr) {
     void* ptr = nullptr;
     FS_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
     if (ptr == nullptr) return fail(FS_E_HIP, "fs_spmv_csr_noalloc: no device address for the scratch array");
-    g_scratch_ptr[dev] = ptr;
+    FS_CHECK_HIP(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+    s.ptr = ptr;
   }
-  *out = g_scratch_ptr[dev];
+  *out = &s;
   return FS_OK;
 }
 
@@ -1872,12 +1885,23 @@ extern "C" int fs_spmv_csr_noalloc(const fs_csr_plan* plan, const void* vals, co
     return fail(FS_E_WORKSPACE, "fs_spmv_csr_noalloc: the matrix needs " + std::to_string(need) +
                                     " bytes of carry scratch, more than the " + std::to_string(kNoAllocScratchBytes) +
                                     " bytes this entry point holds; call fs_spmv_csr with a workspace");
-  void* carry = nullptr;
-  if (uses_carry) {
-    const int rc = scratch_for_current_device(&carry);
-    if (rc != FS_OK) return rc;
+  if (!uses_carry) return fs_spmv_csr(plan, vals, cols, indptr, x, y, part_dev, nullptr, 0, stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot* slot = nullptr;
+  int rc = scratch_for_current_device(&slot);
+  if (rc != FS_OK) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  FS_CHECK_HIP(hipStreamIsCapturing(stream, &cap));
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order && slot->used && slot->last != stream) FS_CHECK_HIP(hipStreamWaitEvent(stream, slot->done, 0));
+  rc = fs_spmv_csr(plan, vals, cols, indptr, x, y, part_dev, slot->ptr, kNoAllocScratchBytes, stream);
+  if (rc != FS_OK) return rc;
+  if (order) {
+    FS_CHECK_HIP(hipEventRecord(slot->done, stream));
+    slot->last = stream;
+    slot->used = true;
   }
-  return fs_spmv_csr(plan, vals, cols, indptr, x, y, part_dev, carry, uses_carry ? kNoAllocScratchBytes : 0, stream);
+  return FS_OK;
 }
 
 extern "C" size_t fs_spmv_panels_workspace_bytes(const fs_csr_plan* plan, int n_panels) {

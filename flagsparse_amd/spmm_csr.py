@@ -278,23 +278,6 @@ class _SpmmPlan:
             self.csr.plan.spmm_wg_cap = _SPMM_SKEW_WG_CAP
 
 
-def _spmm_kernel_name(plan, value_dtype, n_dense, row_major=True):
-    """Name of the kernel fs_spmm_csr launches for this plan and width (for
-    reports): the merge-path kernel for B rows of at least 512 bytes on
-    skewed columns (plan.spmm_wg_cap set), else the lane-group kernel."""
-    import os
-
-    forced = os.environ.get("FLAGSPARSE_SPMM_KERNEL")
-    esz = torch.empty(0, dtype=_compute_dtype(value_dtype)).element_size()
-    if forced == "merge":
-        merge = True
-    elif forced == "group":
-        merge = False
-    else:
-        merge = n_dense * esz >= 512 and int(plan.csr.plan.spmm_wg_cap) > 0
-    return "spmm_merge_kernel" if merge and row_major else "spmm_group_kernel"
-
-
 def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
     """C = A @ B for a dense B of any non-negative strides (row-major,
     column-major or strided views); returns C.

@@ -902,32 +902,6 @@ def _spmv_prepared_with_int32_indices(prepared, reason):
     return out
 
 
-def _spmv_kernel_symbol(prepared):
-    """Name of the kernel function a prepared matrix's SpMV launches (for
-    reports): mirrors the choice in fs_spmv_csr / fs_spmv_sell."""
-    name = prepared.kernel_name
-    if name == "sell":
-        return "spmv_sell_group_kernel" if prepared._sell.layout == _SELL_PAIR else "spmv_sell_kernel"
-    if name == "stream":
-        plan = prepared.hip_plan().plan
-        items = 16384 // (16 if prepared.compute_data().dtype.is_complex else 8)
-        wide = os.environ.get("FLAGSPARSE_SPMV_STREAM_T_WIDE", "1") != "0"
-        rows = 64 if int(plan.max_row) * 64 <= items else (32 if wide and int(plan.max_row) * 32 <= items else 0)
-        t_ok = (os.environ.get("FLAGSPARSE_SPMV_STREAM_T", "1") != "0" and rows > 0
-                and -(-int(plan.n_rows) // rows) * 256 < (1 << 32))
-        return "spmv_stream_t_kernel" if t_ok else "spmv_stream_kernel"
-    if name == "panel":
-        pc = prepared._panels
-        pipe = (8 % pc.n_panels == 0 and int(pc.plan.plan.nnz) > 0
-                and os.environ.get("FLAGSPARSE_PANEL_PIPE", "1") != "0")
-        return "spmv_panel_pipe_kernel" if pipe else "spmv_panel_merge_kernel"
-    if name == "merge":
-        pipe = (int(prepared.hip_plan().plan.nnz) > 0 and os.environ.get("FLAGSPARSE_MERGE_PIPE", "1") != "0")
-        return "spmv_merge_pipe_kernel" if pipe else "spmv_merge_kernel"
-    return {"vector": "spmv_vector_kernel",
-            "nnzblock": "spmv_nnzblock_kernel"}.get(name, name)
-
-
 class _SpmvOptBuckets:
     """Row ids of the use_opt path partitioned into the reference's row-length
     tiers (spmv_csr.py:136-161, 353-410), on the device, with the tier sizes

@@ -82,6 +82,14 @@ typedef struct fs_csr_plan {
 /* Last error message of the calling thread ("" if none). */
 const char* fs_last_error(void);
 
+/*
+ * Name of the main kernel (e.g. "spmv_sell_group_kernel") that the calling
+ * thread's latest successful SpMV / SpMM launch ran ("" before any).  For
+ * reports and profiles.  No counterpart in the reference, whose Triton
+ * kernels are named by the Python function that launches them.
+ */
+const char* fs_last_kernel(void);
+
 /* Library version string. */
 const char* fs_version(void);
 
@@ -172,8 +180,12 @@ int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
  * device array of fs_spmv_noalloc_scratch_bytes() bytes (16 MiB) per GPU,
  * held until the process ends; matrices whose plan needs more
  * (plan->carry_bytes) are rejected with FS_E_WORKSPACE.  The entry point
- * calls no allocator.  All calls on one GPU share the array: calls that
- * overlap in time on that GPU (other streams or host threads) race.
+ * calls no allocator.  All calls on one GPU share the array; calls from
+ * several streams or host threads are ordered on the GPU (each call waits
+ * for the previous call's kernels when that call used another stream, by an
+ * event created at the first call on the device).  Under stream capture the
+ * ordering is skipped: replays of captured calls that run at the same time
+ * on one GPU race on the array.
  */
 size_t fs_spmv_noalloc_scratch_bytes(void);
 int fs_spmv_csr_noalloc(const fs_csr_plan* plan, const void* vals, const void* cols,
@@ -368,18 +380,6 @@ int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_row
                  const void* sell_vals, const void* sell_cols,
                  const int32_t* code_table, const int64_t* slice_ptr,
                  const void* indptr, const void* x, void* y, hipStream_t stream);
-
-/* ---- Diagnostic (no counterpart in the reference) -------------------------
- * fs_diag_gather_rows gathers the rows idx[0..n_idx) of a row-major B of
- * n_b_rows rows of row_bytes bytes (a power of two in [4, 1024]; B aligned to
- * min(row_bytes, 16) bytes; every idx value in [0, n_b_rows); rows of 4 or 8
- * bytes are SpMV x entries) with nothing else in flight, and
- * XORs the loaded words into *checksum (one uint32 of device memory).  It
- * measures the gather floor an SpMM with the same column order cannot beat
- * (bench.py --gather-floor).  Does not synchronise `stream`.
- */
-int fs_diag_gather_rows(int idx_t, const void* B, int64_t n_b_rows, int64_t row_bytes,
-                        const void* idx, int64_t n_idx, void* checksum, hipStream_t stream);
 
 #ifdef __cplusplus
 }

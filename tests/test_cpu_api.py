@@ -45,6 +45,7 @@ def test_public_surface():
         "flagsparse_spmm_coo", "PreparedAlphaSpmmAlg1", "prepare_alpha_spmm_alg1", "flagsparse_alpha_spmm_alg1",
         "flagsparse_alpha_spmm_alg1_tle", "flagsparse_alpha_spmm_alg1_tle_opt", "flagsparse_alpha_spmm_alg1_tle_opt2",
         "is_alpha_spmm_alg1_tle_available", "alpha_spmm_alg1_tle_unavailable_reason",
+        "benchmark_spmv_case", "benchmark_spmm_case", "benchmark_spmm_opt_case", "benchmark_spmm_opt_alg2_case",
     }
     assert expected <= set(dir(fs)) and expected <= set(fs.__all__)
 
@@ -59,6 +60,25 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} not exported"
     assert lib.fs_version().decode().startswith("flagsparse_hip")
+    assert lib.fs_last_kernel() == b""
+
+
+def test_diagnostic_lives_in_its_own_library():
+    """The gather-floor probe is measurement tooling: declared in its own
+    header and built into libflagsparse_diag.so, absent from the product
+    library and its header."""
+    if not os.path.exists(_lib.LIB_PATH) or not os.path.exists(_lib.DIAG_LIB_PATH):
+        pytest.skip("libraries not built")
+    assert not hasattr(_lib.load_library(), "fs_diag_gather_rows")
+    text = open(os.path.join(ROOT, "flagsparse_amd", "csrc", "flagsparse_diag.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    declared = set(re.findall(r"\b(fs_[a-z0-9_]+)\s*\(", text))
+    assert declared == {"fs_last_error", "fs_diag_gather_rows"}
+    d = _lib.diag_lib()
+    for name in declared:
+        assert hasattr(d, name)
+    assert d.fs_diag_gather_rows(0, None, 1, 12, None, 1, None, None) == -1
+    assert b"row_bytes" in d.fs_last_error()
 
 
 def test_abi_rejects_bad_arguments_without_touching_the_gpu():

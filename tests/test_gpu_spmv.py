@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import flagsparse_amd as fs
+from flagsparse_amd import _lib
 from flagsparse_amd import spmv_csr as spmv_mod
 from flagsparse_amd import synthetic as S
 from oracle import csr_oracle as O
@@ -823,15 +824,15 @@ def test_panel_pipelined_walk_matches_one_tile_per_wave(device, monkeypatch, n_p
     x = S.vector(sh[1], dtype, device, seed=5)
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
     assert prep.kernel_name == "panel"
-    assert spmv_mod._spmv_kernel_symbol(prep) == "spmv_panel_pipe_kernel"
     monkeypatch.setenv("FLAGSPARSE_PANEL_WG_CAP", "1")
     y_pipe = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert _lib.last_kernel() == "spmv_panel_pipe_kernel"
     assert torch.equal(y_pipe, fs.flagsparse_spmv_csr(x=x, prepared=prep))
     monkeypatch.delenv("FLAGSPARSE_PANEL_WG_CAP")
     assert torch.equal(y_pipe, fs.flagsparse_spmv_csr(x=x, prepared=prep))
     monkeypatch.setenv("FLAGSPARSE_PANEL_PIPE", "0")
-    assert spmv_mod._spmv_kernel_symbol(prep) == "spmv_panel_merge_kernel"
     y_tile = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    assert _lib.last_kernel() == "spmv_panel_merge_kernel"
     assert torch.equal(y_pipe, y_tile)
     gen = np.random.default_rng(2)
     rows = sorted(set(gen.integers(0, sh[0], 2000).tolist()) | {0, sh[0] - 1})
@@ -877,11 +878,32 @@ def test_stream_t_eight_lanes_per_row(device, monkeypatch, per_row, dtype, index
     data, indices, indptr, sh = S.uniform_rows(3001, 2500, per_row, dtype, index_dtype, device, seed=per_row)
     x = S.vector(sh[1], dtype, device, seed=6)
     prep = fs.prepare_spmv_csr(data, indices, indptr, sh)
-    if per_row * 32 <= (1024 if dtype.is_complex else 2048):
-        assert spmv_mod._spmv_kernel_symbol(prep) == "spmv_stream_t_kernel"
     y = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    if per_row * 32 <= (1024 if dtype.is_complex else 2048):
+        assert _lib.last_kernel() == "spmv_stream_t_kernel"
     ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
     assert rel_err(np_(y), ref) <= REL_TOL[dtype]
     monkeypatch.setenv("FLAGSPARSE_SPMV_STREAM_T_WIDE", "0")
     y3 = fs.flagsparse_spmv_csr(x=x, prepared=prep)
     assert rel_err(np_(y3), ref) <= REL_TOL[dtype]
+
+
+@pytest.mark.parametrize("forced,expect", [
+    ("vector", "spmv_vector_kernel"), ("merge", "spmv_merge_pipe_kernel"), ("stream", "spmv_stream_t_kernel"),
+    ("nnzblock", "spmv_nnzblock_kernel"),
+])
+def test_last_kernel_names_the_launched_kernel(device, monkeypatch, forced, expect):
+    """fs_last_kernel reports the kernel the launch itself chose (recorded
+    at the launch in C, so the name cannot drift from the dispatch)."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", forced)
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "0")
+    data, indices, indptr, sh = S.uniform_rows(2000, 2000, 8, torch.float32, torch.int32, device, seed=3)
+    x = S.vector(sh[1], torch.float32, device, seed=4)
+    fs.flagsparse_spmv_csr(data, indices, indptr, x, sh)
+    assert _lib.last_kernel() == expect
+    monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL")
+    monkeypatch.delenv("FLAGSPARSE_SPMV_SELL")
+    d2, i2, p2, sh2 = S.stencil27(64, torch.float64, torch.int32, device, seed=7)
+    prep = fs.prepare_spmv_csr(d2, i2, p2, sh2)
+    fs.flagsparse_spmv_csr(x=S.vector(sh2[1], torch.float64, device, seed=8), prepared=prep)
+    assert _lib.last_kernel() == "spmv_sell_group_kernel"
