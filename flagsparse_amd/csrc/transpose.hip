@@ -48,11 +48,13 @@ __device__ inline void wave_sync_t() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Lanes (among `active`) whose digit equals this lane's digit.
-__device__ inline uint64_t peer_mask(unsigned digit, uint64_t active) {
+// Lanes (among `active`) whose digit equals this lane's digit; `mask` has
+// the pass's digit bits (a uniform value: bits above it are skipped).
+__device__ inline uint64_t peer_mask(unsigned digit, uint64_t active, unsigned mask) {
   uint64_t peers = active;
 #pragma unroll
   for (int b = 0; b < kRadixBits; ++b) {
+    if (!((mask >> b) & 1u)) break;
     const bool bit = (digit >> b) & 1u;
     const uint64_t m = __ballot(bit);
     peers &= bit ? m : ~m;
@@ -81,130 +83,6 @@ __device__ inline void load_tile_keys(const void* keys, int kind, int64_t base, 
   }
 }
 
-template <class K>
-__global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict__ keys, int kind, int64_t n,
-                                                          int shift, int64_t n_sub,
-                                                          int64_t* __restrict__ counts) {
-  __shared__ unsigned s_hist[kWavesPerBlock][kDigits];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int64_t sub = (int64_t)blockIdx.x * kWavesPerBlock + w;
-  if (sub >= n_sub) return;  // wave-local work only
-  unsigned* hist = s_hist[w];
-  for (int d = lane; d < kDigits; d += 64) hist[d] = 0;
-  const int64_t base = sub * kSub;
-  K key[kChunks];
-  load_tile_keys<K>(keys, kind, base, n, lane, key);
-  wave_sync_t();
-  // Counts only (no ranks): one LDS integer atomic per entry.  Integer sums do
-  // not depend on order, so the counts are deterministic; the stable ranks
-  // come from the scatter pass.  (Ballot peer groups here measured 98 us per
-  // pass on 33.5 M keys.)
-#pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch) {
-    if (base + (int64_t)ch * 64 + lane < n) atomicAdd(&hist[(unsigned)(key[ch] >> shift) & (kDigits - 1)], 1u);
-  }
-  wave_sync_t();
-  for (int d = lane; d < kDigits; d += 64) counts[(int64_t)d * n_sub + sub] = hist[d];
-}
-
-// Exclusive scan of 256 per-digit counts held 4 per lane (digits 4l..4l+3);
-// writes the starts to out[256].
-__device__ inline void wave_digit_scan(const unsigned (&c)[4], int lane, unsigned* out) {
-  const unsigned lane_sum = c[0] + c[1] + c[2] + c[3];
-  unsigned incl = lane_sum;
-  for (int off = 1; off < 64; off <<= 1) {
-    const unsigned y = (unsigned)__builtin_amdgcn_ds_bpermute((lane - off) << 2, (int)incl);
-    if (lane >= off) incl += y;
-  }
-  unsigned run = incl - lane_sum;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    out[4 * lane + k] = run;
-    run += c[k];
-  }
-}
-
-// Stable scatter of one pass.  One wave per sub-tile (kSub entries):
-//  1. keys / positions into registers (all loads in flight);
-//  2. the tile's digit counts (ballot peer masks) and their exclusive scan;
-//  3. every entry to its digit-sorted slot of an LDS copy of the tile, in
-//     input order within a digit (rank = lanes of the same digit below it,
-//     plus the digit's cursor), which keeps the sort stable;
-//  4. the LDS copy written out in order: entry i of digit d goes to
-//     offsets[d][sub] + (i - start[d]), so a digit's entries leave as one
-//     contiguous run instead of single scattered stores.
-template <class K, class Pos>
-__global__ __launch_bounds__(64) void radix_scatter_kernel(const void* __restrict__ keys_in, int kind,
-                                                           const Pos* __restrict__ pos_in, int64_t n, int shift,
-                                                           int64_t n_sub, const int64_t* __restrict__ offsets,
-                                                           K* __restrict__ keys_out, Pos* __restrict__ pos_out) {
-  __shared__ K s_key[kSub];
-  __shared__ Pos s_pos[kSub];
-  __shared__ unsigned s_start[kDigits];
-  __shared__ unsigned s_cur[kDigits];
-  __shared__ int64_t s_glob[kDigits];
-  const int lane = threadIdx.x;
-  const int64_t sub = blockIdx.x;
-  if (sub >= n_sub) return;
-  const int64_t base = sub * kSub;
-  const int cnt = n - base < kSub ? (int)(n - base) : (int)kSub;
-  K key[kChunks];
-  Pos pos[kChunks];
-  load_tile_keys<K>(keys_in, kind, base, n, lane, key);
-#pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch) {
-    const int64_t e = base + (int64_t)ch * 64 + lane;
-    pos[ch] = e < n ? (pos_in ? pos_in[e] : (Pos)e) : (Pos)0;
-  }
-  for (int d = lane; d < kDigits; d += 64) {
-    s_cur[d] = 0;
-    s_glob[d] = offsets[(int64_t)d * n_sub + sub];
-  }
-  wave_sync_t();
-  // 2. per-digit counts of the tile (LDS integer atomics: order independent)
-#pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch)
-    if (ch * 64 + lane < cnt) atomicAdd(&s_cur[(unsigned)(key[ch] >> shift) & (kDigits - 1)], 1u);
-  wave_sync_t();
-  unsigned c4[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) c4[k] = s_cur[4 * lane + k];
-  wave_sync_t();
-  wave_digit_scan(c4, lane, s_start);
-  wave_sync_t();
-#pragma unroll
-  for (int k = 0; k < 4; ++k) s_cur[4 * lane + k] = s_start[4 * lane + k];
-  wave_sync_t();
-  // 3. stable placement into the digit-sorted LDS copy
-#pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch) {
-    const bool valid = ch * 64 + lane < cnt;
-    const uint64_t active = __ballot(valid);
-    if (active == 0) break;
-    const unsigned digit = (unsigned)(key[ch] >> shift) & (kDigits - 1);
-    const uint64_t peers = peer_mask(digit, active);
-    const int rank = count_below_t(peers);
-    if (valid) {
-      const unsigned slot = s_cur[digit] + (unsigned)rank;
-      s_key[slot] = key[ch];
-      s_pos[slot] = pos[ch];
-    }
-    wave_sync_t();
-    if (valid && rank == 0) s_cur[digit] += (unsigned)__popcll(peers);
-    wave_sync_t();
-  }
-  // 4. runs out
-  for (int i = lane; i < cnt; i += 64) {
-    const K k = s_key[i];
-    const unsigned digit = (unsigned)(k >> shift) & (kDigits - 1);
-    const int64_t dst = s_glob[digit] + (int64_t)(i - (int)s_start[digit]);
-    keys_out[dst] = k;
-    pos_out[dst] = s_pos[i];
-  }
-}
-
-// ---- exclusive scan over int64 (reduce -> scan partials -> downsweep) ----
 __device__ inline int64_t block_exclusive_scan(int64_t v, int64_t* s_wave, int64_t& total) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -227,6 +105,315 @@ __device__ inline int64_t block_exclusive_scan(int64_t v, int64_t* s_wave, int64
   return wave_base + x - v;
 }
 
+template <class K, class CT>
+__global__ __launch_bounds__(256) void radix_count_kernel(const void* __restrict__ keys, int kind, int64_t n,
+                                                          int shift, unsigned mask, int64_t n_sub,
+                                                          CT* __restrict__ counts) {
+  __shared__ unsigned s_hist[kWavesPerBlock][kDigits];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t sub = (int64_t)blockIdx.x * kWavesPerBlock + w;
+  if (sub >= n_sub) return;  // wave-local work only
+  unsigned* hist = s_hist[w];
+  for (int d = lane; d < kDigits; d += 64) hist[d] = 0;
+  const int64_t base = sub * kSub;
+  K key[kChunks];
+  load_tile_keys<K>(keys, kind, base, n, lane, key);
+  wave_sync_t();
+  // Counts only (no ranks): one LDS integer atomic per entry.  Integer sums do
+  // not depend on order, so the counts are deterministic; the stable ranks
+  // come from the scatter pass.  (Ballot peer groups here measured 98 us per
+  // pass on 33.5 M keys.)
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    if (base + (int64_t)ch * 64 + lane < n) atomicAdd(&hist[(unsigned)(key[ch] >> shift) & mask], 1u);
+  }
+  wave_sync_t();
+  // sub-tile-major: the wave's 256 counts leave as one contiguous row (the
+  // digit-major layout made them 256 scattered 8-byte stores per wave)
+  for (int d = lane; d < kDigits; d += 64) counts[sub * kDigits + d] = (CT)hist[d];
+}
+
+// ---- exclusive scan of the counts in (digit, sub-tile) order ----
+// The counts are stored sub-tile-major, cnt[sub][digit]; the scatter needs
+// for every (sub, digit) the number of entries with a smaller digit, plus
+// those with the same digit in earlier sub-tiles.  Thread t of a workgroup
+// owns digit t, and a workgroup owns kDigitScanSubs consecutive sub-tiles,
+// so every load and store is a coalesced row: per-block digit sums, one
+// workgroup scanning those in (digit, block) order, then a downsweep.
+constexpr int kDigitScanSubs = 64;
+
+// (loads are issued kScanBatch at a time before they are summed: a plain
+// loop over dependent sums left the one-workgroup top scan at 83 us on 256
+// blocks)
+constexpr int kScanBatch = 16;
+constexpr int kScanTopBatch = 64;  // the one-workgroup top scan: fewer round trips
+
+template <class CT>
+__global__ __launch_bounds__(256) void digit_scan_reduce_kernel(const CT* __restrict__ cnt, int64_t n_sub,
+                                                                CT* __restrict__ partial) {
+  const int t = threadIdx.x;
+  const int64_t s0 = (int64_t)blockIdx.x * kDigitScanSubs;
+  const int64_t s1 = s0 + kDigitScanSubs < n_sub ? s0 + kDigitScanSubs : n_sub;
+  CT sum = 0;
+  for (int64_t s = s0; s < s1; s += kScanBatch) {
+    CT v[kScanBatch];
+#pragma unroll
+    for (int k = 0; k < kScanBatch; ++k) v[k] = s + k < s1 ? cnt[(s + k) * kDigits + t] : (CT)0;
+#pragma unroll
+    for (int k = 0; k < kScanBatch; ++k) sum += v[k];
+  }
+  partial[(int64_t)blockIdx.x * kDigits + t] = sum;
+}
+
+template <class CT>
+__global__ __launch_bounds__(256) void digit_scan_top_kernel(CT* __restrict__ partial, int64_t n_blocks) {
+  __shared__ int64_t s_wave[4];
+  const int t = threadIdx.x;
+  int64_t total = 0;
+  for (int64_t b = 0; b < n_blocks; b += kScanTopBatch) {
+    CT v[kScanTopBatch];
+#pragma unroll
+    for (int k = 0; k < kScanTopBatch; ++k) v[k] = b + k < n_blocks ? partial[(b + k) * kDigits + t] : (CT)0;
+#pragma unroll
+    for (int k = 0; k < kScanTopBatch; ++k) total += (int64_t)v[k];
+  }
+  int64_t all;
+  int64_t run = block_exclusive_scan(total, s_wave, all);
+  for (int64_t b = 0; b < n_blocks; b += kScanTopBatch) {
+    CT v[kScanTopBatch];
+#pragma unroll
+    for (int k = 0; k < kScanTopBatch; ++k) v[k] = b + k < n_blocks ? partial[(b + k) * kDigits + t] : (CT)0;
+#pragma unroll
+    for (int k = 0; k < kScanTopBatch; ++k) {
+      if (b + k < n_blocks) partial[(b + k) * kDigits + t] = (CT)run;
+      run += (int64_t)v[k];
+    }
+  }
+}
+
+template <class CT>
+__global__ __launch_bounds__(256) void digit_scan_down_kernel(CT* __restrict__ cnt, int64_t n_sub,
+                                                              const CT* __restrict__ partial) {
+  const int t = threadIdx.x;
+  const int64_t s0 = (int64_t)blockIdx.x * kDigitScanSubs;
+  const int64_t s1 = s0 + kDigitScanSubs < n_sub ? s0 + kDigitScanSubs : n_sub;
+  CT run = partial[(int64_t)blockIdx.x * kDigits + t];
+  for (int64_t s = s0; s < s1; s += kScanBatch) {
+    CT v[kScanBatch];
+#pragma unroll
+    for (int k = 0; k < kScanBatch; ++k) v[k] = s + k < s1 ? cnt[(s + k) * kDigits + t] : (CT)0;
+#pragma unroll
+    for (int k = 0; k < kScanBatch; ++k) {
+      if (s + k < s1) cnt[(s + k) * kDigits + t] = run;
+      run += v[k];
+    }
+  }
+}
+
+// Exclusive scan of 256 per-digit counts held 4 per lane (digits 4l..4l+3);
+// writes the starts to out[256].
+__device__ inline void wave_digit_scan(const unsigned (&c)[4], int lane, unsigned* out) {
+  const unsigned lane_sum = c[0] + c[1] + c[2] + c[3];
+  unsigned incl = lane_sum;
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned y = (unsigned)__builtin_amdgcn_ds_bpermute((lane - off) << 2, (int)incl);
+    if (lane >= off) incl += y;
+  }
+  unsigned run = incl - lane_sum;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    out[4 * lane + k] = run;
+    run += c[k];
+  }
+}
+
+// Extra inputs / outputs of the transpose's fused first and last passes
+// (4-byte values with row ids below 2^32): the first pass builds each
+// entry's (value, row) word from the CSR arrays itself, the last writes the
+// transposed values and row indices straight from the words.
+struct FusedIO {
+  const uint32_t* vals;     // first pass: the CSR values (4-byte words)
+  const void* rowptr;       // first pass: the CSR row pointer (type P)
+  const int64_t* tile_row;  // first pass: row of each sub-tile's first entry
+  int64_t n_rows;
+  uint32_t* t_vals;         // last pass: transposed values
+  void* t_cols;             // last pass: transposed column indices (type OI)
+};
+
+constexpr int kScatterPlain = 0;  // keys + payload in, keys + payload out
+constexpr int kScatterFirst = 1;  // payload built from values and row ids
+constexpr int kScatterLast = 2;   // payload out as transposed values / rows
+constexpr int kScatterOnly = 3;   // first and last (a single pass)
+
+// Inclusive max-scan over the wave (DPP row shifts within 16-lane rows,
+// then row broadcasts across them; lanes without a source read 0, the
+// identity of an unsigned max).
+template <int CTRL, int ROWMASK>
+__device__ inline unsigned dpp_shift_u(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xF, false);
+}
+__device__ inline unsigned umax_(unsigned a, unsigned b) { return a > b ? a : b; }
+__device__ inline unsigned wave_max_scan(unsigned v) {
+  v = umax_(v, dpp_shift_u<0x111, 0xF>(v));  // row_shr:1
+  v = umax_(v, dpp_shift_u<0x112, 0xF>(v));  // row_shr:2
+  v = umax_(v, dpp_shift_u<0x114, 0xF>(v));  // row_shr:4
+  v = umax_(v, dpp_shift_u<0x118, 0xF>(v));  // row_shr:8
+  v = umax_(v, dpp_shift_u<0x142, 0xA>(v));  // row_bcast:15 -> rows 1, 3
+  v = umax_(v, dpp_shift_u<0x143, 0xC>(v));  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+// Row marks of a sub-tile (kSub entries from `base`, rows r0..r1 touching
+// it): every row that starts inside the tile marks its first entry with
+// r - r0 in s_mark (rows read with unit stride, empty rows mark nothing).
+// The row of entry j is then r0 + the largest mark at or before j.
+template <class P>
+__device__ inline void tile_row_marks(const P* __restrict__ rowptr, int64_t r0, int64_t r1, int64_t base, int cnt,
+                                      unsigned* s_mark, int lane) {
+  for (int j = lane; j < (int)kSub; j += 64) s_mark[j] = 0u;
+  wave_sync_t();
+  for (int64_t r = r0 + 1 + lane; r <= r1; r += 64) {
+    const int64_t st = (int64_t)rowptr[r];
+    if (st - base < cnt && (int64_t)rowptr[r + 1] > st) s_mark[st - base] = (unsigned)(r - r0);
+  }
+  wave_sync_t();
+}
+
+// Stable scatter of one pass.  One wave per sub-tile (kSub entries):
+//  1. keys / payload into registers (all loads in flight);
+//  2. every entry's rank within its digit, chunk by chunk in input order:
+//     the lanes of a chunk holding the same digit find each other with
+//     ballots (peer masks); the lowest of them adds the group's size to the
+//     digit's LDS counter with one returning atomic and hands the old value
+//     to its peers.  A wave's LDS operations complete in issue order, so
+//     chunk c sees every earlier chunk's additions and equal digits keep
+//     their input order (the sort is stable) without a barrier per chunk;
+//  3. the counters, now the tile's digit counts, scanned into digit starts;
+//  4. the keys, then the payload, through one digit-sorted LDS copy of the
+//     tile, written out in order: entry i of digit d goes to
+//     offsets[sub][d] + (i - start[d]), so a digit's entries leave as one
+//     contiguous run instead of single scattered stores.
+// MODE kScatterFirst / kScatterLast / kScatterOnly fuse the transpose's
+// (value, row) packing into the first pass and its unpacking into the last
+// (FusedIO; Pos is then the 8-byte word, value in the low half).
+template <class K, class Pos, class CT, int MODE = kScatterPlain, class P = int32_t, class OI = int32_t>
+__global__ __launch_bounds__(64, 2) void radix_scatter_kernel(const void* __restrict__ keys_in, int kind,
+                                                           const Pos* __restrict__ pos_in, int64_t n, int shift,
+                                                           unsigned mask, int64_t n_sub, const CT* __restrict__ offsets,
+                                                           K* __restrict__ keys_out, Pos* __restrict__ pos_out,
+                                                           FusedIO io) {
+  constexpr bool kFirst = MODE == kScatterFirst || MODE == kScatterOnly;
+  constexpr bool kLast = MODE == kScatterLast || MODE == kScatterOnly;
+  // One LDS buffer stages the keys, then the payload (the tile's footprint
+  // is the larger of the two, not their sum); a byte per slot keeps its
+  // digit, so the write-out loops need no registers per entry; the digit
+  // starts overwrite the counters, and offsets are 32-bit while every one
+  // fits.  20 KB per wave with an 8-byte payload: 8 waves per CU.  The fused
+  // first pass computes the row ids in the buffer before all that.
+  using Off = std::conditional_t<sizeof(CT) == 4, uint32_t, int64_t>;
+  constexpr int kBufWords = (int)((kSub * (sizeof(Pos) > sizeof(K) ? sizeof(Pos) : sizeof(K))) / 8);
+  static_assert(!kFirst || kSub * 4 <= kBufWords * 8, "row marks fit the staging buffer");
+  __shared__ uint64_t s_buf[kBufWords];
+  __shared__ unsigned s_cnt[kDigits];  // digit counts, then digit starts
+  __shared__ Off s_off[kDigits];
+  __shared__ uint8_t s_dig[kSub];
+  K* s_key = reinterpret_cast<K*>(s_buf);
+  Pos* s_pos = reinterpret_cast<Pos*>(s_buf);
+  const int lane = threadIdx.x;
+  const int64_t sub = blockIdx.x;
+  if (sub >= n_sub) return;
+  const int64_t base = sub * kSub;
+  const int cnt = n - base < kSub ? (int)(n - base) : (int)kSub;
+  K key[kChunks];
+  Pos pos[kChunks];
+  load_tile_keys<K>(keys_in, kind, base, n, lane, key);
+  if constexpr (kFirst) {
+    static_assert(sizeof(Pos) == 8, "the fused passes carry 8-byte (value, row) words");
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      const int64_t e = base + (int64_t)ch * 64 + lane;
+      pos[ch] = (Pos)(e < n ? io.vals[e] : 0u);
+    }
+    const int64_t r0 = io.tile_row[sub];
+    const int64_t r1 = sub + 1 < n_sub ? io.tile_row[sub + 1] : io.n_rows - 1;
+    unsigned* s_mark = reinterpret_cast<unsigned*>(s_buf);
+    tile_row_marks<P>(static_cast<const P*>(io.rowptr), r0, r1, base, cnt, s_mark, lane);
+    // rows chunk by chunk: a wave max-scan of the marks, carried across chunks
+    unsigned carry = 0u;
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      const unsigned m = umax_(wave_max_scan(s_mark[ch * 64 + lane]), carry);
+      carry = (unsigned)__builtin_amdgcn_readlane((int)m, 63);
+      pos[ch] |= (Pos)((uint64_t)(r0 + (int64_t)m) << 32);
+    }
+    wave_sync_t();
+  } else {
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      const int64_t e = base + (int64_t)ch * 64 + lane;
+      pos[ch] = e < n ? (pos_in ? pos_in[e] : (Pos)e) : (Pos)0;
+    }
+  }
+  for (int d = lane; d < kDigits; d += 64) s_cnt[d] = 0;
+  wave_sync_t();
+  // 2. ranks within the digit, in input order
+  unsigned local[kChunks];
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const bool valid = ch * 64 + lane < cnt;
+    const uint64_t active = __ballot(valid);
+    const unsigned digit = (unsigned)(key[ch] >> shift) & mask;
+    const uint64_t peers = peer_mask(digit, active, mask);
+    const int rank = count_below_t(peers);
+    unsigned old = 0;
+    if (valid && rank == 0) old = atomicAdd(&s_cnt[digit], (unsigned)__popcll(peers));
+    const int leader = peers ? (int)__builtin_ctzll(peers) : lane;
+    old = (unsigned)__builtin_amdgcn_ds_bpermute(leader << 2, (int)old);
+    local[ch] = old + (unsigned)rank;
+  }
+  wave_sync_t();
+  // 3. digit starts within the tile (over the counts: every lane holds its
+  // four counts in registers before any start is stored), and each digit's
+  // global base minus its start (never negative)
+  unsigned c4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) c4[k] = s_cnt[4 * lane + k];
+  wave_digit_scan(c4, lane, s_cnt);
+  wave_sync_t();
+  for (int d = lane; d < kDigits; d += 64) s_off[d] = (Off)((int64_t)offsets[sub * kDigits + d] - (int64_t)s_cnt[d]);
+  // 4. keys (and digits) to their slots of the digit-sorted LDS copy
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const unsigned digit = (unsigned)(key[ch] >> shift) & mask;
+    local[ch] += s_cnt[digit];
+    if (ch * 64 + lane < cnt) {
+      s_key[local[ch]] = key[ch];
+      s_dig[local[ch]] = (uint8_t)digit;
+    }
+  }
+  wave_sync_t();
+  // keys out as contiguous runs
+  for (int i = lane; i < cnt; i += 64) keys_out[(int64_t)s_off[s_dig[i]] + i] = s_key[i];
+  wave_sync_t();
+  // the payload through the same buffer, out to the same slots
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch)
+    if (ch * 64 + lane < cnt) s_pos[local[ch]] = pos[ch];
+  wave_sync_t();
+  for (int i = lane; i < cnt; i += 64) {
+    const int64_t dst = (int64_t)s_off[s_dig[i]] + i;
+    if constexpr (kLast) {
+      const uint64_t w = (uint64_t)s_pos[i];
+      io.t_vals[dst] = (uint32_t)w;
+      static_cast<OI*>(io.t_cols)[dst] = (OI)(w >> 32);
+    } else {
+      pos_out[dst] = s_pos[i];
+    }
+  }
+}
+
+// ---- exclusive scan over int64 (reduce -> scan partials -> downsweep) ----
 // Tile total: integer sums do not depend on order, so the loads are
 // coalesced (item k * 256 + t of the tile to thread t).
 __global__ __launch_bounds__(256) void scan_reduce_kernel(const int64_t* __restrict__ in, int64_t n,
@@ -558,7 +745,9 @@ Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz, bool payload = f
   L.off_pos_b = o; o = align256(o + slot * nnz);
   L.off_rowid = o; o = align256(o + L.rowid_bytes * nnz);
   L.off_counts = o; o = align256(o + sizeof(int64_t) * L.n_counts);
-  L.off_partials = o; o = align256(o + sizeof(int64_t) * (L.n_partials + 1));
+  // partials: the flat scan's tile totals, or the digit scan's per-block rows
+  const int64_t n_part = std::max<int64_t>(L.n_partials + 1, ceil_div(L.n_sub, kDigitScanSubs) * kDigits);
+  L.off_partials = o; o = align256(o + sizeof(int64_t) * n_part);
   L.total = o;
   L.payload = payload;
   (void)n_rows;
@@ -577,45 +766,77 @@ int device_exclusive_scan(int64_t* data, int64_t n, int64_t* partial, hipStream_
   return FS_OK;
 }
 
+// Exclusive scan of cnt[sub][digit] in (digit, sub) order, in place.
+template <class CT>
+int digit_exclusive_scan(CT* cnt, int64_t n_sub, CT* partial, hipStream_t s) {
+  if (n_sub == 0) return FS_OK;
+  const int64_t blocks = ceil_div(n_sub, kDigitScanSubs);
+  hipLaunchKernelGGL((digit_scan_reduce_kernel<CT>), dim3((unsigned)blocks), dim3(256), 0, s, cnt, n_sub, partial);
+  FS_CHECK_LAUNCH("digit_scan_reduce_kernel");
+  hipLaunchKernelGGL((digit_scan_top_kernel<CT>), dim3(1), dim3(256), 0, s, partial, blocks);
+  FS_CHECK_LAUNCH("digit_scan_top_kernel");
+  hipLaunchKernelGGL((digit_scan_down_kernel<CT>), dim3((unsigned)blocks), dim3(256), 0, s, cnt, n_sub, partial);
+  FS_CHECK_LAUNCH("digit_scan_down_kernel");
+  return FS_OK;
+}
+
 int key_bits(int64_t n_cols) {
   int b = 0;
   while (b < 64 && ((n_cols - 1) >> b) > 0) ++b;  // bits needed for n_cols-1
   return b;
 }
 
-template <class K, class Pos>
-int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, int64_t nnz, int64_t n_cols,
-                    const K** sorted_keys, const Pos** perm, hipStream_t s, const Pos* pos_init = nullptr) {
+// The passes of the LSD sort.  With Fused (the transpose's 8-byte
+// (value, row) payload, FusedIO io) the first pass builds the words from the
+// CSR arrays and the last writes the transposed values and rows; *perm is
+// then null.
+template <class K, class Pos, class CT, bool Fused = false, class P = int32_t, class OI = int32_t>
+int radix_passes(const Layout& L, char* ws, const void* cols, int col_kind, int64_t nnz, int total_bits, int passes,
+                 const K** sorted_keys, const Pos** perm, hipStream_t s, const Pos* pos_init,
+                 FusedIO io = FusedIO{}) {
   K* ka = reinterpret_cast<K*>(ws + L.off_keys_a);
   K* kb = reinterpret_cast<K*>(ws + L.off_keys_b);
   Pos* pa = reinterpret_cast<Pos*>(ws + L.off_pos_a);
   Pos* pb = reinterpret_cast<Pos*>(ws + L.off_pos_b);
-  int64_t* counts = reinterpret_cast<int64_t*>(ws + L.off_counts);
-  int64_t* partial = reinterpret_cast<int64_t*>(ws + L.off_partials);
-  const int passes = (key_bits(n_cols) + kRadixBits - 1) / kRadixBits;
+  CT* counts = reinterpret_cast<CT*>(ws + L.off_counts);
+  CT* partial = reinterpret_cast<CT*>(ws + L.off_partials);
   const unsigned blocks = (unsigned)ceil_div(L.n_sub, kWavesPerBlock);
   const void* kin = cols;
   int kind = col_kind;
   const Pos* pin = pos_init;  // null: positions 0, 1, ... on the first pass
   K* kout = ka;
   Pos* pout = pa;
-  if (passes == 0) {
-    hipLaunchKernelGGL((identity_kernel<K>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s, cols, col_kind,
-                       nnz, ka);
-    FS_CHECK_LAUNCH("identity_kernel");
-    *sorted_keys = ka;
-    *perm = nullptr;
-    return FS_OK;
-  }
+  // The key bits split evenly over the passes (20 bits: 7 + 7 + 6, not
+  // 8 + 8 + 4): fewer digits per pass make each digit's run in a sub-tile's
+  // output longer, and the scattered runs write faster the longer they are.
+  int shift = 0;
   for (int p = 0; p < passes; ++p) {
-    const int shift = p * kRadixBits;
-    hipLaunchKernelGGL((radix_count_kernel<K>), dim3(blocks), dim3(256), 0, s, kin, kind, nnz, shift, L.n_sub,
-                       counts);
+    const int bits = (total_bits - shift + (passes - p) - 1) / (passes - p);
+    const unsigned mask = (1u << bits) - 1u;
+    hipLaunchKernelGGL((radix_count_kernel<K, CT>), dim3(blocks), dim3(256), 0, s, kin, kind, nnz, shift, mask,
+                       L.n_sub, counts);
     FS_CHECK_LAUNCH("radix_count_kernel");
-    int rc = device_exclusive_scan(counts, L.n_counts, partial, s);
+    int rc = digit_exclusive_scan<CT>(counts, L.n_sub, partial, s);
     if (rc != FS_OK) return rc;
-    hipLaunchKernelGGL((radix_scatter_kernel<K, Pos>), dim3((unsigned)L.n_sub), dim3(64), 0, s, kin, kind, pin, nnz,
-                       shift, L.n_sub, counts, kout, pout);
+    const dim3 g((unsigned)L.n_sub);
+    if constexpr (Fused) {
+      if (passes == 1)
+        hipLaunchKernelGGL((radix_scatter_kernel<K, Pos, CT, kScatterOnly, P, OI>), g, dim3(64), 0, s, kin, kind,
+                           pin, nnz, shift, mask, L.n_sub, counts, kout, pout, io);
+      else if (p == 0)
+        hipLaunchKernelGGL((radix_scatter_kernel<K, Pos, CT, kScatterFirst, P, OI>), g, dim3(64), 0, s, kin, kind,
+                           pin, nnz, shift, mask, L.n_sub, counts, kout, pout, io);
+      else if (p == passes - 1)
+        hipLaunchKernelGGL((radix_scatter_kernel<K, Pos, CT, kScatterLast, P, OI>), g, dim3(64), 0, s, kin, kind,
+                           pin, nnz, shift, mask, L.n_sub, counts, kout, pout, io);
+      else
+        hipLaunchKernelGGL((radix_scatter_kernel<K, Pos, CT>), g, dim3(64), 0, s, kin, kind, pin, nnz, shift, mask,
+                           L.n_sub, counts, kout, pout, io);
+    } else {
+      hipLaunchKernelGGL((radix_scatter_kernel<K, Pos, CT>), g, dim3(64), 0, s, kin, kind, pin, nnz, shift, mask,
+                         L.n_sub, counts, kout, pout, io);
+    }
+    shift += bits;
     FS_CHECK_LAUNCH("radix_scatter_kernel");
     kin = kout;
     kind = 2;
@@ -624,8 +845,29 @@ int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, i
     pout = (pout == pa) ? pb : pa;
   }
   *sorted_keys = static_cast<const K*>(kin);
-  *perm = pin;
+  *perm = Fused ? nullptr : pin;
   return FS_OK;
+}
+
+template <class K, class Pos>
+int radix_sort_cols(const Layout& L, char* ws, const void* cols, int col_kind, int64_t nnz, int64_t n_cols,
+                    const K** sorted_keys, const Pos** perm, hipStream_t s, const Pos* pos_init = nullptr) {
+  const int passes = (key_bits(n_cols) + kRadixBits - 1) / kRadixBits;
+  if (passes == 0) {
+    K* ka = reinterpret_cast<K*>(ws + L.off_keys_a);
+    hipLaunchKernelGGL((identity_kernel<K>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s, cols, col_kind,
+                       nnz, ka);
+    FS_CHECK_LAUNCH("identity_kernel");
+    *sorted_keys = ka;
+    *perm = nullptr;
+    return FS_OK;
+  }
+  // 32-bit counts and offsets while every offset fits
+  if (nnz <= (int64_t)0xffffffffLL)
+    return radix_passes<K, Pos, uint32_t>(L, ws, cols, col_kind, nnz, key_bits(n_cols), passes, sorted_keys, perm, s,
+                                          pos_init);
+  return radix_passes<K, Pos, uint64_t>(L, ws, cols, col_kind, nnz, key_bits(n_cols), passes, sorted_keys, perm, s,
+                                        pos_init);
 }
 
 template <class Pos>
@@ -650,6 +892,10 @@ inline bool transpose_payload_enabled() {
   return !(e && std::atoi(e) == 0);
 }
 
+template <class P>
+__global__ __launch_bounds__(256) void tile_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows, int64_t n_sub,
+                                                        int64_t* __restrict__ tile_row);
+
 template <class V, class P, class OI, class OP, class K, class Pos>
 int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
                     const void* vals, const void* cols, const void* indptr, int conj, void* t_vals, void* t_cols,
@@ -657,7 +903,34 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
   const K* keys = nullptr;
   const unsigned expand_blocks = (unsigned)ceil_div(nnz, kExpandTile);
   if constexpr (sizeof(V) == 4) {
+    if (L.payload && n_rows <= (int64_t)0xffffffffLL && key_bits(n_cols) > 0) {
+      // The (value, row) words are built inside the first radix pass and
+      // unpacked by the last: no packing or unpacking pass over the arrays.
+      // The row of each sub-tile's first entry comes from one binary search
+      // per sub-tile, in the slot the packed words used to take.
+      int64_t* tile_row = reinterpret_cast<int64_t*>(ws + L.off_rowid);
+      hipLaunchKernelGGL((tile_rows_kernel<P>), dim3((unsigned)ceil_div(L.n_sub, 256)), dim3(256), 0, s,
+                         static_cast<const P*>(indptr), n_rows, L.n_sub, tile_row);
+      FS_CHECK_LAUNCH("tile_rows_kernel");
+      FusedIO io{static_cast<const uint32_t*>(vals), indptr, tile_row, n_rows, static_cast<uint32_t*>(t_vals), t_cols};
+      const uint64_t* none = nullptr;
+      const int bits = key_bits(n_cols);
+      const int passes = (bits + kRadixBits - 1) / kRadixBits;
+      const int kind = idx_t == FS_I32 ? 0 : 1;
+      int rc = nnz <= (int64_t)0xffffffffLL
+                   ? radix_passes<K, uint64_t, uint32_t, true, P, OI>(L, ws, cols, kind, nnz, bits, passes, &keys,
+                                                                     &none, s, nullptr, io)
+                   : radix_passes<K, uint64_t, uint64_t, true, P, OI>(L, ws, cols, kind, nnz, bits, passes, &keys,
+                                                                     &none, s, nullptr, io);
+      if (rc != FS_OK) return rc;
+      hipLaunchKernelGGL((colptr_kernel<K, OP>), dim3((unsigned)ceil_div(ceil_div(nnz + 1, 16 / (int64_t)sizeof(K)), 256)), dim3(256), 0, s, keys, nnz,
+                         n_cols, static_cast<OP*>(t_indptr));
+      FS_CHECK_LAUNCH("colptr_kernel");
+      (void)conj;  // real 4-byte values: conj is the identity
+      return FS_OK;
+    }
     if (L.payload && n_rows <= (int64_t)0xffffffffLL) {
+      // one column: the order is unchanged
       uint2* packed = reinterpret_cast<uint2*>(ws + L.off_rowid);
       hipLaunchKernelGGL((expand_pack_kernel<P, V, OI>), dim3(expand_blocks), dim3(256), 0, s,
                          static_cast<const P*>(indptr), n_rows, nnz, static_cast<const V*>(vals), packed);
@@ -666,7 +939,7 @@ int transpose_typed(const Layout& L, char* ws, int idx_t, int64_t n_rows, int64_
       int rc = radix_sort_cols<K, uint64_t>(L, ws, cols, idx_t == FS_I32 ? 0 : 1, nnz, n_cols, &keys, &sorted, s,
                                             reinterpret_cast<const uint64_t*>(packed));
       if (rc != FS_OK) return rc;
-      if (sorted == nullptr) sorted = reinterpret_cast<const uint64_t*>(packed);  // one column: order unchanged
+      if (sorted == nullptr) sorted = reinterpret_cast<const uint64_t*>(packed);
       hipLaunchKernelGGL((unpack_kernel<V, OI>), dim3((unsigned)ceil_div(nnz, 256)), dim3(256), 0, s,
                          reinterpret_cast<const uint2*>(sorted), nnz, static_cast<V*>(t_vals),
                          static_cast<OI*>(t_cols));
