@@ -52,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "fs_spmv_csr",
     "fs_spmv_noalloc_scratch_bytes",
     "fs_spmv_csr_noalloc",
+    "fs_spmv_csr_oneshot",
     "fs_spmv_opt_max_buckets",
     "fs_spmv_opt_workspace_bytes",
     "fs_spmv_opt_buckets",
@@ -186,6 +187,8 @@ def _declare(lib):
     lib.fs_csr_to_sell.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_sell.restype = _i32
     lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.fs_spmv_csr_oneshot.restype = _i32
+    lib.fs_spmv_csr_oneshot.argtypes = [_i32, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_last_kernel.restype = ctypes.c_char_p
     lib.fs_last_kernel.argtypes = []
 

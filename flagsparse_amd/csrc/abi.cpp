@@ -23,6 +23,9 @@ int fail(int code, const std::string& msg) {
 
 int check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return FS_OK;
+  // clear the runtime's last-error state too: a failed API call must not be
+  // reported again by the caller's next, unrelated launch check
+  (void)hipGetLastError();
   return fail(FS_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 

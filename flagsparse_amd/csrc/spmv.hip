@@ -551,6 +551,188 @@ __global__ __launch_bounds__(256) void spmv_stream_t_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// One-shot SpMV: the unprepared public call's kernel.  The reference
+// validates the CSR structure with separate device reads before its launch
+// (spmv_csr.py:546-558) and picks its launch from the row lengths
+// (spmv_csr.py:623-647); here one kernel does both jobs while it computes:
+//   - every workgroup reads its 65 row pointers (it needs them anyway) and
+//     flags a start other than 0 (first block), an end other than nnz (last
+//     block) and any decrease; every gathered column outside [0, n_cols)
+//     is flagged and read as column 0, so no access leaves the arrays;
+//   - row pointers are clamped into [0, nnz] before use, so a malformed
+//     matrix is computed on garbage but never read out of bounds; the host
+//     raises the reference's error for any flag and discards y;
+//   - the block's rows go through K3t's LDS stage with 4 lanes per row when
+//     their entries fit it, else as two 32-row halves with 8 lanes per row,
+//     else row by row with the whole workgroup per row (long rows).
+// flags[0..3]: start, end, decrease, column (set to 1; zeroed by the host).
+// ---------------------------------------------------------------------------
+template <int SUBS, class V, class I, bool DL>
+__device__ inline void oneshot_rows(const V* __restrict__ vals, const I* __restrict__ cols,
+                                    const V* __restrict__ x, V* __restrict__ y, int64_t row0, int rows,
+                                    int64_t S, int cnt, const int* s_off, unsigned char* t_lds, int C,
+                                    uint64_t n_cols, bool& bad) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  constexpr int NT = 256;
+  constexpr int RPW = 64 / SUBS;
+  constexpr int CMAX = stream_items<A>();
+  constexpr int K = CMAX / NT;
+  const StreamTLayout L = stream_t_layout(C, sizeof(V), sizeof(I), DL);
+  V* s_val = reinterpret_cast<V*>(t_lds);
+  I* s_col = reinterpret_cast<I*>(t_lds + L.col_off);
+  const int t = threadIdx.x;
+  int ov = 0, oi = 0;
+  if constexpr (DL) {
+    constexpr int EV = 16 / (int)sizeof(V);
+    constexpr int EI = 16 / (int)sizeof(I);
+    const int64_t Sv = S & ~(int64_t)(EV - 1);
+    const int64_t Si = S & ~(int64_t)(EI - 1);
+    ov = (int)(S - Sv);
+    oi = (int)(S - Si);
+    constexpr int KV = (CMAX + 2 * EV + NT * EV - 1) / (NT * EV);
+    constexpr int KI = (CMAX + 2 * EI + NT * EI - 1) / (NT * EI);
+    lds_copy16<NT / 64, KV>(reinterpret_cast<const unsigned char*>(vals + Sv), reinterpret_cast<unsigned char*>(s_val),
+                            (ov + cnt + EV - 1) / EV);
+    lds_copy16<NT / 64, KI>(reinterpret_cast<const unsigned char*>(cols + Si), reinterpret_cast<unsigned char*>(s_col),
+                            (oi + cnt + EI - 1) / EI);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS copies have landed
+  } else {
+    V v[K];
+    I c[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int q = t + NT * k;
+      if (q < cnt) {
+        v[k] = load_stream(vals + S + q);
+        c[k] = __builtin_nontemporal_load(cols + S + q);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int q = t + NT * k;
+      if (q < cnt) {
+        s_col[q] = c[k];
+        s_val[q] = v[k];
+      }
+    }
+  }
+  __syncthreads();
+  const int lane = t & 63;
+  const int r = (t >> 6) * RPW + lane % RPW;
+  const int sub = lane / RPW;
+  A acc0 = T::zero(), acc1 = T::zero(), acc2 = T::zero(), acc3 = T::zero();
+  auto guard = [&](I c) -> I {
+    if ((uint64_t)(int64_t)c >= n_cols) {
+      bad = true;
+      return (I)0;
+    }
+    return c;
+  };
+  if (r < rows) {
+    const int a = s_off[r], b = s_off[r + 1];
+    const I* sc = s_col + oi;
+    const V* sv = s_val + ov;
+    for (int q = a + sub; q < b; q += 4 * SUBS) {
+      const bool h1 = q + SUBS < b, h2 = q + 2 * SUBS < b, h3 = q + 3 * SUBS < b;
+      const I c0 = guard(sc[q]), c1 = h1 ? guard(sc[q + SUBS]) : c0, c2 = h2 ? guard(sc[q + 2 * SUBS]) : c0,
+              c3 = h3 ? guard(sc[q + 3 * SUBS]) : c0;
+      const V x0 = x[c0], x1 = x[c1], x2 = x[c2], x3 = x[c3];
+      acc0 = T::fma(sv[q], x0, acc0);
+      if (h1) acc1 = T::fma(sv[q + SUBS], x1, acc1);
+      if (h2) acc2 = T::fma(sv[q + 2 * SUBS], x2, acc2);
+      if (h3) acc3 = T::fma(sv[q + 3 * SUBS], x3, acc3);
+    }
+  }
+  A acc = add(add(acc0, acc1), add(acc2, acc3));
+#pragma unroll
+  for (int off = RPW; off < 64; off <<= 1) acc = add(acc, shfl(acc, lane ^ off));  // fixed order
+  if (sub == 0 && r < rows) store_stream(y + row0 + r, T::out(acc));
+  __syncthreads();  // the stage is reused by the caller
+}
+
+template <class V, class I, class P, bool DL>
+__global__ __launch_bounds__(256) void spmv_oneshot_kernel(
+    const V* __restrict__ vals, const I* __restrict__ cols, const P* __restrict__ rowptr,
+    const V* __restrict__ x, V* __restrict__ y, int64_t n_rows, int64_t n_cols, int64_t nnz, int64_t n_blocks,
+    int remap, int stage, int32_t* __restrict__ flags) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  constexpr int R = 64;
+  const int C = stage;  // LDS stage in entries (at most stream_items)
+  extern __shared__ __align__(16) unsigned char t_lds[];
+  const StreamTLayout L = stream_t_layout(C, sizeof(V), sizeof(I), DL);
+  // flags live in pinned host memory: system-scope stores reach it directly
+  auto raise = [&](int k) { __hip_atomic_store(flags + k, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
+  int* s_off = reinterpret_cast<int*>(t_lds + L.off_off);
+  __shared__ int64_t s_p[R + 1];
+  __shared__ A s_red[4];
+  const int t = threadIdx.x;
+  const int64_t blk = logical_block(remap, n_blocks);
+  if (blk < 0) return;  // whole workgroup
+  const int64_t rb0 = blk * R;
+  const int rows = n_rows - rb0 < R ? (int)(n_rows - rb0) : R;
+  if (t <= rows) s_p[t] = (int64_t)rowptr[rb0 + t];
+  __syncthreads();
+  if (t < rows && s_p[t + 1] < s_p[t]) raise(2);
+  if (t == 0 && blk == 0 && s_p[0] != 0) raise(0);
+  if (t == 0 && rb0 + rows == n_rows && s_p[rows] != nnz) raise(1);
+  // clamped into [S, E] within [0, nnz]: only the arrays' own entries are read
+  const int64_t S = s_p[0] < 0 ? 0 : (s_p[0] > nnz ? nnz : s_p[0]);
+  const int64_t E = s_p[rows] < S ? S : (s_p[rows] > nnz ? nnz : s_p[rows]);
+  if (t <= rows) {
+    const int64_t v = s_p[t] < S ? S : (s_p[t] > E ? E : s_p[t]);
+    s_off[t] = (int)(v - S);
+  }
+  __syncthreads();
+  const int cnt = (int)(E - S);
+  const uint64_t nc = (uint64_t)n_cols;
+  bool bad = false;
+  if (cnt <= C) {
+    oneshot_rows<4, V, I, DL>(vals, cols, x, y, rb0, rows, S, cnt, s_off, t_lds, C, nc, bad);
+  } else {
+    const int half = rows < 32 ? rows : 32;
+    const int c0 = s_off[half] - s_off[0], c1 = s_off[rows] - s_off[half];
+    if (c0 >= 0 && c0 <= C && c1 >= 0 && c1 <= C) {
+      // two 32-row halves, 8 lanes per row (offsets rebased on each half)
+      for (int h = 0; h < 2; ++h) {
+        const int lo = h * half, nr = h == 0 ? half : rows - half;
+        if (nr <= 0) break;
+        const int base = s_off[lo];
+        __syncthreads();
+        int* s_half = s_off + R + 1;  // 33 rebased offsets past the block's own
+        if (t <= nr) s_half[t] = s_off[lo + t] - base;
+        __syncthreads();
+        oneshot_rows<8, V, I, DL>(vals, cols, x, y, rb0 + lo, nr, S + base, h == 0 ? c0 : c1, s_half, t_lds, C,
+                                  nc, bad);
+      }
+    } else {
+      // long rows: the whole workgroup per row, straight from global memory
+      const int lane = t & 63;
+      for (int r = 0; r < rows; ++r) {
+        const int a = s_off[r], b = s_off[r + 1];
+        A acc = T::zero();
+        for (int q = a + t; q < b; q += 256) {
+          I c = cols[S + q];
+          if ((uint64_t)(int64_t)c >= nc) {
+            bad = true;
+            c = (I)0;
+          }
+          acc = T::fma(vals[S + q], x[c], acc);
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) acc = add(acc, shfl(acc, lane ^ off));  // fixed order
+        if (lane == 0) s_red[t >> 6] = acc;
+        __syncthreads();
+        if (t == 0) y[rb0 + r] = T::out(add(add(s_red[0], s_red[1]), add(s_red[2], s_red[3])));
+        __syncthreads();
+      }
+    }
+  }
+  if (bad) raise(3);
+}
+
+// ---------------------------------------------------------------------------
 // K3b: entry-aligned streaming SpMV.  Block b owns the entry range
 // [b*C, (b+1)*C) (C = the LDS stage), so its value / index loads depend on
 // nothing and go out at once; the rows it owns (those whose last entry, or
@@ -1584,6 +1766,36 @@ void choose_spmv_kernel(fs_csr_plan* plan, int force_kernel) {
   plan->carry_bytes = (size_t)plan->n_tiles * 2 * acc_bytes(plan->val_t);
 }
 
+template <class V, class I, class P>
+int launch_spmv_oneshot(int64_t n_rows, int64_t n_cols, int64_t nnz, const void* vals, const void* cols,
+                        const void* indptr, const void* x, void* y, int32_t* flags, hipStream_t stream) {
+  using A = typename VT<V>::acc;
+  const int64_t blocks = ceil_div(n_rows, (int64_t)64);
+  const int remap = xcd_remap();
+  const int64_t grid = remap ? ceil_div(blocks, kXcds) * kXcds : blocks;
+  if (grid * 256 >= (int64_t(1) << 32)) return fail(FS_E_INVALID, "fs_spmv_csr_oneshot: grid too large");
+  const V* v = static_cast<const V*>(vals);
+  const I* c = static_cast<const I*>(cols);
+  const bool dl = stream_t_dl_enabled() && ((uintptr_t)v % 16) == 0 && ((uintptr_t)c % 16) == 0;
+  // The stage holds 64 rows of 1.1 x the average row (rounded up to 64
+  // entries, at most the K3t stage): blocks of regular matrices fit it
+  // without paying LDS for the longest possible block; a block that does
+  // not fit takes the half-block or row-by-row path.
+  const int64_t want = ceil_div((nnz * 64 * 11) / 10 + 63, n_rows);
+  const int stage = (int)std::min<int64_t>(stream_items<A>(), std::max<int64_t>(64, ceil_div(want, 64) * 64));
+  // plus 33 rebased offsets for the half-block path
+  const size_t lds = stream_t_layout(stage, sizeof(V), sizeof(I), dl).total + 33 * sizeof(int);
+  auto go = [&](auto dc) {
+    hipLaunchKernelGGL((spmv_oneshot_kernel<V, I, P, decltype(dc)::value>), dim3((unsigned)grid), dim3(256), lds,
+                       stream, v, c, static_cast<const P*>(indptr), static_cast<const V*>(x), static_cast<V*>(y),
+                       n_rows, n_cols, nnz, blocks, remap, stage, flags);
+  };
+  if (dl) go(std::true_type{});
+  else go(std::false_type{});
+  FS_CHECK_MAIN_LAUNCH("spmv_oneshot_kernel");
+  return FS_OK;
+}
+
 }  // namespace fs
 
 using namespace fs;
@@ -1822,6 +2034,44 @@ extern "C" int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void
     case FS_C64: return dispatch_idx<c32>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
     default: return dispatch_idx<c64>(plan, vals, cols, indptr, x, y, part_dev, carry_dev, carry_bytes, stream);
   }
+}
+
+extern "C" int fs_spmv_csr_oneshot(int val_t, int idx_t, int ptr_t, int64_t n_rows, int64_t n_cols, int64_t nnz,
+                                   const void* vals, const void* cols, const void* indptr, const void* x, void* y,
+                                   int32_t* flags, hipStream_t stream) {
+  if (!valid_types(val_t, idx_t, ptr_t)) return fail(FS_E_INVALID, "fs_spmv_csr_oneshot: bad type code");
+  if (n_rows <= 0 || n_cols <= 0 || nnz <= 0)
+    return fail(FS_E_INVALID, "fs_spmv_csr_oneshot: needs rows, columns and entries (use fs_spmv_csr)");
+  if (!vals || !cols || !indptr || !x || !y || !flags) return fail(FS_E_INVALID, "fs_spmv_csr_oneshot: null pointer");
+  // the kernel writes the flags through the pinned buffer's device mapping
+  // (memory that is not pinned and mapped fails here, before any launch)
+  void* dflags = nullptr;
+  FS_CHECK_HIP(hipHostGetDevicePointer(&dflags, flags, 0));
+  for (int k = 0; k < 4; ++k) flags[k] = 0;  // host memory: no copy either way
+  int32_t* dev_flags = static_cast<int32_t*>(dflags);
+  auto by_idx = [&](auto vtag) -> int {
+    using V = decltype(vtag);
+    if (idx_t == FS_I32) {
+      if (ptr_t == FS_I32)
+        return launch_spmv_oneshot<V, int32_t, int32_t>(n_rows, n_cols, nnz, vals, cols, indptr, x, y, dev_flags, stream);
+      return launch_spmv_oneshot<V, int32_t, int64_t>(n_rows, n_cols, nnz, vals, cols, indptr, x, y, dev_flags, stream);
+    }
+    if (ptr_t == FS_I32)
+      return launch_spmv_oneshot<V, int64_t, int32_t>(n_rows, n_cols, nnz, vals, cols, indptr, x, y, dev_flags, stream);
+    return launch_spmv_oneshot<V, int64_t, int64_t>(n_rows, n_cols, nnz, vals, cols, indptr, x, y, dev_flags, stream);
+  };
+  int rc;
+  switch (val_t) {
+    case FS_F32: rc = by_idx(float{}); break;
+    case FS_F64: rc = by_idx(double{}); break;
+    case FS_C64: rc = by_idx(c32{}); break;
+    default: rc = by_idx(c64{}); break;
+  }
+  if (rc != FS_OK) return rc;
+  // the kernel's flags are in host memory once the stream has drained: the
+  // caller raises before y is used
+  FS_CHECK_HIP(hipStreamSynchronize(stream));
+  return FS_OK;
 }
 
 // ---------------------------------------------------------------------------

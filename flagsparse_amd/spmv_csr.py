@@ -16,6 +16,7 @@ into libflagsparse_hip; there is no CPU path.
 
 import ctypes
 import os
+import threading
 import time
 
 import numpy as np
@@ -24,6 +25,7 @@ import torch
 from . import _lib
 from ._common import (
     _INDEX_LIMIT_INT32,
+    HIP_VALUE_DTYPES,
     SUPPORTED_INDEX_DTYPES,
     _compute_dtype,
 )
@@ -691,6 +693,16 @@ def _prepare_spmv_csr_matrix(data, indices, indptr, shape, index_fallback_policy
     """Validation of spmv_csr.py:518-572 (same order, types and messages).
     With analyze=True the row-length analysis shares the check's device
     round trip and its plan is returned last."""
+    data, indices, indptr, n_rows, n_cols = _validate_spmv_host(data, indices, indptr, shape, index_fallback_policy)
+    if analyze:
+        _, plan = _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES, analyze=True)
+        return data, indices, indptr, n_rows, n_cols, None, plan
+    _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
+    return data, indices, indptr, n_rows, n_cols, None
+
+
+def _validate_spmv_host(data, indices, indptr, shape, index_fallback_policy="auto"):
+    """The checks of spmv_csr.py:518-545 that need no device read, in order."""
     _normalize_spmv_index_fallback_policy(index_fallback_policy)
     if not all(torch.is_tensor(t) for t in (data, indices, indptr)):
         raise TypeError("data, indices, indptr must all be torch.Tensor")
@@ -712,29 +724,26 @@ def _prepare_spmv_csr_matrix(data, indices, indptr, shape, index_fallback_policy
     if indptr.dtype not in SUPPORTED_INDEX_DTYPES:
         raise TypeError("indptr dtype must be torch.int32 or torch.int64")
 
-    data = data.contiguous()
-    indices = indices.contiguous()
-    indptr = indptr.contiguous()
-    if analyze:
-        _, plan = _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES, analyze=True)
-        return data, indices, indptr, n_rows, n_cols, None, plan
-    _check_structure(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
-    return data, indices, indptr, n_rows, n_cols, None
+    return data.contiguous(), indices.contiguous(), indptr.contiguous(), n_rows, n_cols
 
 
 def _validate_spmv_x(x, prepared):
     """spmv_csr.py:575-588."""
+    return _validate_spmv_x_for(x, prepared.data.dtype, prepared.n_cols, prepared.data.device)
+
+
+def _validate_spmv_x_for(x, dtype, n_cols, device):
     if x is None or not torch.is_tensor(x):
         raise TypeError("x must be a torch.Tensor")
     if x.ndim != 1:
         raise ValueError("x must be a 1D tensor")
     if not x.is_cuda:
         raise ValueError("x must be a CUDA tensor")
-    if x.dtype != prepared.data.dtype:
+    if x.dtype != dtype:
         raise TypeError("x dtype must match sparse matrix dtype")
-    if x.numel() != prepared.n_cols:
-        raise ValueError(f"x length must be n_cols={prepared.n_cols}, got {x.numel()}")
-    if x.device != prepared.data.device:
+    if x.numel() != n_cols:
+        raise ValueError(f"x length must be n_cols={n_cols}, got {x.numel()}")
+    if x.device != device:
         raise ValueError("x must be on the same device as sparse matrix data")
     return x.contiguous()
 
@@ -1023,6 +1032,10 @@ def flagsparse_spmv_csr(
     if prepared is None:
         if any(arg is None for arg in (data, indices, indptr, shape)):
             raise ValueError("data, indices, indptr, and shape are required when prepared is not provided")
+        if op_code == SPMV_OP_NON and not use_opt:
+            fast = _spmv_oneshot(data, indices, indptr, x, shape, index_fallback_policy, bool(return_time or return_meta))
+            if fast is not None:
+                return _finish_spmv(fast[0], out, return_time, return_meta, 0.0, fast[1], 0, "oneshot")
         prepared = _prepare_spmv(
             data,
             indices,
@@ -1062,6 +1075,14 @@ def flagsparse_spmv_csr(
         torch.cuda.synchronize()
         compute_ms = (time.perf_counter() - t1) * 1000.0
         op_total_ms = symbolic_ms + compute_ms
+    kernel = ("opt" if opt is not None else prepared.kernel_name) if prepared.n_rows > 0 else None
+    return _finish_spmv(y, out, return_time, return_meta, symbolic_ms, compute_ms,
+                        opt.bucket_count if opt is not None else 0, kernel)
+
+
+def _finish_spmv(y, out, return_time, return_meta, symbolic_ms, compute_ms, bucket_count, kernel):
+    """`out` handling and the return forms of spmv_csr.py:892-913."""
+    op_total_ms = None if compute_ms is None else (symbolic_ms or 0.0) + compute_ms
     if out is not None:
         if not out.is_cuda:
             raise ValueError("out must be a CUDA tensor")
@@ -1076,8 +1097,8 @@ def flagsparse_spmv_csr(
             "symbolic_ms": symbolic_ms,
             "compute_ms": compute_ms,
             "op_total_ms": op_total_ms,
-            "bucket_count": opt.bucket_count if opt is not None else 0,
-            "kernel": ("opt" if opt is not None else prepared.kernel_name) if prepared.n_rows > 0 else None,
+            "bucket_count": bucket_count,
+            "kernel": kernel,
         }
         if return_time:
             return y, op_total_ms, meta
@@ -1085,3 +1106,64 @@ def flagsparse_spmv_csr(
     if return_time:
         return y, op_total_ms
     return y
+
+
+_oneshot_local = threading.local()
+
+
+def _oneshot_flags():
+    """This thread's 4 pinned int32 flags for the one-shot kernel (the kernel
+    writes them in host memory; calls on one thread never overlap, each
+    synchronises its stream before it returns)."""
+    f = getattr(_oneshot_local, "flags", None)
+    if f is None:
+        f = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        _oneshot_local.flags = f
+    return f
+
+
+def _oneshot_launch(data, indices, indptr, x, y, n_rows, n_cols, flags):
+    """One fs_spmv_csr_oneshot call; its status (nonzero: the general path runs)."""
+    return _lib.lib().fs_spmv_csr_oneshot(
+        _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype), n_rows, n_cols,
+        data.numel(), _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(x), _lib.ptr(y),
+        flags.data_ptr(), _lib.stream_handle(data.device))
+
+
+def _spmv_oneshot(data, indices, indptr, x, shape, index_fallback_policy, timed):
+    """The unprepared y = A x in one launch (fs_spmv_csr_oneshot): the
+    kernel checks the structure while it computes, and the reference's
+    errors are raised here, in its order (spmv_csr.py:546-558), before y
+    is returned or `out` is written.  Returns (y, compute_ms) or None when
+    the general path must run: an invalid x (its error comes after the
+    structure checks), empty shapes, float16 / bfloat16, a forced kernel,
+    or a failed launch (the general path holds the int64 -> int32 fallback)."""
+    if os.environ.get("FLAGSPARSE_SPMV_ONESHOT", "1") == "0" or os.environ.get("FLAGSPARSE_SPMV_KERNEL"):
+        return None
+    data, indices, indptr, n_rows, n_cols = _validate_spmv_host(data, indices, indptr, shape, index_fallback_policy)
+    nnz = data.numel()
+    if data.dtype not in HIP_VALUE_DTYPES or n_rows == 0 or n_cols == 0 or nnz == 0:
+        return None
+    try:
+        x = _validate_spmv_x_for(x, data.dtype, n_cols, data.device)
+    except (TypeError, ValueError):
+        return None
+    y = torch.empty(n_rows, dtype=data.dtype, device=data.device)
+    flag_t = _oneshot_flags()
+    if timed:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+    rc = _oneshot_launch(data, indices, indptr, x, y, n_rows, n_cols, flag_t)
+    if rc != 0:
+        return None
+    compute_ms = (time.perf_counter() - t0) * 1000.0 if timed else None
+    flags = flag_t.tolist()
+    if flags[0]:
+        raise ValueError(_SPMV_STRUCT_MESSAGES["start"])
+    if flags[1]:
+        raise ValueError(_SPMV_STRUCT_MESSAGES["last"](None))
+    if flags[2]:
+        raise ValueError(_SPMV_STRUCT_MESSAGES["monotone"])
+    if flags[3]:
+        raise IndexError("indices out of range for n_cols")
+    return y, compute_ms

@@ -173,6 +173,26 @@ int fs_spmv_csr(const fs_csr_plan* plan, const void* vals, const void* cols,
                 hipStream_t stream);
 
 /*
+ * The unprepared public SpMV call in one launch and one round trip.
+ * Replaces the structure checks of _prepare_spmv_csr_matrix
+ * (spmv_csr.py:546-558: indptr[0] == 0, indptr[-1] == nnz, a non-decreasing
+ * indptr, columns in [0, n_cols)) and the launch of
+ * _triton_spmv_csr_impl_prepared (spmv_csr.py:679-723) as the reference's
+ * flagsparse_spmv_csr runs them without `prepared` (spmv_csr.py:813-913).
+ * The kernel checks the structure while it computes y = A x; malformed
+ * input is never read out of bounds (row pointers are clamped, stray
+ * columns read column 0) and its y is garbage.  flags is 4 int32 of pinned,
+ * device-accessible host memory (hipHostMalloc, or a torch tensor with
+ * pin_memory=True): the call zeroes it, the kernel writes it directly, and
+ * on return (the call synchronises `stream`) flags[0..3] are nonzero for a
+ * bad start, a bad end, a decrease and a column out of range, the
+ * reference's order of checks.  Needs n_rows, n_cols and nnz > 0.
+ */
+int fs_spmv_csr_oneshot(int val_t, int idx_t, int ptr_t, int64_t n_rows, int64_t n_cols,
+                        int64_t nnz, const void* vals, const void* cols, const void* indptr,
+                        const void* x, void* y, int32_t* flags, hipStream_t stream);
+
+/*
  * fs_spmv_csr without a caller workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The

@@ -211,6 +211,7 @@ def test_spmv_prepared_op_mismatch_rejected(device):
 
 
 def test_spmv_int64_auto_fallback_to_int32(device, monkeypatch):
+    monkeypatch.setenv("FLAGSPARSE_SPMV_ONESHOT", "0")  # the general path's launcher fails
     d, i, p, sh = S.random_csr(12, 9, 0.4, torch.float32, torch.int64, device, seed=2)
     x = S.vector(9, torch.float32, device)
     ref = O.spmv_csr_wide(np_(d), np_(i), np_(p), np_(x), sh)
@@ -230,6 +231,7 @@ def test_spmv_int64_auto_fallback_to_int32(device, monkeypatch):
 
 
 def test_spmv_int64_strict_no_fallback(device, monkeypatch):
+    monkeypatch.setenv("FLAGSPARSE_SPMV_ONESHOT", "0")
     d, i, p, sh = S.random_csr(12, 9, 0.4, torch.float32, torch.int64, device, seed=2)
     x = S.vector(9, torch.float32, device)
 
@@ -329,12 +331,13 @@ def test_spmv_panels_match_unpanelled(device, monkeypatch, index_dtype):
     # both are f64 sums rounded once to f32: at most one ulp apart
     diff = (y.double() - y0.double()).abs()
     assert bool((diff <= y0.double().abs() * 2.0**-23 + 1e-30).all())
-    # a one-shot call (no prepared object) skips the panel copy: same kernel
-    # and bits as the unpanelled prepared path
+    # a one-shot call (no prepared object) skips the panel copy and runs the
+    # one-launch kernel: again an f64 sum rounded once
     monkeypatch.delenv("FLAGSPARSE_SPMV_PANELS")
     y1, meta = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh, return_meta=True)
-    assert meta["kernel"] == "merge"
-    assert torch.equal(y1, y0)
+    assert meta["kernel"] == "oneshot"
+    diff = (y1.double() - y0.double()).abs()
+    assert bool((diff <= y0.double().abs() * 2.0**-23 + 1e-30).all())
     gen = np.random.default_rng(1)
     rows = sorted(set(gen.integers(0, sh[0], 3000).tolist()) | {0, sh[0] - 1})
     _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[data.dtype])
@@ -847,6 +850,7 @@ def test_stream_t_misaligned_arrays_match(device, monkeypatch, dtype):
     for k in ("FLAGSPARSE_SPMV_SELL", "FLAGSPARSE_SPMV_KERNEL", "FLAGSPARSE_SPMV_STREAM_T_DL"):
         monkeypatch.delenv(k, raising=False)
     monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "0")
+    monkeypatch.setenv("FLAGSPARSE_SPMV_ONESHOT", "0")  # the unprepared call runs K3t itself
     data, indices, indptr, sh = S.stencil27(24, dtype, torch.int32, device, seed=9)
     x = S.vector(sh[1], dtype, device, seed=4)
     y = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh, return_meta=True)
