@@ -50,6 +50,9 @@ CONFIGS = {
                                                 n=64),
     "c5_spmm_rmat21_f32_i64_n256_non": dict(op_kind="spmm", gen="rmat", dtype="f32", index="i64", op="non", n=256),
     "c5_spmm_rmat21_c64_i64_n32_conj": dict(op_kind="spmm", gen="rmat", dtype="c64", index="i64", op="conj", n=32),
+    # not a BASELINE config: the stencil's SpMM on the prepared route (block vectors
+    # in iterative solvers), where neighbouring rows share B rows
+    "x_spmm_stencil128_f32_i32_n32": dict(op_kind="spmm", gen="stencil", dtype="f32", index="i32", op="non", n=32),
 }
 DEFAULT_CONFIG = "c2_spmv_stencil128_f64_i32"
 CONFIG_ORDER = [DEFAULT_CONFIG] + [c for c in CONFIGS if c != DEFAULT_CONFIG]
@@ -354,6 +357,18 @@ def run_config(name, args):
             _lib.ptr(ws), ws.numel(), _lib.stream_handle(device),
         )
         kernel_call = lambda: lib.fs_spmm_csr(*args_abi)  # noqa: E731
+        step()  # the first launch builds the route's copies (the SELL-64 copy of a stencil)
+        sell = plan._sell
+        if sell is not None and sell.spmm_fits(B, C):
+            sell_abi = (
+                _lib.value_code(sell.vals.dtype), sell.col_code, _lib.index_code(sell.indptr.dtype), sell.layout,
+                sell.n_rows, _lib.ptr(sell.vals), _lib.ptr(sell.cols),
+                _lib.ptr(sell.table) if sell.table is not None else None, _lib.ptr(sell.slice_ptr),
+                _lib.ptr(sell.indptr), _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.stream_handle(device),
+            )
+            kernel_call = lambda: lib.fs_spmm_sell(*sell_abi)  # noqa: E731
+            extra["sell_column_storage"] = {0: "int32", 1: "int64", 2: "int16 offset from the row",
+                                            3: "uint8 code of the offset from the row"}[sell.col_code]
         bytes_alg = S.bytes_spmm(nnz, m, k, n_dense, vb, ib, pb)
         flops = S.flops_spmm(nnz, n_dense, complex_values)
         extra.update(max_row_nnz=plan.csr.max_row_nnz, analysis_ms=round(analysis_ms, 3), n_dense=n_dense)

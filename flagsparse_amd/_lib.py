@@ -73,6 +73,7 @@ EXPORTED_SYMBOLS = (
     "fs_sell_max_offset",
     "fs_csr_to_sell",
     "fs_spmv_sell",
+    "fs_spmm_sell",
 )
 
 
@@ -189,6 +190,9 @@ def _declare(lib):
     lib.fs_spmv_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.fs_spmv_csr_oneshot.restype = _i32
     lib.fs_spmv_csr_oneshot.argtypes = [_i32, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.fs_spmm_sell.restype = _i32
+    lib.fs_spmm_sell.argtypes = [_i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
+                                 _vp]
     lib.fs_last_kernel.restype = ctypes.c_char_p
     lib.fs_last_kernel.argtypes = []
 

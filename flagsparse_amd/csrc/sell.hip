@@ -453,6 +453,203 @@ struct SpmvF {
   }
 };
 
+// ---------------------------------------------------------------------------
+// SELL-64 SpMM: C = A B for a prepared matrix with a SELL-64 copy (banded and
+// stencil matrices) and a row-major B / C.  Replaces, for these matrices,
+// the reference's per-row SpMM kernels (spmm_csr.py:134-237) on the
+// prepared route (spmm_csr.py:2040-2174).
+//
+// One wave per (slice, column tile): LPR lanes cover a B-row slice of
+// LPR x 16 bytes (one 16-byte load each), so one load instruction gathers
+// 64 / LPR consecutive rows' B rows, and for a stencil's slot j those are
+// B rows r + o_j .. r + o_j + 64 / LPR - 1: one contiguous run of
+// 64 x 16 bytes, as coalesced as a dense row block.  A lane accumulates
+// LPR rows (rows sub, sub + 64 / LPR, ...) of its column slice, each in CSR
+// entry order and in the accumulator type, as the lane-group kernel sums a
+// row that stays inside one of its sub-tiles.  Slots past a row's length are never
+// loaded or multiplied.  U slots' gathers are issued before any is used.
+// ---------------------------------------------------------------------------
+// Lane `src`'s value of any 4-byte-multiple type, by ds_bpermute.
+template <class X>
+__device__ inline X bcast_lane_any(const X& v, int src) {
+  constexpr int W = (int)(sizeof(X) / 4);
+  int w[W];
+  __builtin_memcpy(w, &v, sizeof(X));
+#pragma unroll
+  for (int k = 0; k < W; ++k) w[k] = __builtin_amdgcn_ds_bpermute(src << 2, w[k]);
+  X out;
+  __builtin_memcpy(&out, w, sizeof(X));
+  return out;
+}
+
+template <class V, class SI, class P, int LPR, int G, bool DELTA, int U>
+__global__ __launch_bounds__(256) void spmm_sell_kernel(const V* __restrict__ sell_vals,
+                                                        const SI* __restrict__ sell_cols,
+                                                        const int* __restrict__ table,
+                                                        const int64_t* __restrict__ slice_ptr,
+                                                        const P* __restrict__ rowptr, const V* __restrict__ B,
+                                                        int64_t ldb, V* __restrict__ C, int64_t ldc,
+                                                        int64_t n_dense, int64_t n_rows, int64_t n_slices,
+                                                        int col_tiles, int64_t n_blocks, int remap) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  using L4 = __attribute__((ext_vector_type(4))) unsigned int;
+  constexpr int EPL = (int)(16 / sizeof(V));
+  constexpr int RW = 64 / LPR;  // rows per load instruction
+  constexpr bool kCodes = std::is_same<SI, uint8_t>::value;
+  __shared__ int s_tab[kCodes ? kSellCodes : 1];
+  if constexpr (kCodes) {
+    s_tab[threadIdx.x] = table[threadIdx.x];  // blockDim.x == kSellCodes
+    __syncthreads();
+  }
+  int64_t blk = blockIdx.x;
+  if (remap) {  // XCD k walks a contiguous range of slices (their B rows overlap)
+    const int64_t per = (n_blocks + 7) / 8;
+    blk = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (blk >= n_blocks) return;  // whole workgroup
+  }
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = blk * 4 + (threadIdx.x >> 6);
+  const int64_t slice = wid / col_tiles;
+  const int ctile = (int)(wid - slice * col_tiles);
+  if (slice >= n_slices) return;  // whole wave
+  const int sub = lane / LPR;
+  const int gl = lane % LPR;
+  const int64_t col = (int64_t)ctile * (LPR * EPL) + (int64_t)gl * EPL;
+  const bool cvalid = col < n_dense;
+  const int64_t col_ld = cvalid ? col : 0;
+  const int64_t row0 = slice * kSellRows;
+  int len[LPR];
+#pragma unroll
+  for (int k = 0; k < LPR; ++k) {
+    const int64_t r = row0 + sub + RW * k;
+    len[k] = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
+  }
+  const int64_t base = slice_ptr[slice];
+  const int slots = (int)((slice_ptr[slice + 1] - base) / kSellRows);
+  // lane = row for the slot's value and column (one coalesced load each);
+  // the lanes that gather a row's B slice take them by ds_bpermute
+  const int64_t my_r = row0 + lane;
+  const int my_len = my_r < n_rows ? (int)((int64_t)rowptr[my_r + 1] - (int64_t)rowptr[my_r]) : 0;
+  A acc[LPR][EPL];
+#pragma unroll
+  for (int k = 0; k < LPR; ++k)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[k][e] = T::zero();
+  const char* Bc = reinterpret_cast<const char*>(B + col_ld);
+  const int64_t row_bytes = ldb * (int64_t)sizeof(V);
+  for (int j0 = 0; j0 < slots; j0 += U) {
+    V a[U][LPR];
+    L4 q[U][LPR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + u;
+      V my_a = V{};
+      int64_t my_b = 0;  // B row of this lane's row at slot j
+      if (j < my_len) {
+        const int64_t idx = base + (int64_t)(j / G) * (G * kSellRows) + G * lane + (j % G);
+        my_a = load_stream(sell_vals + idx);
+        const SI c = __builtin_nontemporal_load(sell_cols + idx);
+        if constexpr (kCodes)
+          my_b = my_r + s_tab[c];
+        else
+          my_b = DELTA ? my_r + (int64_t)c : (int64_t)c;
+      }
+#pragma unroll
+      for (int k = 0; k < LPR; ++k) {
+        const int src = sub + RW * k;
+        a[u][k] = bcast_lane_any(my_a, src);
+        const int64_t brow = bcast_lane_any(my_b, src);
+        if (j < len[k]) q[u][k] = *reinterpret_cast<const L4*>(Bc + brow * row_bytes);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int k = 0; k < LPR; ++k) {
+        if (j0 + u < len[k]) {
+          V b[EPL];
+          __builtin_memcpy(b, &q[u][k], 16);
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[k][e] = T::fma(a[u][k], b[e], acc[k][e]);
+        }
+      }
+    }
+  }
+  if (!cvalid) return;
+#pragma unroll
+  for (int k = 0; k < LPR; ++k) {
+    const int64_t r = row0 + sub + RW * k;
+    if (r < n_rows) {
+      V o[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = T::out(acc[k][e]);
+      L4 w;
+      __builtin_memcpy(&w, o, 16);
+      *reinterpret_cast<L4*>(C + r * ldc + col) = w;
+    }
+  }
+}
+
+template <class V, class I, class P, bool DELTA>
+int spmm_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, const int* table,
+                const int64_t* slice_ptr, const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc,
+                int64_t n_dense, hipStream_t s) {
+  constexpr int EPL = (int)(16 / sizeof(V));
+  if (n_dense % EPL || ldb % EPL || ldc % EPL || ((uintptr_t)B % 16) || ((uintptr_t)C % 16))
+    return fail(FS_E_INVALID, "fs_spmm_sell: B / C rows must be whole 16-byte slices (n_dense, ldb, ldc multiples of " +
+                                  std::to_string(EPL) + ", 16-byte aligned)");
+  if (layout == FS_SELL_PAIR && VT<V>::complex) return fail(FS_E_INVALID, "fs_spmm_sell: the pair layout is for real values");
+  const int64_t n_slices = ceil_div(n_rows, kSellRows);
+  const int64_t slices_lanes = n_dense / EPL;  // 16-byte slices per B row
+  // lanes per row: 8 (a 128-byte tile of the row per lane group; wider B runs
+  // several column tiles), fewer for narrower B
+  int lpr = env_int("FLAGSPARSE_SPMM_SELL_LPR", 8);
+  if (lpr != 1 && lpr != 2 && lpr != 4) lpr = 8;
+  while (lpr > 1 && lpr / 2 >= slices_lanes) lpr /= 2;
+  const int u = env_int("FLAGSPARSE_SPMM_SELL_U", 1);  // 27-point 128^3 f32 N = 32: 0.588 / 0.650 / 1.028 ms at 1 / 2 / 4
+  const int col_tiles = (int)ceil_div(slices_lanes, lpr);
+  const int64_t waves = n_slices * col_tiles;
+  const int64_t blocks = ceil_div(waves, 4);
+  int remap = env_int("FLAGSPARSE_SPMM_SELL_REMAP", 1);
+  const int64_t grid = remap ? ceil_div(blocks, 8) * 8 : blocks;
+  if (grid > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmm_sell: grid too large");
+  auto go = [&](auto lc, auto gc) {
+    auto launch = [&](auto uc) {
+      hipLaunchKernelGGL((spmm_sell_kernel<V, I, P, decltype(lc)::value, decltype(gc)::value, DELTA,
+                                           decltype(uc)::value>),
+                         dim3((unsigned)grid), dim3(256), 0, s, static_cast<const V*>(sv), static_cast<const I*>(sc),
+                         table, slice_ptr, static_cast<const P*>(indptr), static_cast<const V*>(B), ldb,
+                         static_cast<V*>(C), ldc, n_dense, n_rows, n_slices, col_tiles, blocks, remap);
+    };
+    if (u <= 1) launch(std::integral_constant<int, 1>{});
+    else if (u >= 4) launch(std::integral_constant<int, 4>{});
+    else launch(std::integral_constant<int, 2>{});
+  };
+  auto by_g = [&](auto lc) {
+    if (layout == FS_SELL_PAIR) go(lc, std::integral_constant<int, 2>{});
+    else go(lc, std::integral_constant<int, 1>{});
+  };
+  switch (lpr) {
+    case 1: by_g(std::integral_constant<int, 1>{}); break;
+    case 2: by_g(std::integral_constant<int, 2>{}); break;
+    case 4: by_g(std::integral_constant<int, 4>{}); break;
+    default: by_g(std::integral_constant<int, 8>{}); break;
+  }
+  FS_CHECK_MAIN_LAUNCH("spmm_sell_kernel");
+  return FS_OK;
+}
+
+template <class V, class I, class P>
+struct SpmmF {
+  int operator()(int layout, int64_t n_rows, const void* sv, const void* sc, const int* table,
+                 const int64_t* slice_ptr, const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc,
+                 int64_t n_dense, hipStream_t s) const {
+    return spmm_sell_t<V, I, P, std::is_same<I, int16_t>::value>(layout, n_rows, sv, sc, table, slice_ptr, indptr,
+                                                                  B, ldb, C, ldc, n_dense, s);
+  }
+};
+
 }  // namespace fs
 
 using namespace fs;
@@ -520,4 +717,20 @@ extern "C" int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, in
   if (!indptr || !slice_ptr || !y) return fail(FS_E_INVALID, "fs_spmv_sell: null pointer");
   return dispatch_vip<SpmvF>(val_t, sell_idx_t, ptr_t, layout, n_rows, sell_vals, sell_cols, code_table, slice_ptr,
                              indptr, x, y, stream);
+}
+
+extern "C" int fs_spmm_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
+                            const void* sell_vals, const void* sell_cols, const int32_t* code_table,
+                            const int64_t* slice_ptr, const void* indptr, const void* B, int64_t ldb, void* C,
+                            int64_t ldc, int64_t n_dense, hipStream_t stream) {
+  if (!valid_types(val_t, (sell_idx_t == FS_SELL_D16 || sell_idx_t == FS_SELL_C8) ? FS_I32 : sell_idx_t, ptr_t))
+    return fail(FS_E_INVALID, "fs_spmm_sell: bad type code");
+  if (sell_idx_t == FS_SELL_C8 && !code_table) return fail(FS_E_INVALID, "fs_spmm_sell: code table is null");
+  if (!(layout == FS_SELL_SLOT || layout == FS_SELL_PAIR)) return fail(FS_E_INVALID, "fs_spmm_sell: bad layout");
+  if (n_rows < 0 || n_dense < 0) return fail(FS_E_INVALID, "fs_spmm_sell: negative size");
+  if (n_rows == 0 || n_dense == 0) return FS_OK;
+  if (ldc < n_dense || ldb < n_dense) return fail(FS_E_INVALID, "fs_spmm_sell: leading dimension smaller than n_dense");
+  if (!indptr || !slice_ptr || !C || !B) return fail(FS_E_INVALID, "fs_spmm_sell: null pointer");
+  return dispatch_vip<SpmmF>(val_t, sell_idx_t, ptr_t, layout, n_rows, sell_vals, sell_cols, code_table, slice_ptr,
+                             indptr, B, ldb, C, ldc, n_dense, stream);
 }

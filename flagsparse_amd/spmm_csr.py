@@ -15,6 +15,7 @@ each into libflagsparse_hip; there is no CPU path.
 """
 
 import ctypes
+import os
 import time
 from dataclasses import dataclass
 
@@ -29,7 +30,7 @@ from ._common import (
     _tolerance_for_dtype,
 )
 from ._csr import analyze_csr, transpose_csr
-from .spmv_csr import _check_structure
+from .spmv_csr import _build_sell, _check_structure, _sell_codes_possible, _spmv_sell_locality
 
 SUPPORTED_SPMM_VALUE_DTYPES = SUPPORTED_VALUE_DTYPES
 
@@ -227,13 +228,39 @@ class _SpmmPlan:
     The sub-tile size of the SpMM kernel depends on the dense width (it sets
     the lanes per B row), so partitions are built per tile size and cached."""
 
-    __slots__ = ("csr", "indptr", "_skew_checked", "_wide")
+    __slots__ = ("csr", "indptr", "_skew_checked", "_wide", "kept", "_sell", "_sell_checked")
 
-    def __init__(self, data, indices, indptr, n_rows, n_cols):
+    def __init__(self, data, indices, indptr, n_rows, n_cols, kept=False):
         self.csr = analyze_csr(data, indices, indptr, n_rows, n_cols)
         self.indptr = indptr
         self._skew_checked = False
         self._wide = None
+        self.kept = bool(kept)  # a prepared matrix: worth a SELL-64 copy
+        self._sell = None
+        self._sell_checked = False
+
+    def sell_copy(self, data, indices):
+        """The SELL-64 copy of a kept matrix whose rows are short and whose
+        neighbouring rows use neighbouring columns (stencils, bands), built on
+        the first launch with the SpMV's criteria (_spmv_sell_locality), else
+        None.  FLAGSPARSE_SPMM_SELL=0 / 1 switches it off / forces it."""
+        if not self.kept or self._sell_checked:
+            return self._sell
+        self._sell_checked = True
+        mode = os.environ.get("FLAGSPARSE_SPMM_SELL")
+        if mode == "0":
+            return None
+        p = self.csr.plan
+        locality = 1.0 if mode == "1" else _spmv_sell_locality(
+            p, indices, self.indptr, False, _sell_codes_possible(data.element_size()))
+        if locality is not None:
+            try:
+                self._sell = _build_sell(data, indices, self.indptr, int(p.n_rows), int(p.n_cols), int(p.nnz),
+                                         locality, force=mode == "1")
+            except torch.OutOfMemoryError:
+                self._sell = None
+                torch.cuda.empty_cache()
+        return self._sell
 
     def tiling(self, value_dtype, n_dense):
         """(tile_items, n_tiles, partition) of the kernel fs_spmm_csr runs for
@@ -298,7 +325,10 @@ def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
         C_k = C
     if n_rows == 0 or n_dense == 0:
         return C_k if cdt == out_dtype else C_k.to(out_dtype)
-    if data.numel() == 0:
+    sell = plan.sell_copy(data_c, indices) if data.numel() > 0 else None
+    if sell is not None and sell.spmm_fits(B_c, C_k):
+        sell.spmm(B_c, C_k)
+    elif data.numel() == 0:
         C_k.zero_()
     else:
         plan.set_residency(indices, int(plan.csr.plan.n_cols), n_dense, cdt)
@@ -483,7 +513,8 @@ class PreparedCsrSpmmRoute:
 
     def hip_plan(self):
         if self._plan is None and self.n_rows > 0:
-            self._plan = _SpmmPlan(self.data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols)
+            self._plan = _SpmmPlan(self.data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols,
+                                   kept=True)
         return self._plan
 
 

@@ -31,7 +31,8 @@ _LONG_ROW_BIN = 12  # rows with >= 2048 nnz, the reference's long-row threshold 
 class _PreparedBase:
     def _hip_plan(self):
         if self._plan is None and self.n_rows > 0:
-            self._plan = _SpmmPlan(self.data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols)
+            self._plan = _SpmmPlan(self.data, self.kernel_indices, self.kernel_indptr, self.n_rows, self.n_cols,
+                                   kept=True)
         return self._plan
 
 

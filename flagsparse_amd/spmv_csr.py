@@ -514,14 +514,15 @@ def _sell_column_code(indices, indptr, n_rows, n_cols, value_bytes):
     return (_SELL_I32 if n_cols - 1 <= _INDEX_LIMIT_INT32 else _SELL_I64), None
 
 
-def _build_sell(data, indices, indptr, n_rows, n_cols, nnz, locality=1.0):
+def _build_sell(data, indices, indptr, n_rows, n_cols, nnz, locality=1.0, force=False):
     """The SELL-64 copy, or None, unless forced, when the sampled locality is
     below _SELL_MIN_LOCALITY (_SELL_MIN_LOCALITY_CODES with offset codes) or
     its stored slots would exceed _SELL_MAX_PADDING x nnz
     (_SELL_MAX_PADDING_CODES x nnz with offset codes; rows too uneven)."""
     col_code, offsets = _sell_column_code(indices, indptr, n_rows, n_cols, data.element_size())
     codes = col_code == _SELL_C8
-    if locality < (_SELL_MIN_LOCALITY_CODES if codes else _SELL_MIN_LOCALITY) and not _sell_forced():
+    force = force or _sell_forced()
+    if locality < (_SELL_MIN_LOCALITY_CODES if codes else _SELL_MIN_LOCALITY) and not force:
         return None
     # pairs pay with 2-byte offsets (f64 stencil 0.114 -> 0.107 ms, f32 0.086 -> 0.076);
     # with 4-byte columns they do not (f64 0.123 both, f32 0.086 -> 0.093)
@@ -529,7 +530,7 @@ def _build_sell(data, indices, indptr, n_rows, n_cols, nnz, locality=1.0):
     layout = _SELL_PAIR if pair else _SELL_SLOT
     slice_ptr, stored = _sell_slice_ptr(indptr, n_rows, _SELL_GROUP[layout])
     bound = _SELL_MAX_PADDING_CODES if codes else _SELL_MAX_PADDING
-    if stored > bound * max(1, nnz) and not _sell_forced():
+    if stored > bound * max(1, nnz) and not force:
         return None
     return SellCsr(data, indices, indptr, slice_ptr, col_code, layout, offsets)
 
@@ -582,6 +583,27 @@ class SellCsr:
             "fs_csr_to_sell",
         )
         del lut  # stream-ordered: the caching allocator reuses it only after the fill
+
+    def spmm_fits(self, B, C):
+        """Whether fs_spmm_sell takes these B / C: row-major, rows of whole
+        16-byte slices, 16-byte aligned, the copy's value type."""
+        epl = 16 // self.vals.element_size()
+        n = B.shape[1]
+        return (B.dtype == self.vals.dtype and C.dtype == self.vals.dtype and B.stride(1) == 1 and C.stride(1) == 1
+                and n % epl == 0 and B.stride(0) % epl == 0 and C.stride(0) % epl == 0
+                and B.data_ptr() % 16 == 0 and C.data_ptr() % 16 == 0 and B.stride(0) >= n and C.stride(0) >= n)
+
+    def spmm(self, B, C):
+        _lib.check(
+            _lib.lib().fs_spmm_sell(
+                _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype), self.layout,
+                self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols),
+                _lib.ptr(self.table) if self.table is not None else None, _lib.ptr(self.slice_ptr),
+                _lib.ptr(self.indptr), _lib.ptr(B), int(B.stride(0)), _lib.ptr(C), int(C.stride(0)), int(B.shape[1]),
+                _lib.stream_handle(self.vals.device),
+            ),
+            "fs_spmm_sell",
+        )
 
     def spmv(self, x, y):
         _lib.check(

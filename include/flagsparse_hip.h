@@ -396,6 +396,20 @@ int fs_csr_to_sell(int val_t, int idx_t, int ptr_t, int sell_idx_t,
                    const void* indptr, const int64_t* slice_ptr,
                    const void* code_lut, void* sell_vals, void* sell_cols,
                    hipStream_t stream);
+/*
+ * C = A B on the SELL-64 copy of a prepared matrix (fs_csr_to_sell) with a
+ * row-major B (n_cols x n_dense, leading dimension ldb) and C (n_rows x
+ * n_dense, ldc): n_dense, ldb and ldc multiples of 16 / sizeof(value), B and
+ * C 16-byte aligned.  Each row sums its entries in CSR order in the
+ * accumulator type, in one sequence.  Replaces, for banded and
+ * stencil matrices, the reference's SpMM kernels on its prepared route
+ * (spmm_csr.py:134-237 launched from spmm_csr.py:2040-2174).
+ */
+int fs_spmm_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
+                 const void* sell_vals, const void* sell_cols,
+                 const int32_t* code_table, const int64_t* slice_ptr,
+                 const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc,
+                 int64_t n_dense, hipStream_t stream);
 int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
                  const void* sell_vals, const void* sell_cols,
                  const int32_t* code_table, const int64_t* slice_ptr,
