@@ -147,7 +147,6 @@ constexpr int kDigitScanSubs = 64;
 // loop over dependent sums left the one-workgroup top scan at 83 us on 256
 // blocks)
 constexpr int kScanBatch = 16;
-constexpr int kScanTopBatch = 64;  // the one-workgroup top scan: fewer round trips
 
 template <class CT>
 __global__ __launch_bounds__(256) void digit_scan_reduce_kernel(const CT* __restrict__ cnt, int64_t n_sub,
@@ -166,39 +165,41 @@ __global__ __launch_bounds__(256) void digit_scan_reduce_kernel(const CT* __rest
   partial[(int64_t)blockIdx.x * kDigits + t] = sum;
 }
 
+// One workgroup per digit: the exclusive prefix of that digit's block sums
+// over the blocks (in place), and the digit's total into totals[digit].
+// (A single workgroup walking every digit's column took 27 us per pass on
+// C4: one CU's bandwidth.)
 template <class CT>
-__global__ __launch_bounds__(256) void digit_scan_top_kernel(CT* __restrict__ partial, int64_t n_blocks) {
+__global__ __launch_bounds__(256) void digit_scan_column_kernel(CT* __restrict__ partial, int64_t n_blocks,
+                                                                int64_t* __restrict__ totals) {
   __shared__ int64_t s_wave[4];
-  const int t = threadIdx.x;
-  int64_t total = 0;
-  for (int64_t b = 0; b < n_blocks; b += kScanTopBatch) {
-    CT v[kScanTopBatch];
-#pragma unroll
-    for (int k = 0; k < kScanTopBatch; ++k) v[k] = b + k < n_blocks ? partial[(b + k) * kDigits + t] : (CT)0;
-#pragma unroll
-    for (int k = 0; k < kScanTopBatch; ++k) total += (int64_t)v[k];
+  const int d = blockIdx.x;
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < n_blocks; b0 += 256) {
+    const int64_t b = b0 + threadIdx.x;
+    const int64_t v = b < n_blocks ? (int64_t)partial[b * kDigits + d] : 0;
+    int64_t sum;
+    const int64_t ex = block_exclusive_scan(v, s_wave, sum);
+    if (b < n_blocks) partial[b * kDigits + d] = (CT)(carry + ex);
+    carry += sum;
   }
-  int64_t all;
-  int64_t run = block_exclusive_scan(total, s_wave, all);
-  for (int64_t b = 0; b < n_blocks; b += kScanTopBatch) {
-    CT v[kScanTopBatch];
-#pragma unroll
-    for (int k = 0; k < kScanTopBatch; ++k) v[k] = b + k < n_blocks ? partial[(b + k) * kDigits + t] : (CT)0;
-#pragma unroll
-    for (int k = 0; k < kScanTopBatch; ++k) {
-      if (b + k < n_blocks) partial[(b + k) * kDigits + t] = (CT)run;
-      run += (int64_t)v[k];
-    }
-  }
+  if (threadIdx.x == 0) totals[d] = carry;
 }
 
+// Per block: every sub-tile's offset = the digit's base (the digits below it,
+// from the 256 totals) + the block's prefix within the digit + the sub-tiles
+// before it in the block.
 template <class CT>
 __global__ __launch_bounds__(256) void digit_scan_down_kernel(CT* __restrict__ cnt, int64_t n_sub,
-                                                              const CT* __restrict__ partial) {
+                                                              const CT* __restrict__ partial,
+                                                              const int64_t* __restrict__ totals) {
+  __shared__ int64_t s_wave[4];
   const int t = threadIdx.x;
+  int64_t all;
+  const int64_t base = block_exclusive_scan(totals[t], s_wave, all);
   const int64_t s0 = (int64_t)blockIdx.x * kDigitScanSubs;
   const int64_t s1 = s0 + kDigitScanSubs < n_sub ? s0 + kDigitScanSubs : n_sub;
-  CT run = partial[(int64_t)blockIdx.x * kDigits + t];
+  CT run = (CT)(base + (int64_t)partial[(int64_t)blockIdx.x * kDigits + t]);
   for (int64_t s = s0; s < s1; s += kScanBatch) {
     CT v[kScanBatch];
 #pragma unroll
@@ -746,7 +747,8 @@ Layout make_layout(int64_t n_rows, int64_t n_cols, int64_t nnz, bool payload = f
   L.off_rowid = o; o = align256(o + L.rowid_bytes * nnz);
   L.off_counts = o; o = align256(o + sizeof(int64_t) * L.n_counts);
   // partials: the flat scan's tile totals, or the digit scan's per-block rows
-  const int64_t n_part = std::max<int64_t>(L.n_partials + 1, ceil_div(L.n_sub, kDigitScanSubs) * kDigits);
+  // (the digit scan's block rows, then its 256 digit totals)
+  const int64_t n_part = std::max<int64_t>(L.n_partials + 1, ceil_div(L.n_sub, kDigitScanSubs) * kDigits + kDigits);
   L.off_partials = o; o = align256(o + sizeof(int64_t) * n_part);
   L.total = o;
   L.payload = payload;
@@ -771,11 +773,13 @@ template <class CT>
 int digit_exclusive_scan(CT* cnt, int64_t n_sub, CT* partial, hipStream_t s) {
   if (n_sub == 0) return FS_OK;
   const int64_t blocks = ceil_div(n_sub, kDigitScanSubs);
+  int64_t* totals = reinterpret_cast<int64_t*>(partial + blocks * kDigits);  // 256 more, 8-byte aligned
   hipLaunchKernelGGL((digit_scan_reduce_kernel<CT>), dim3((unsigned)blocks), dim3(256), 0, s, cnt, n_sub, partial);
   FS_CHECK_LAUNCH("digit_scan_reduce_kernel");
-  hipLaunchKernelGGL((digit_scan_top_kernel<CT>), dim3(1), dim3(256), 0, s, partial, blocks);
-  FS_CHECK_LAUNCH("digit_scan_top_kernel");
-  hipLaunchKernelGGL((digit_scan_down_kernel<CT>), dim3((unsigned)blocks), dim3(256), 0, s, cnt, n_sub, partial);
+  hipLaunchKernelGGL((digit_scan_column_kernel<CT>), dim3(kDigits), dim3(256), 0, s, partial, blocks, totals);
+  FS_CHECK_LAUNCH("digit_scan_column_kernel");
+  hipLaunchKernelGGL((digit_scan_down_kernel<CT>), dim3((unsigned)blocks), dim3(256), 0, s, cnt, n_sub, partial,
+                     totals);
   FS_CHECK_LAUNCH("digit_scan_down_kernel");
   return FS_OK;
 }

@@ -68,3 +68,35 @@ def test_noalloc_rejects_oversized_plan(device, monkeypatch):
                                  _lib.ptr(prep._part), _lib.stream_handle(device))
     assert rc == _lib.FS_E_WORKSPACE
     assert "carry scratch" in lib.fs_last_error().decode()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(device, monkeypatch):
+    """Back-to-back calls on two streams share the static array; the entry
+    point orders the second after the first (an event per call), so both
+    give fs_spmv_csr's bits with no synchronisation between them."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", "merge")
+    monkeypatch.setenv("FLAGSPARSE_SPMV_PANELS", "0")
+    monkeypatch.setenv("FLAGSPARSE_SPMV_SELL", "0")
+    lib = _lib.lib()
+    cases = []
+    for n_rows, seed in ((1 << 18, 4), (1 << 17, 5)):
+        d, i, p, sh = S.powerlaw(n_rows, torch.float64, torch.int32, device, seed=seed)
+        prep = fs.prepare_spmv_csr(d, i, p, sh)
+        x = S.vector(sh[1], torch.float64, device, seed=seed + 10)
+        y_ref, _ = _both(prep, x)
+        cases.append((prep, x, y_ref))
+    streams = [torch.cuda.Stream(device=device), torch.cuda.Stream(device=device)]
+    outs = []
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (prep, x, _), st in zip(cases, streams):
+            y = torch.full((prep.n_rows,), float("nan"), dtype=torch.float64, device=device)
+            st.wait_stream(torch.cuda.current_stream(device))  # y's fill is done before the launch
+            _lib.check(lib.fs_spmv_csr_noalloc(prep.hip_plan().plan, _lib.ptr(prep.compute_data()),
+                                               _lib.ptr(prep.kernel_indices), _lib.ptr(prep.kernel_indptr),
+                                               _lib.ptr(x), _lib.ptr(y), _lib.ptr(prep._part), st.cuda_stream),
+                       "fs_spmv_csr_noalloc")
+            outs.append((y, cases[streams.index(st)][2]))
+    torch.cuda.synchronize()
+    for y, y_ref in outs:
+        assert torch.equal(y, y_ref)
