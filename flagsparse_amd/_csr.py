@@ -37,6 +37,20 @@ class CsrPlan:
     def row_length_histogram(self):
         return [int(v) for v in self.plan.hist]
 
+    @classmethod
+    def from_sizes(cls, data, indices, indptr, n_rows, n_cols):
+        """A plan from the matrix's sizes and types alone, with no device
+        work: enough for launches that read no row statistics (the SpMM
+        kernels); its statistics (max_row_nnz, histogram) are unset."""
+        p = _lib.FsCsrPlan()
+        p.n_rows, p.n_cols, p.nnz = int(n_rows), int(n_cols), int(data.numel())
+        p.val_t = _lib.value_code(_compute_dtype(data.dtype))
+        p.idx_t = _lib.index_code(indices.dtype)
+        p.ptr_t = _lib.index_code(indptr.dtype)
+        p.kernel = _lib.FS_KERNEL_MERGE
+        p.max_row = -1
+        return cls(p, indptr.device)
+
     def n_tiles(self, tile_items):
         p = self.plan
         total = int(p.n_rows) + int(p.nnz)

@@ -76,7 +76,7 @@ class PreparedAlphaSpmmAlg1:
 
 def _prepare_alpha_spmm_alg1_common(data, indices, indptr, shape):
     """alpha_spmm_alg1.py:74-95: the CSR checks of the SpMM path, then float32 / float64 only."""
-    data, indices, indptr, n_rows, n_cols = _prepare_spmm_csr_matrix(data, indices, indptr, shape)
+    data, indices, indptr, n_rows, n_cols, _ = _prepare_spmm_csr_matrix(data, indices, indptr, shape)
     if data.dtype not in SUPPORTED_ALPHA_SPMM_ALG1_DTYPES:
         raise TypeError("alpha_spmm_alg1 TLE routes only support float32 and float64")
     row_lengths = indptr[1:] - indptr[:-1] if n_rows > 0 else indptr.new_empty((0,))

@@ -29,7 +29,7 @@ from ._common import (
     _is_complex_dtype,
     _tolerance_for_dtype,
 )
-from ._csr import analyze_csr, transpose_csr
+from ._csr import CsrPlan, analyze_csr, transpose_csr
 from .spmv_csr import _build_sell, _check_structure, _sell_codes_possible, _spmv_sell_locality
 
 SUPPORTED_SPMM_VALUE_DTYPES = SUPPORTED_VALUE_DTYPES
@@ -136,7 +136,7 @@ _SPMM_STRUCT_MESSAGES = {
 }
 
 
-def _prepare_spmm_csr_matrix(data, indices, indptr, shape):
+def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False):
     """Validation of spmm_csr.py:239-297 (same order, types and messages).
 
     The HIP kernels take int32 and int64 column indices / row pointers
@@ -170,8 +170,12 @@ def _prepare_spmm_csr_matrix(data, indices, indptr, shape):
     data = data.contiguous()
     indices = indices.contiguous()
     indptr = indptr.contiguous()
+    if analyze:
+        # the row statistics ride on the structure check's round trip
+        _, csr = _check_structure(data, indices, indptr, n_cols, messages, analyze=True)
+        return data, indices, indptr, n_rows, n_cols, csr
     _check_structure(data, indices, indptr, n_cols, messages)
-    return data, indices, indptr, n_rows, n_cols
+    return data, indices, indptr, n_rows, n_cols, None
 
 
 def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code):
@@ -230,8 +234,11 @@ class _SpmmPlan:
 
     __slots__ = ("csr", "indptr", "_skew_checked", "_wide", "kept", "_sell", "_sell_checked")
 
-    def __init__(self, data, indices, indptr, n_rows, n_cols, kept=False):
-        self.csr = analyze_csr(data, indices, indptr, n_rows, n_cols)
+    def __init__(self, data, indices, indptr, n_rows, n_cols, kept=False, csr=None):
+        # csr: a CsrPlan of this matrix from a round trip the caller already
+        # made (the structure check's), or one built from its sizes alone
+        # (CsrPlan.from_sizes) when no launch decision needs row statistics
+        self.csr = csr if csr is not None else analyze_csr(data, indices, indptr, n_rows, n_cols)
         self.indptr = indptr
         self._skew_checked = False
         self._wide = None
@@ -395,7 +402,8 @@ def flagsparse_spmm_csr(
     if max_segments is not None and max_segments <= 0:
         raise ValueError("max_segments must be positive when provided")
 
-    data, indices, indptr, n_rows, n_cols = _prepare_spmm_csr_matrix(data, indices, indptr, shape)
+    data, indices, indptr, n_rows, n_cols, csr0 = _prepare_spmm_csr_matrix(
+        data, indices, indptr, shape, analyze=not _spmm_op_transposes(op_code))
     if B.ndim != 2:
         raise ValueError("B must be a 2D dense tensor")
     eff_rows, eff_cols = (n_cols, n_rows) if _spmm_op_transposes(op_code) else (n_rows, n_cols)
@@ -430,9 +438,14 @@ def flagsparse_spmm_csr(
         t1 = time.perf_counter()
         symbolic_ms = (t1 - t0) * 1000.0 if _spmm_op_transposes(op_code) else 0.0
 
-    plan = _SpmmPlan(data, indices, indptr, n_rows, n_cols) if n_rows > 0 else None
-    max_row = plan.csr.max_row_nnz if plan is not None else 0
-    _check_segment_override(max_row, block_nnz, max_segments)
+    plan = None
+    if n_rows > 0:
+        if csr0 is None and max_segments is None:
+            # A^T / A^H: no launch decision needs its row statistics (only an
+            # explicit max_segments does), so no analysis round trip
+            csr0 = CsrPlan.from_sizes(data, indices, indptr, n_rows, n_cols)
+        plan = _SpmmPlan(data, indices, indptr, n_rows, n_cols, csr=csr0)
+        _check_segment_override(plan.csr.max_row_nnz if max_segments is not None else 0, block_nnz, max_segments)
     if do_timing:
         torch.cuda.synchronize()
         t1 = time.perf_counter()
@@ -782,7 +795,8 @@ def prepare_spmm_csr_route(data, indices, indptr, shape, *, op="non", alg="auto"
     """Prepare matrix-level CSR SpMM metadata for the route-based run API."""
     op_code = _normalize_spmm_op(op)
     op_name = _spmm_op_to_name(op_code)
-    data, indices, indptr, n_rows, n_cols = _prepare_spmm_csr_matrix(data, indices, indptr, shape)
+    data, indices, indptr, n_rows, n_cols, csr0 = _prepare_spmm_csr_matrix(data, indices, indptr, shape,
+                                                                            analyze=True)
     resolved = _normalize_spmm_csr_alg(alg)
     if resolved != "auto":
         resolve_spmm_csr_algorithm(resolved, op_name, data.dtype)
@@ -799,6 +813,8 @@ def prepare_spmm_csr_route(data, indices, indptr, shape, *, op="non", alg="auto"
         op=op_name,
         alg=resolved,
     )
+    if n_rows > 0:  # the row statistics came with the structure check's round trip
+        route._plan = _SpmmPlan(data, indices, indptr, n_rows, n_cols, kept=True, csr=csr0)
     plan = route.hip_plan()
     route.max_row_nnz = plan.csr.max_row_nnz if plan is not None else 0
     return route

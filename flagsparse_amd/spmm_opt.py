@@ -120,7 +120,7 @@ class PreparedCsrSpmmOptAlg2(_PreparedBase):
 
 
 def _prepared_fields(data, indices, indptr, shape):
-    data, indices, indptr, n_rows, n_cols = _prepare_spmm_csr_matrix(data, indices, indptr, shape)
+    data, indices, indptr, n_rows, n_cols, _ = _prepare_spmm_csr_matrix(data, indices, indptr, shape)
     row_lengths = indptr[1:] - indptr[:-1] if n_rows > 0 else indptr.new_empty((0,))
     return data, indices, indptr, n_rows, n_cols, row_lengths
 
