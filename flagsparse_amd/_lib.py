@@ -43,6 +43,9 @@ EXPORTED_SYMBOLS = (
     "fs_version",
     "fs_csr_check_bytes",
     "fs_csr_check",
+    "fs_csr_check_enqueue",
+    "fs_csr_transpose_bounded",
+    "fs_csr_check_decode",
     "fs_csr_check_analyze_bytes",
     "fs_csr_check_analyze",
     "fs_csr_stats_bytes",
@@ -122,6 +125,12 @@ def _declare(lib):
     lib.fs_csr_check_bytes.argtypes = []
     lib.fs_csr_check.restype = _i32
     lib.fs_csr_check.argtypes = [_vp, _i32, _vp, _i32, _i64, _i64, _vp, ctypes.POINTER(_i64), _vp]
+    lib.fs_csr_transpose_bounded.restype = _i32
+    lib.fs_csr_transpose_bounded.argtypes = [_i32, _i64, _i64, _i64]
+    lib.fs_csr_check_enqueue.restype = _i32
+    lib.fs_csr_check_enqueue.argtypes = [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _vp, _vp]
+    lib.fs_csr_check_decode.restype = _i32
+    lib.fs_csr_check_decode.argtypes = [_vp, _i64, ctypes.POINTER(_i64)]
     lib.fs_csr_check_analyze_bytes.restype = _sz
     lib.fs_csr_check_analyze_bytes.argtypes = []
     lib.fs_csr_check_analyze.restype = _i32

@@ -1957,6 +1957,25 @@ extern "C" int fs_csr_check(const void* indptr, int ptr_t, const void* indices, 
   return FS_OK;
 }
 
+extern "C" int fs_csr_check_enqueue(const void* indptr, int ptr_t, const void* indices, int idx_t, int64_t n_rows,
+                                    int64_t nnz, void* check_dev, void* host_words, hipStream_t stream) {
+  if (!host_words) return fail(FS_E_INVALID, "fs_csr_check_enqueue: host_words is null");
+  const int64_t dummy = 0;
+  int rc = check_args("fs_csr_check_enqueue", indptr, ptr_t, indices, idx_t, n_rows, nnz, check_dev, &dummy);
+  if (rc != FS_OK) return rc;
+  unsigned long long* ck = static_cast<unsigned long long*>(check_dev);
+  rc = launch_check(indptr, ptr_t, indices, idx_t, n_rows, nnz, ck, stream);
+  if (rc != FS_OK) return rc;
+  FS_CHECK_HIP(hipMemcpyAsync(host_words, ck, 5 * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream));
+  return FS_OK;
+}
+
+extern "C" int fs_csr_check_decode(const void* host_words, int64_t nnz, int64_t* out) {
+  if (!host_words || !out) return fail(FS_E_INVALID, "fs_csr_check_decode: null pointer");
+  decode_check(static_cast<const unsigned long long*>(host_words), nnz, out);
+  return FS_OK;
+}
+
 extern "C" size_t fs_csr_check_analyze_bytes(void) { return (5 + kStatsWords) * sizeof(unsigned long long); }
 
 extern "C" int fs_csr_check_analyze(const void* indptr, int ptr_t, const void* indices, int idx_t, int val_t,

@@ -717,6 +717,508 @@ __global__ __launch_bounds__(256) void identity_kernel(const void* __restrict__ 
   if (k < n) keys[k] = load_key<K>(cols, kind, k);
 }
 
+// ---- workgroup-tile radix passes (the transpose of 4- and 8-byte values) ----
+// A workgroup of kWgWaves waves sorts a tile of kWgTile entries per pass
+// (wave w holds entries [w * kWgSub, (w + 1) * kWgSub) of the tile in
+// registers, kWgChunks per lane, and ranks them as radix_scatter_kernel
+// does, against its own LDS counters).  The larger tile allows more digits
+// at the same run length per digit, up to 11 key bits per pass: the 20-bit
+// columns of a 1M-column matrix take two passes instead of three.  The
+// payload carries the entry's value and row (an 8-byte word for 4-byte
+// values, 12 bytes for 8-byte values), built by the first pass from the
+// CSR arrays and written out as the transposed values and rows by the last,
+// and the last pass writes no keys: the column pointer comes from an atomic
+// minimum of the first position of each column the tile holds, and a
+// suffix minimum over the columns (empty columns take the next one's start).
+#ifndef FS_WG_WAVES
+#define FS_WG_WAVES 16
+#endif
+#ifndef FS_WG_CHUNKS
+#define FS_WG_CHUNKS 12
+#endif
+#ifndef FS_WG_MIN_WAVES
+#define FS_WG_MIN_WAVES 4
+#endif
+constexpr int kWgWaves = FS_WG_WAVES;
+constexpr int kWgThreads = 64 * kWgWaves;
+constexpr int kWgChunks = FS_WG_CHUNKS;
+constexpr int64_t kWgSub = 64 * kWgChunks;
+constexpr int64_t kWgTile = kWgWaves * kWgSub;
+constexpr int kWgMaxBits = 11;
+constexpr int kWgScanTiles = 16;  // tiles per block of the digit scan
+constexpr int kWgMaxDigits = 1 << kWgMaxBits;
+// staging buffer: row marks, wave counters, keys, then the payload in
+// windows (a multiple of 8 and 12 bytes; half a tile of 12-byte payload, so
+// the payload leaves in two windows)
+constexpr int kWgBufHalf = (int)(kWgTile / 2) * 12;
+constexpr int kWgBufMin = kWgWaves * kWgMaxDigits * 2 > kWgBufHalf ? kWgWaves * kWgMaxDigits * 2 : kWgBufHalf;
+constexpr int kWgBufBytes = (kWgBufMin + 23) / 24 * 24;
+// the wave counters hold two digits per word (16-bit counts: a wave ranks
+// at most kWgSub entries, a tile at most kWgTile < 2^16)
+static_assert(kWgTile < 65536, "16-bit digit counters");
+static_assert(kWgWaves * kWgMaxDigits * 2 <= kWgBufBytes, "wave counters fit the staging buffer");
+static_assert(kWgTile * 4 <= kWgBufBytes, "row marks and keys fit the staging buffer");
+
+// The payload between passes: the entry's value word(s) and row.  (Records
+// that also carried the key, so that a digit's run left as one block, measured
+// slower: the next pass's count then reads the whole records.)
+struct alignas(4) Pay12 {
+  uint32_t v0, v1, r;
+};
+template <int VW>
+struct WgPay;
+template <>
+struct WgPay<1> {
+  using T = uint64_t;  // value | row << 32
+};
+template <>
+struct WgPay<2> {
+  using T = Pay12;
+};
+
+struct WgIO {
+  const void* vals;         // first pass: CSR values (VW 4-byte words each)
+  const void* rowptr;       // first pass: CSR row pointer
+  int ptr64;
+  const int64_t* tile_row;  // first pass: row of each wave sub-tile's first entry
+  int64_t n_rows;
+  int64_t n_sub;
+  void* t_vals;             // last pass: transposed values
+  void* t_cols;             // last pass: transposed column indices (the rows)
+  int oi64;
+  void* colptr;             // last pass: atomic minimum per column (null: the sorted keys go to keys_out)
+  int op64;
+  int64_t n_cols;
+  uint32_t conj_mask;       // xor into the high word of 8-byte values (complex64 conj)
+};
+
+// Keys of a wave sub-tile: `cnt` entries from `base` (kind 1: 8-byte
+// column indices below 2^32; otherwise 4-byte keys); one per-lane base
+// pointer, the chunks at immediate offsets from it.
+__device__ inline void wg_load_keys(const void* keys, int kind, int64_t base, int cnt, int lane,
+                                    uint32_t (&key)[kWgChunks]) {
+  if (kind == 1) {
+    const int64_t* p = static_cast<const int64_t*>(keys) + base + lane;
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) key[ch] = ch * 64 + lane < cnt ? (uint32_t)p[ch * 64] : 0u;
+  } else {
+    const uint32_t* p = static_cast<const uint32_t*>(keys) + base + lane;
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) key[ch] = ch * 64 + lane < cnt ? p[ch * 64] : 0u;
+  }
+}
+
+// Row of every entry of a wave sub-tile (rows r0..r1 touch it): each row
+// starting inside marks its first entry with r - r0, and a wave max-scan
+// carried across the chunks gives entry j the largest mark at or before j.
+template <class P>
+__device__ inline void wg_rows(const P* __restrict__ rowptr, int64_t r0, int64_t r1, int64_t base, int cnt,
+                               unsigned* s_mark, int lane, uint32_t (&row)[kWgChunks]) {
+  for (int j = lane; j < (int)kWgSub; j += 64) s_mark[j] = 0u;
+  wave_sync_t();
+  for (int64_t r = r0 + 1 + lane; r <= r1; r += 64) {
+    const int64_t st = (int64_t)rowptr[r];
+    // (st >= base on a valid row pointer; the test keeps a malformed one,
+    // which the caller's structure check reports, inside the tile's marks)
+    if (st >= base && st - base < cnt && (int64_t)rowptr[r + 1] > st) s_mark[st - base] = (unsigned)(r - r0);
+  }
+  wave_sync_t();
+  unsigned carry = 0u;
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch) {
+    const unsigned m = umax_(wave_max_scan(s_mark[ch * 64 + lane]), carry);
+    carry = (unsigned)__builtin_amdgcn_readlane((int)m, 63);
+    row[ch] = (uint32_t)(r0 + (int64_t)m);
+  }
+}
+
+// Row of the first entry of every wave sub-tile (binary search).
+template <class P>
+__global__ __launch_bounds__(256) void wg_tile_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                                           int64_t n_sub, int64_t* __restrict__ tile_row) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_sub) return;
+  const int64_t e = t * kWgSub;
+  int64_t lo = 0, hi = n_rows - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)rowptr[mid + 1] <= e) lo = mid + 1;
+    else hi = mid;
+  }
+  tile_row[t] = lo;
+}
+
+// Per-tile digit counts, cnt[tile][nd] (nd = mask + 1 digits).
+__global__ __launch_bounds__(kWgThreads) void wg_count_kernel(const void* __restrict__ keys, int kind, int64_t n,
+                                                              int shift, unsigned mask,
+                                                              uint32_t* __restrict__ counts) {
+  __shared__ unsigned s_hist[kWgMaxDigits];
+  const int nd = (int)mask + 1;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t tile = blockIdx.x;
+  for (int d = threadIdx.x; d < nd; d += kWgThreads) s_hist[d] = 0;
+  __syncthreads();
+  const int64_t base = tile * kWgTile + (int64_t)w * kWgSub;
+  const int cnt = n - base >= kWgSub ? (int)kWgSub : (n - base > 0 ? (int)(n - base) : 0);
+  uint32_t key[kWgChunks];
+  wg_load_keys(keys, kind, base, cnt, lane, key);
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch)
+    if (ch * 64 + lane < cnt) atomicAdd(&s_hist[(key[ch] >> shift) & mask], 1u);
+  __syncthreads();
+  for (int d = threadIdx.x; d < nd; d += kWgThreads) counts[tile * nd + d] = s_hist[d];
+}
+
+// Exclusive scan of cnt[tile][d] in (digit, tile) order (nd digits, up to
+// kWgMaxDigits): per-block digit sums over kWgScanTiles tiles, one
+// workgroup per digit scanning its block sums, then the downsweep.
+__global__ __launch_bounds__(256) void wg_scan_reduce_kernel(const uint32_t* __restrict__ cnt, int64_t n_tiles,
+                                                             int nd, uint32_t* __restrict__ partial) {
+  const int64_t s0 = (int64_t)blockIdx.x * kWgScanTiles;
+  const int64_t s1 = s0 + kWgScanTiles < n_tiles ? s0 + kWgScanTiles : n_tiles;
+  for (int d = threadIdx.x; d < nd; d += 256) {
+    uint32_t sum = 0;
+    for (int64_t s = s0; s < s1; s += kScanBatch) {
+      uint32_t v[kScanBatch];
+#pragma unroll
+      for (int k = 0; k < kScanBatch; ++k) v[k] = s + k < s1 ? cnt[(s + k) * nd + d] : 0u;
+#pragma unroll
+      for (int k = 0; k < kScanBatch; ++k) sum += v[k];
+    }
+    partial[(int64_t)blockIdx.x * nd + d] = sum;
+  }
+}
+
+__global__ __launch_bounds__(256) void wg_scan_column_kernel(uint32_t* __restrict__ partial, int64_t n_blocks, int nd,
+                                                             uint32_t* __restrict__ totals) {
+  __shared__ int64_t s_wave[4];
+  const int d = blockIdx.x;
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < n_blocks; b0 += 256) {
+    const int64_t b = b0 + threadIdx.x;
+    const int64_t v = b < n_blocks ? (int64_t)partial[b * nd + d] : 0;
+    int64_t sum;
+    const int64_t ex = block_exclusive_scan(v, s_wave, sum);
+    if (b < n_blocks) partial[b * nd + d] = (uint32_t)(carry + ex);
+    carry += sum;
+  }
+  if (threadIdx.x == 0) totals[d] = (uint32_t)carry;
+}
+
+__global__ __launch_bounds__(256) void wg_scan_down_kernel(uint32_t* __restrict__ cnt, int64_t n_tiles, int nd,
+                                                           const uint32_t* __restrict__ partial,
+                                                           const uint32_t* __restrict__ totals) {
+  __shared__ int64_t s_wave[4];
+  __shared__ uint32_t s_base[kWgMaxDigits];
+  // digit starts: thread t scans digits [t q, t q + q)
+  const int q = (nd + 255) / 256;
+  const int d0 = threadIdx.x * q;
+  int64_t mine = 0;
+  for (int j = 0; j < q; ++j)
+    if (d0 + j < nd) mine += totals[d0 + j];
+  int64_t all;
+  int64_t run = block_exclusive_scan(mine, s_wave, all);
+  for (int j = 0; j < q; ++j)
+    if (d0 + j < nd) {
+      s_base[d0 + j] = (uint32_t)run;
+      run += totals[d0 + j];
+    }
+  __syncthreads();
+  const int64_t s0 = (int64_t)blockIdx.x * kWgScanTiles;
+  const int64_t s1 = s0 + kWgScanTiles < n_tiles ? s0 + kWgScanTiles : n_tiles;
+  for (int d = threadIdx.x; d < nd; d += 256) {
+    uint32_t r = s_base[d] + partial[(int64_t)blockIdx.x * nd + d];
+    for (int64_t s = s0; s < s1; s += kScanBatch) {
+      uint32_t v[kScanBatch];
+#pragma unroll
+      for (int k = 0; k < kScanBatch; ++k) v[k] = s + k < s1 ? cnt[(s + k) * nd + d] : 0u;
+#pragma unroll
+      for (int k = 0; k < kScanBatch; ++k) {
+        if (s + k < s1) cnt[(s + k) * nd + d] = r;
+        r += v[k];
+      }
+    }
+  }
+}
+
+// Stable scatter of one workgroup-tile pass (see above).  Steps: keys and
+// payload into registers; per wave, ranks within the digit against the
+// wave's LDS counters (16-bit, two digits per word); per digit, the waves'
+// counts turned into wave bases plus the tile's digit start (one scan over
+// the digits); the keys through a digit-sorted LDS copy, out as contiguous
+// runs (or, in the last pass, the column starts to colptr); the payload
+// through the same buffer in windows.
+template <int VW, int MODE>
+__global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel(
+    const void* __restrict__ keys_in, int kind, const typename WgPay<VW>::T* __restrict__ pay_in, int64_t n, int shift,
+    unsigned mask, const uint32_t* __restrict__ offsets, uint32_t* __restrict__ keys_out,
+    typename WgPay<VW>::T* __restrict__ pay_out, WgIO io) {
+  using Pay = typename WgPay<VW>::T;
+  constexpr bool kFirst = MODE == kScatterFirst || MODE == kScatterOnly;
+  constexpr bool kLast = MODE == kScatterLast || MODE == kScatterOnly;
+  constexpr int kWords = kWgMaxDigits / 2;  // counter words per wave
+  __shared__ __attribute__((aligned(16))) uint8_t s_buf[kWgBufBytes];
+  __shared__ uint32_t s_off[kWgMaxDigits];
+  __shared__ uint16_t s_dig[kWgTile];
+  __shared__ int64_t s_wave[kWgWaves];
+  const int nd = (int)mask + 1;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int w = t >> 6;
+  const int64_t tile = blockIdx.x;
+  const int64_t tbase = tile * kWgTile;
+  const int tcnt = n - tbase < kWgTile ? (int)(n - tbase) : (int)kWgTile;
+  const int64_t base = tbase + (int64_t)w * kWgSub;
+  const int cnt = n - base >= kWgSub ? (int)kWgSub : (n - base > 0 ? (int)(n - base) : 0);
+  uint32_t key[kWgChunks];
+  Pay pay[kWgChunks];
+  wg_load_keys(keys_in, kind, base, cnt, lane, key);
+  if constexpr (kFirst) {
+    if constexpr (VW == 1) {
+      const uint32_t* vp = static_cast<const uint32_t*>(io.vals) + base + lane;
+#pragma unroll
+      for (int ch = 0; ch < kWgChunks; ++ch) pay[ch] = (uint64_t)(ch * 64 + lane < cnt ? vp[ch * 64] : 0u);
+    } else {
+      const uint2* vp = static_cast<const uint2*>(io.vals) + base + lane;
+#pragma unroll
+      for (int ch = 0; ch < kWgChunks; ++ch) {
+        const uint2 v = ch * 64 + lane < cnt ? vp[ch * 64] : make_uint2(0u, 0u);
+        pay[ch].v0 = v.x;
+        pay[ch].v1 = v.y;
+      }
+    }
+    uint32_t row[kWgChunks];
+    if (cnt > 0) {
+      const int64_t sub = tile * kWgWaves + w;
+      const int64_t r0 = io.tile_row[sub];
+      const int64_t r1 = sub + 1 < io.n_sub ? io.tile_row[sub + 1] : io.n_rows - 1;
+      unsigned* s_mark = reinterpret_cast<unsigned*>(s_buf) + w * kWgSub;
+      if (io.ptr64)
+        wg_rows<int64_t>(static_cast<const int64_t*>(io.rowptr), r0, r1, base, cnt, s_mark, lane, row);
+      else
+        wg_rows<int32_t>(static_cast<const int32_t*>(io.rowptr), r0, r1, base, cnt, s_mark, lane, row);
+    } else {
+#pragma unroll
+      for (int ch = 0; ch < kWgChunks; ++ch) row[ch] = 0u;
+    }
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) {
+      if constexpr (VW == 1) pay[ch] |= (uint64_t)row[ch] << 32;
+      else pay[ch].r = row[ch];
+    }
+    // every wave is done with its row marks before any wave's counters
+    // (which need not cover the same bytes) are written over them
+    __syncthreads();
+  } else {
+    const Pay* pp = pay_in + base + lane;
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) pay[ch] = ch * 64 + lane < cnt ? pp[ch * 64] : Pay{};
+  }
+  // ranks within the wave's digits, against wave w's own counters
+  uint32_t* wc = reinterpret_cast<uint32_t*>(s_buf);
+  uint32_t* my = wc + w * kWords;
+  for (int j = lane; j < (nd + 1) / 2; j += 64) my[j] = 0u;
+  wave_sync_t();
+  unsigned local[kWgChunks];
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch) {
+    const bool valid = ch * 64 + lane < cnt;
+    const uint64_t active = __ballot(valid);
+    const unsigned digit = (key[ch] >> shift) & mask;
+    uint64_t peers = active;
+#pragma unroll
+    for (int b = 0; b < kWgMaxBits; ++b) {
+      if (!((mask >> b) & 1u)) break;
+      const bool bit = (digit >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = count_below_t(peers);
+    const unsigned half = (digit & 1u) * 16u;
+    unsigned old = 0;
+    if (valid && rank == 0) old = atomicAdd(&my[digit >> 1], (unsigned)__popcll(peers) << half) >> half;
+    const int leader = peers ? (int)__builtin_ctzll(peers) : lane;
+    old = (unsigned)__builtin_amdgcn_ds_bpermute(leader << 2, (int)(old & 0xffffu));
+    local[ch] = old + (unsigned)rank;
+  }
+  __syncthreads();
+  // per digit pair: wave bases, then the tile's digit starts (thread t owns
+  // digits [t q, t q + q), q even, so both halves of a counter word)
+  {
+    const int q = nd > 2 * kWgThreads ? 2 * ((nd + 2 * kWgThreads - 1) / (2 * kWgThreads)) : 2;
+    const int d0 = t * q;
+    constexpr int kQMax = 2 * ((kWgMaxDigits + 2 * kWgThreads - 1) / (2 * kWgThreads));
+    uint32_t sums[kQMax];
+    int64_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < kQMax; j += 2) {
+      sums[j] = sums[j + 1] = 0u;
+      const int d = d0 + j;
+      if (j < q && d < nd) {
+        uint32_t pre = 0u;  // two 16-bit prefixes
+#pragma unroll
+        for (int v = 0; v < kWgWaves; ++v) {
+          const uint32_t c = wc[v * kWords + (d >> 1)];
+          wc[v * kWords + (d >> 1)] = pre;
+          pre += c;
+        }
+        sums[j] = pre & 0xffffu;
+        sums[j + 1] = pre >> 16;
+        mine += sums[j] + sums[j + 1];
+      }
+    }
+    int64_t all;
+    uint32_t run = (uint32_t)block_exclusive_scan(mine, s_wave, all);
+#pragma unroll
+    for (int j = 0; j < kQMax; j += 2) {
+      const int d = d0 + j;
+      if (j < q && d < nd) {
+        const uint32_t st0 = run, st1 = run + sums[j];
+        const uint32_t add = st0 | (st1 << 16);  // starts < kWgTile < 2^16
+#pragma unroll
+        for (int v = 0; v < kWgWaves; ++v) wc[v * kWords + (d >> 1)] += add;
+        s_off[d] = offsets[tile * nd + d] - st0;
+        if (d + 1 < nd) s_off[d + 1] = offsets[tile * nd + d + 1] - st1;
+        run += sums[j] + sums[j + 1];
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch) {
+    const unsigned digit = (key[ch] >> shift) & mask;
+    local[ch] += (my[digit >> 1] >> ((digit & 1u) * 16u)) & 0xffffu;
+  }
+  __syncthreads();
+  // keys (and digits) into the digit-sorted copy
+  uint32_t* s_key = reinterpret_cast<uint32_t*>(s_buf);
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch) {
+    if (ch * 64 + lane < cnt) {
+      s_key[local[ch]] = key[ch];
+      s_dig[local[ch]] = (uint16_t)((key[ch] >> shift) & mask);
+    }
+  }
+  __syncthreads();
+  if (!kLast || io.colptr == nullptr) {
+    for (int i = t; i < tcnt; i += kWgThreads) keys_out[s_off[s_dig[i]] + (uint32_t)i] = s_key[i];
+  } else {
+    // the first entry of each column in the tile: its position is a
+    // candidate for the column's start (the smallest over tiles wins)
+    for (int i = t; i < tcnt; i += kWgThreads) {
+      const uint32_t k = s_key[i];
+      if ((i == 0 || s_key[i - 1] != k) && (int64_t)k < io.n_cols) {
+        const uint32_t dst = s_off[s_dig[i]] + (uint32_t)i;
+        if (io.op64)
+          __hip_atomic_fetch_min(static_cast<uint64_t*>(io.colptr) + k, (uint64_t)dst, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        else
+          __hip_atomic_fetch_min(static_cast<uint32_t*>(io.colptr) + k, dst, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  __syncthreads();
+  // the payload, in windows of the buffer
+  constexpr int kWin = kWgBufBytes / (int)sizeof(Pay);
+  Pay* s_pay = reinterpret_cast<Pay*>(s_buf);
+  for (int w0 = 0; w0 < tcnt; w0 += kWin) {
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) {
+      const unsigned j = local[ch] - (unsigned)w0;
+      if (ch * 64 + lane < cnt && j < (unsigned)kWin) s_pay[j] = pay[ch];
+    }
+    __syncthreads();
+    const int w1 = w0 + kWin < tcnt ? w0 + kWin : tcnt;
+    for (int i = w0 + t; i < w1; i += kWgThreads) {
+      const uint32_t dst = s_off[s_dig[i]] + (uint32_t)i;
+      const Pay v = s_pay[i - w0];
+      if constexpr (kLast) {
+        uint32_t r;
+        if constexpr (VW == 1) {
+          static_cast<uint32_t*>(io.t_vals)[dst] = (uint32_t)v;
+          r = (uint32_t)(v >> 32);
+        } else {
+          static_cast<uint2*>(io.t_vals)[dst] = make_uint2(v.v0, v.v1 ^ io.conj_mask);
+          r = v.r;
+        }
+        if (io.oi64) static_cast<int64_t*>(io.t_cols)[dst] = (int64_t)r;
+        else static_cast<int32_t*>(io.t_cols)[dst] = (int32_t)r;
+      } else {
+        pay_out[dst] = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// colptr[c] = min(colptr[c], colptr[c + 1], ...): block minima, then every
+// block's suffix minimum with the minimum of the blocks after it.
+constexpr int kMinItems = 16;
+constexpr int64_t kMinTile = 256 * kMinItems;
+
+template <class OP>
+__global__ __launch_bounds__(256) void suffix_min_reduce_kernel(const OP* __restrict__ p, int64_t n,
+                                                                OP* __restrict__ bmin) {
+  __shared__ OP s[256];
+  const int64_t b0 = (int64_t)blockIdx.x * kMinTile;
+  OP m = p[b0 < n ? b0 : n - 1];
+  for (int k = 0; k < kMinItems; ++k) {
+    const int64_t i = b0 + (int64_t)k * 256 + threadIdx.x;
+    if (i < n && p[i] < m) m = p[i];
+  }
+  s[threadIdx.x] = m;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off && s[threadIdx.x + off] < s[threadIdx.x]) s[threadIdx.x] = s[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) bmin[blockIdx.x] = s[0];
+}
+
+template <class OP>
+__global__ __launch_bounds__(256) void suffix_min_down_kernel(OP* __restrict__ p, int64_t n,
+                                                              const OP* __restrict__ bmin, int64_t n_blocks) {
+  __shared__ OP s[256];
+  // the minimum over the blocks after this one (the last entry, nnz, bounds all)
+  OP carry = p[n - 1];
+  for (int64_t b = (int64_t)blockIdx.x + 1 + threadIdx.x; b < n_blocks; b += 256)
+    if (bmin[b] < carry) carry = bmin[b];
+  s[threadIdx.x] = carry;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off && s[threadIdx.x + off] < s[threadIdx.x]) s[threadIdx.x] = s[threadIdx.x + off];
+    __syncthreads();
+  }
+  carry = s[0];
+  __syncthreads();
+  // thread t owns kMinItems consecutive entries: its own suffix minima, then
+  // the minimum over the threads after it
+  const int64_t i0 = (int64_t)blockIdx.x * kMinTile + (int64_t)threadIdx.x * kMinItems;
+  OP v[kMinItems];
+  OP m = carry;
+  for (int k = kMinItems - 1; k >= 0; --k) {
+    const int64_t i = i0 + k;
+    v[k] = i < n ? p[i] : carry;
+    if (v[k] < m) m = v[k];
+  }
+  s[threadIdx.x] = m;  // this thread's minimum (with the carry)
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const OP o = (int)threadIdx.x + off < 256 ? s[threadIdx.x + off] : carry;
+    __syncthreads();
+    if (o < s[threadIdx.x]) s[threadIdx.x] = o;
+    __syncthreads();
+  }
+  OP after = (int)threadIdx.x + 1 < 256 ? s[threadIdx.x + 1] : carry;
+  for (int k = kMinItems - 1; k >= 0; --k) {
+    const int64_t i = i0 + k;
+    if (v[k] < after) after = v[k];
+    if (i < n) p[i] = after;
+  }
+}
+
 // ---- host side ----
 struct Layout {
   size_t key_bytes, pos_bytes, rowid_bytes;
@@ -894,6 +1396,170 @@ inline bool transpose_pack16_enabled() {
 inline bool transpose_payload_enabled() {
   const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_PAYLOAD");
   return !(e && std::atoi(e) == 0);
+}
+
+// ---- the workgroup-tile transpose (4- and 8-byte values) ----
+struct WgLayout {
+  int64_t n_tiles = 0, n_sub = 0, n_blocks = 0, n_min_blocks = 0;
+  size_t off_keys_a = 0, off_keys_b = 0, off_pay_a = 0, off_pay_b = 0, off_counts = 0, off_partial = 0,
+         off_totals = 0, off_tile_row = 0, off_bmin = 0, total = 0;
+};
+
+WgLayout make_wg_layout(int64_t n_cols, int64_t nnz) {
+  WgLayout L;
+  L.n_tiles = ceil_div(nnz, kWgTile);
+  L.n_sub = ceil_div(nnz, kWgSub);
+  L.n_blocks = ceil_div(L.n_tiles, kWgScanTiles);
+  L.n_min_blocks = ceil_div(n_cols + 1, kMinTile);
+  size_t o = 0;
+  L.off_keys_a = o; o = align256(o + 4 * (size_t)nnz);
+  L.off_keys_b = o; o = align256(o + 4 * (size_t)nnz);
+  L.off_pay_a = o; o = align256(o + sizeof(Pay12) * (size_t)nnz);
+  L.off_pay_b = o; o = align256(o + sizeof(Pay12) * (size_t)nnz);
+  L.off_counts = o; o = align256(o + 4 * (size_t)L.n_tiles * kWgMaxDigits);
+  L.off_partial = o; o = align256(o + 4 * (size_t)L.n_blocks * kWgMaxDigits);
+  L.off_totals = o; o = align256(o + 4 * (size_t)kWgMaxDigits);
+  L.off_tile_row = o; o = align256(o + 8 * (size_t)L.n_sub);
+  L.off_bmin = o; o = align256(o + 8 * (size_t)L.n_min_blocks);
+  L.total = o;
+  return L;
+}
+
+// The workgroup-tile path takes 4- and 8-byte values with positions, rows
+// and columns below 2^32; FLAGSPARSE_TRANSPOSE_WG=0 keeps the wave-tile
+// passes (A/B).
+inline bool transpose_wg_applies(int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz) {
+  if (const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_WG"))
+    if (std::atoi(e) == 0) return false;
+  const int64_t lim = (int64_t)0xffffffffLL;
+  return val_t != FS_C128 && nnz > 0 && nnz < lim && n_rows <= lim && n_cols <= lim + 1;
+}
+
+template <class OP>
+int colptr_suffix_min(OP* colptr, int64_t n, OP* bmin, int64_t n_blocks, hipStream_t s) {
+  hipLaunchKernelGGL((suffix_min_reduce_kernel<OP>), dim3((unsigned)n_blocks), dim3(256), 0, s, colptr, n, bmin);
+  FS_CHECK_LAUNCH("suffix_min_reduce_kernel");
+  hipLaunchKernelGGL((suffix_min_down_kernel<OP>), dim3((unsigned)n_blocks), dim3(256), 0, s, colptr, n, bmin,
+                     n_blocks);
+  FS_CHECK_LAUNCH("suffix_min_down_kernel");
+  return FS_OK;
+}
+
+template <int VW>
+int wg_launch_scatter(int mode, dim3 g, hipStream_t s, const void* kin, int kind, const void* pin, int64_t nnz,
+                      int shift, unsigned mask, const uint32_t* counts, uint32_t* kout, void* pout,
+                      const WgIO& io) {
+  using Pay = typename WgPay<VW>::T;
+  const Pay* pi = static_cast<const Pay*>(pin);
+  Pay* po = static_cast<Pay*>(pout);
+  switch (mode) {
+    case kScatterFirst:
+      hipLaunchKernelGGL((wg_scatter_kernel<VW, kScatterFirst>), g, dim3(kWgThreads), 0, s, kin, kind, pi, nnz, shift,
+                         mask, counts, kout, po, io);
+      break;
+    case kScatterLast:
+      hipLaunchKernelGGL((wg_scatter_kernel<VW, kScatterLast>), g, dim3(kWgThreads), 0, s, kin, kind, pi, nnz, shift,
+                         mask, counts, kout, po, io);
+      break;
+    case kScatterOnly:
+      hipLaunchKernelGGL((wg_scatter_kernel<VW, kScatterOnly>), g, dim3(kWgThreads), 0, s, kin, kind, pi, nnz, shift,
+                         mask, counts, kout, po, io);
+      break;
+    default:
+      hipLaunchKernelGGL((wg_scatter_kernel<VW, kScatterPlain>), g, dim3(kWgThreads), 0, s, kin, kind, pi, nnz, shift,
+                         mask, counts, kout, po, io);
+  }
+  FS_CHECK_LAUNCH("wg_scatter_kernel");
+  return FS_OK;
+}
+
+int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, int64_t n_rows, int64_t n_cols,
+                 int64_t nnz, const void* vals, const void* cols, const void* indptr, int conj, void* t_vals,
+                 void* t_cols, void* t_indptr, hipStream_t s) {
+  const WgLayout L = make_wg_layout(n_cols, nnz);
+  const int vw = val_t == FS_F32 ? 1 : 2;
+  int64_t* tile_row = reinterpret_cast<int64_t*>(ws + L.off_tile_row);
+  if (ptr_t == FS_I32)
+    hipLaunchKernelGGL((wg_tile_rows_kernel<int32_t>), dim3((unsigned)ceil_div(L.n_sub, 256)), dim3(256), 0, s,
+                       static_cast<const int32_t*>(indptr), n_rows, L.n_sub, tile_row);
+  else
+    hipLaunchKernelGGL((wg_tile_rows_kernel<int64_t>), dim3((unsigned)ceil_div(L.n_sub, 256)), dim3(256), 0, s,
+                       static_cast<const int64_t*>(indptr), n_rows, L.n_sub, tile_row);
+  FS_CHECK_LAUNCH("wg_tile_rows_kernel");
+  const int64_t n_ptr = n_cols + 1;
+  const char* cp = std::getenv("FLAGSPARSE_TRANSPOSE_COLPTR");
+  const bool by_keys = cp && std::string(cp) == "keys";
+  if (!by_keys) {
+    if (op_t == FS_I32)
+      hipLaunchKernelGGL((fill_kernel<int32_t>), dim3((unsigned)ceil_div(n_ptr, 256)), dim3(256), 0, s,
+                         static_cast<int32_t*>(t_indptr), n_ptr, (int32_t)nnz);
+    else
+      hipLaunchKernelGGL((fill_kernel<int64_t>), dim3((unsigned)ceil_div(n_ptr, 256)), dim3(256), 0, s,
+                         static_cast<int64_t*>(t_indptr), n_ptr, (int64_t)nnz);
+    FS_CHECK_LAUNCH("fill_kernel");
+  }
+  WgIO io{vals,   indptr, ptr_t == FS_I64 ? 1 : 0, tile_row, n_rows, L.n_sub, t_vals, t_cols,
+          oi_t == FS_I64 ? 1 : 0, by_keys ? nullptr : t_indptr, op_t == FS_I64 ? 1 : 0, n_cols,
+          (conj && val_t == FS_C64) ? 0x80000000u : 0u};
+  uint32_t* counts = reinterpret_cast<uint32_t*>(ws + L.off_counts);
+  uint32_t* partial = reinterpret_cast<uint32_t*>(ws + L.off_partial);
+  uint32_t* totals = reinterpret_cast<uint32_t*>(ws + L.off_totals);
+  uint32_t* ka = reinterpret_cast<uint32_t*>(ws + L.off_keys_a);
+  uint32_t* kb = reinterpret_cast<uint32_t*>(ws + L.off_keys_b);
+  void* pa = ws + L.off_pay_a;
+  void* pb = ws + L.off_pay_b;
+  const int bits = key_bits(n_cols);
+  const int passes = bits == 0 ? 1 : (bits + kWgMaxBits - 1) / kWgMaxBits;
+  const void* kin = cols;  // the CSR columns, then the keys of the previous pass
+  int kind = idx_t == FS_I32 ? 0 : 1;
+  const void* pin = nullptr;
+  uint32_t* kout = ka;
+  void* pout = pa;
+  const dim3 g((unsigned)L.n_tiles);
+  int shift = 0;
+  for (int p = 0; p < passes; ++p) {
+    // the key bits split evenly over the passes (longer runs per digit)
+    const int pbits = (bits - shift + (passes - p) - 1) / (passes - p);
+    const unsigned mask = (1u << pbits) - 1u;
+    const int nd = (int)mask + 1;
+    hipLaunchKernelGGL(wg_count_kernel, g, dim3(kWgThreads), 0, s, kin, kind, nnz, shift, mask, counts);
+    FS_CHECK_LAUNCH("wg_count_kernel");
+    hipLaunchKernelGGL(wg_scan_reduce_kernel, dim3((unsigned)L.n_blocks), dim3(256), 0, s, counts, L.n_tiles, nd,
+                       partial);
+    FS_CHECK_LAUNCH("wg_scan_reduce_kernel");
+    hipLaunchKernelGGL(wg_scan_column_kernel, dim3((unsigned)nd), dim3(256), 0, s, partial, L.n_blocks, nd, totals);
+    FS_CHECK_LAUNCH("wg_scan_column_kernel");
+    hipLaunchKernelGGL(wg_scan_down_kernel, dim3((unsigned)L.n_blocks), dim3(256), 0, s, counts, L.n_tiles, nd,
+                       partial, totals);
+    FS_CHECK_LAUNCH("wg_scan_down_kernel");
+    const int mode = passes == 1 ? kScatterOnly : p == 0 ? kScatterFirst : p == passes - 1 ? kScatterLast
+                                                                                            : kScatterPlain;
+    const int rc = vw == 1 ? wg_launch_scatter<1>(mode, g, s, kin, kind, pin, nnz, shift, mask, counts, kout, pout, io)
+                           : wg_launch_scatter<2>(mode, g, s, kin, kind, pin, nnz, shift, mask, counts, kout, pout, io);
+    if (rc != FS_OK) return rc;
+    shift += pbits;
+    kin = kout;
+    kind = 2;
+    pin = pout;
+    kout = kout == ka ? kb : ka;
+    pout = pout == pa ? pb : pa;
+  }
+  if (by_keys) {
+    const unsigned blocks = (unsigned)ceil_div(ceil_div(nnz + 1, 4), 256);
+    if (op_t == FS_I32)
+      hipLaunchKernelGGL((colptr_kernel<uint32_t, int32_t>), dim3(blocks), dim3(256), 0, s,
+                         static_cast<const uint32_t*>(kin), nnz, n_cols, static_cast<int32_t*>(t_indptr));
+    else
+      hipLaunchKernelGGL((colptr_kernel<uint32_t, int64_t>), dim3(blocks), dim3(256), 0, s,
+                         static_cast<const uint32_t*>(kin), nnz, n_cols, static_cast<int64_t*>(t_indptr));
+    FS_CHECK_LAUNCH("colptr_kernel");
+    return FS_OK;
+  }
+  if (op_t == FS_I32)
+    return colptr_suffix_min<uint32_t>(static_cast<uint32_t*>(t_indptr), n_ptr,
+                                       reinterpret_cast<uint32_t*>(ws + L.off_bmin), L.n_min_blocks, s);
+  return colptr_suffix_min<uint64_t>(static_cast<uint64_t*>(t_indptr), n_ptr,
+                                     reinterpret_cast<uint64_t*>(ws + L.off_bmin), L.n_min_blocks, s);
 }
 
 template <class P>
@@ -1423,7 +2089,11 @@ using namespace fs;
 
 extern "C" size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t nnz) {
   if (nnz <= 0) return 0;
-  return make_layout(n_rows, n_cols, nnz, true).total;
+  return std::max(make_layout(n_rows, n_cols, nnz, true).total, make_wg_layout(n_cols, nnz).total);
+}
+
+extern "C" int fs_csr_transpose_bounded(int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz) {
+  return transpose_wg_applies(val_t, n_rows, n_cols, nnz) ? 1 : 0;
 }
 
 extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, int out_ptr_t, int64_t n_rows,
@@ -1448,6 +2118,12 @@ extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, 
   }
   if (!vals || !cols || !indptr || !t_vals || !t_cols) return fail(FS_E_INVALID, "fs_csr_transpose: null pointer");
   if (n_rows == 0 || n_cols == 0) return fail(FS_E_INVALID, "fs_csr_transpose: nnz > 0 with an empty dimension");
+  if (transpose_wg_applies(val_t, n_rows, n_cols, nnz)) {
+    if (!ws || ws_bytes < make_wg_layout(n_cols, nnz).total)
+      return fail(FS_E_WORKSPACE, "fs_csr_transpose: workspace too small");
+    return transpose_wg(static_cast<char*>(ws), val_t, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz, vals,
+                        cols, indptr, conj, t_vals, t_cols, t_indptr, stream);
+  }
   const Layout L = make_layout(n_rows, n_cols, nnz, transpose_payload_enabled());
   if (!ws || ws_bytes < L.total) return fail(FS_E_WORKSPACE, "fs_csr_transpose: workspace too small");
   char* w = static_cast<char*>(ws);

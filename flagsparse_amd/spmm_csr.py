@@ -30,7 +30,7 @@ from ._common import (
     _tolerance_for_dtype,
 )
 from ._csr import CsrPlan, analyze_csr, transpose_csr
-from .spmv_csr import _build_sell, _check_structure, _sell_codes_possible, _spmv_sell_locality
+from .spmv_csr import _PendingCheck, _build_sell, _check_structure, _sell_codes_possible, _spmv_sell_locality
 
 SUPPORTED_SPMM_VALUE_DTYPES = SUPPORTED_VALUE_DTYPES
 
@@ -136,12 +136,16 @@ _SPMM_STRUCT_MESSAGES = {
 }
 
 
-def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False):
+def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False, defer=False):
     """Validation of spmm_csr.py:239-297 (same order, types and messages).
 
     The HIP kernels take int32 and int64 column indices / row pointers
     natively, so the matrix is kept in its own index dtypes (the reference
     narrows indices to int32 and widens indptr to int64 for Triton).
+    The last element returned is the row-length plan (analyze=True), or,
+    with defer=True and a transpose that stays in bounds on any structure
+    (fs_csr_transpose_bounded), a _PendingCheck whose finish() raises the
+    structure errors later; otherwise None.
     """
     if len(shape) != 2:
         raise ValueError("shape must be a 2-tuple: (n_rows, n_cols)")
@@ -170,12 +174,29 @@ def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False):
     data = data.contiguous()
     indices = indices.contiguous()
     indptr = indptr.contiguous()
+    if defer and nnz > 0 and _lib.lib().fs_csr_transpose_bounded(
+            _lib.value_code(_compute_dtype(data.dtype)), n_rows, n_cols, nnz):
+        return data, indices, indptr, n_rows, n_cols, _PendingCheck(data, indices, indptr, n_cols, messages)
     if analyze:
         # the row statistics ride on the structure check's round trip
         _, csr = _check_structure(data, indices, indptr, n_cols, messages, analyze=True)
         return data, indices, indptr, n_rows, n_cols, csr
     _check_structure(data, indices, indptr, n_cols, messages)
     return data, indices, indptr, n_rows, n_cols, None
+
+
+def _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending):
+    """op(A) @ B for A^T / A^H queued behind a pending structure check; the
+    check is finished (and raises) before C is returned."""
+    data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code)
+    n_rows, n_cols = int(shape[0]), int(shape[1])
+    plan = None
+    if n_rows > 0:
+        plan = _SpmmPlan(data, indices, indptr, n_rows, n_cols,
+                         csr=CsrPlan.from_sizes(data, indices, indptr, n_rows, n_cols))
+    C = _hip_spmm(data, indices, indptr, B, n_rows, plan, data.dtype)
+    pending.finish()
+    return C
 
 
 def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code):
@@ -402,30 +423,47 @@ def flagsparse_spmm_csr(
     if max_segments is not None and max_segments <= 0:
         raise ValueError("max_segments must be positive when provided")
 
-    data, indices, indptr, n_rows, n_cols, csr0 = _prepare_spmm_csr_matrix(
-        data, indices, indptr, shape, analyze=not _spmm_op_transposes(op_code))
-    if B.ndim != 2:
-        raise ValueError("B must be a 2D dense tensor")
-    eff_rows, eff_cols = (n_cols, n_rows) if _spmm_op_transposes(op_code) else (n_rows, n_cols)
-    if B.shape[0] != eff_cols:
-        raise ValueError(f"B.shape[0] must be n_cols={eff_cols}, got {B.shape[0]}")
-    if not B.is_cuda:
-        raise ValueError("B must be a CUDA tensor")
-    if B.device != data.device:
-        raise ValueError("B must be on the same CUDA device as the sparse matrix")
-    if B.dtype != data.dtype:
-        raise TypeError("B dtype must match data dtype")
-    B = B.contiguous()
-    n_dense = int(B.shape[1])
-    if out is not None:
-        if not out.is_cuda:
-            raise ValueError("out must be a CUDA tensor")
-        if out.device != data.device:
-            raise ValueError("out must be on the same CUDA device as the inputs")
-        if out.shape != (eff_rows, n_dense) or out.dtype != data.dtype:
-            raise ValueError("out shape/dtype must match result")
-
     do_timing = bool(return_time or return_meta)
+    # A^T / A^H into a fresh C: the structure check's answer is read after
+    # the transpose and the SpMM are queued behind it (one synchronisation at
+    # the end instead of a round trip in between); the reference's error, if
+    # any, is raised before C is returned, and before any argument error
+    # that the reference raises after its check.
+    transposes = _spmm_op_transposes(op_code)
+    defer = transposes and out is None and not do_timing and max_segments is None
+    data, indices, indptr, n_rows, n_cols, csr0 = _prepare_spmm_csr_matrix(
+        data, indices, indptr, shape, analyze=not transposes, defer=defer)
+    pending = csr0 if isinstance(csr0, _PendingCheck) else None
+    if pending is not None:
+        csr0 = None
+    try:
+        if B.ndim != 2:
+            raise ValueError("B must be a 2D dense tensor")
+        eff_rows, eff_cols = (n_cols, n_rows) if transposes else (n_rows, n_cols)
+        if B.shape[0] != eff_cols:
+            raise ValueError(f"B.shape[0] must be n_cols={eff_cols}, got {B.shape[0]}")
+        if not B.is_cuda:
+            raise ValueError("B must be a CUDA tensor")
+        if B.device != data.device:
+            raise ValueError("B must be on the same CUDA device as the sparse matrix")
+        if B.dtype != data.dtype:
+            raise TypeError("B dtype must match data dtype")
+        B = B.contiguous()
+        n_dense = int(B.shape[1])
+        if out is not None:
+            if not out.is_cuda:
+                raise ValueError("out must be a CUDA tensor")
+            if out.device != data.device:
+                raise ValueError("out must be on the same CUDA device as the inputs")
+            if out.shape != (eff_rows, n_dense) or out.dtype != data.dtype:
+                raise ValueError("out shape/dtype must match result")
+        if pending is not None:
+            return _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending)
+    except Exception:
+        if pending is not None:
+            pending.finish()  # the structure error comes first
+        raise
+
     symbolic_ms = compute_ms = op_total_ms = None
     if do_timing:
         torch.cuda.synchronize()

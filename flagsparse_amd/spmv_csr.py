@@ -690,18 +690,63 @@ def _check_structure(data, indices, indptr, n_cols, messages, analyze=False):
             ),
             "fs_csr_check",
         )
+    col_range = _raise_structure(vals, nnz, n_cols, messages)
+    return (col_range, plan) if analyze else col_range
+
+
+def _raise_structure(vals, nnz, n_cols, messages):
+    """The reference's structure errors, in its order, from the five check
+    values; the column range (lo, hi), or None when nnz == 0."""
     if vals[0] != 0:
         raise ValueError(messages["start"])
     if vals[1] != nnz:
         raise ValueError(messages["last"](vals[1]))
     if vals[2] != 0:
         raise ValueError(messages["monotone"])
-    col_range = None
     if nnz > 0:
         if vals[3] < 0 or vals[4] >= n_cols:
             raise IndexError("indices out of range for n_cols")
-        col_range = (vals[3], vals[4])
-    return (col_range, plan) if analyze else col_range
+        return (vals[3], vals[4])
+    return None
+
+
+_check_local = threading.local()
+
+
+class _PendingCheck:
+    """A structure check whose answer is read later (fs_csr_check_enqueue):
+    the check pass and the copy of its five words into this thread's pinned
+    buffer are queued on the stream; finish() synchronises the stream and
+    raises the reference's error, if any."""
+
+    __slots__ = ("words", "nnz", "n_cols", "messages", "stream", "_ws")
+
+    def __init__(self, data, indices, indptr, n_cols, messages):
+        words = getattr(_check_local, "words", None)
+        if words is None:
+            words = torch.zeros(5, dtype=torch.int64, pin_memory=True)
+            _check_local.words = words
+        self.words = words
+        self.nnz = data.numel()
+        self.n_cols = int(n_cols)
+        self.messages = messages
+        self.stream = torch.cuda.current_stream(indptr.device)
+        lib = _lib.lib()
+        self._ws = _lib.workspace(lib.fs_csr_check_bytes(), indptr.device)
+        _lib.check(
+            lib.fs_csr_check_enqueue(
+                _lib.ptr(indptr), _lib.index_code(indptr.dtype), _lib.ptr(indices) if self.nnz > 0 else None,
+                _lib.index_code(indices.dtype), indptr.numel() - 1, self.nnz, _lib.ptr(self._ws),
+                words.data_ptr(), _lib.stream_handle(indptr.device),
+            ),
+            "fs_csr_check_enqueue",
+        )
+
+    def finish(self):
+        self.stream.synchronize()
+        vals = (ctypes.c_int64 * 5)()
+        _lib.check(_lib.lib().fs_csr_check_decode(self.words.data_ptr(), self.nnz, vals), "fs_csr_check_decode")
+        return _raise_structure(vals, self.nnz, self.n_cols, self.messages)
 
 
 _SPMV_STRUCT_MESSAGES = {

@@ -126,6 +126,23 @@ int fs_csr_check(const void* indptr, int ptr_t, const void* indices, int idx_t,
                  hipStream_t stream);
 
 /*
+ * fs_csr_check without the round trip, for a caller that launches more work
+ * before it needs the answer: launches the check pass into `check_dev` and
+ * an asynchronous copy of its five result words (40 bytes) into
+ * `host_words`, which must be pinned host memory; returns without
+ * synchronising.  After the caller has synchronised `stream`,
+ * fs_csr_check_decode turns the words into fs_csr_check's five values.
+ * Used by flagsparse_spmm_csr with op="trans" / "conj" (the reference checks,
+ * spmm_csr.py:239-297, then transposes, :300-349): the transpose and the
+ * SpMM run behind the check, and the reference's error is raised before C is
+ * returned.
+ */
+int fs_csr_check_enqueue(const void* indptr, int ptr_t, const void* indices, int idx_t,
+                         int64_t n_rows, int64_t nnz, void* check_dev, void* host_words,
+                         hipStream_t stream);
+int fs_csr_check_decode(const void* host_words, int64_t nnz, int64_t* out);
+
+/*
  * fs_csr_check and fs_csr_analyze in one device round trip: both passes are
  * launched, then one read-back fills `out` (as fs_csr_check) and `plan` (as
  * fs_csr_analyze) and synchronises `stream`.  `ws` holds
@@ -287,6 +304,16 @@ int fs_spmm_csr_strided(const fs_csr_plan* plan, const void* vals, const void* c
  */
 size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_cols,
                                         int64_t nnz);
+/*
+ * 1 when fs_csr_transpose of a matrix of this value type and these sizes
+ * reads and writes only inside its arguments whatever the structure holds
+ * (a row pointer or column indices that the structure check would reject
+ * give a meaningless transpose, no out-of-bounds access), 0 otherwise.  The
+ * caller may then queue the transpose before it has the check's answer.
+ * No counterpart in the reference (its checks synchronise before the
+ * transpose, spmm_csr.py:239-297).
+ */
+int fs_csr_transpose_bounded(int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz);
 int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t,
                      int out_ptr_t, int64_t n_rows, int64_t n_cols,
                      int64_t nnz, const void* vals, const void* cols,

@@ -189,6 +189,51 @@ def test_spmm_api_contract(device):
     _check(ld, li, lp, lsh, S.dense(2048, 8, torch.float32, device), "non")
 
 
+@pytest.mark.parametrize("op", ["trans", "conj"])
+def test_spmm_transposed_structure_errors(device, op):
+    """A^T / A^H queue the transpose and the SpMM behind the structure check
+    and read its answer at the end: the reference's error and message still
+    come first (also before a B error the reference raises after its check),
+    and the next call is unaffected."""
+    dt = torch.complex64 if op == "conj" else torch.float32
+    data = torch.tensor([1.0, 2.0, 3.0], dtype=dt, device=device)
+    good_i = torch.tensor([0, 1, 1], dtype=torch.int32, device=device)
+    good_p = torch.tensor([0, 2, 3], dtype=torch.int64, device=device)
+    B = torch.randn((2, 4), dtype=torch.float32, device=device).to(dt)
+    bad_B = torch.randn((5, 4), dtype=torch.float32, device=device).to(dt)
+    f = fs.flagsparse_spmm_csr
+    cases = [
+        (good_i, torch.tensor([1, 2, 3], dtype=torch.int64, device=device), ValueError, "must be 0"),
+        (good_i, torch.tensor([0, 2, 2], dtype=torch.int64, device=device), ValueError, "nnz=3"),
+        (good_i, torch.tensor([0, 4, 3], dtype=torch.int64, device=device), ValueError, "nondecreasing"),
+        (torch.tensor([0, 3, 1], dtype=torch.int32, device=device), good_p, IndexError, "out of range"),
+        (torch.tensor([0, -1, 1], dtype=torch.int32, device=device), good_p, IndexError, "out of range"),
+    ]
+    for idx, ptr, exc, msg in cases:
+        for rhs in (B, bad_B):
+            with pytest.raises(exc, match=msg):
+                f(data, idx, ptr, rhs, (2, 2), op=op)
+        got = f(data, good_i, good_p, B, (2, 2), op=op)
+        _check(data, good_i, good_p, (2, 2), B, op)
+        assert got.shape == (2, 4)
+    # a valid structure with a wrong B still gets the B error
+    with pytest.raises(ValueError, match="B.shape"):
+        f(data, good_i, good_p, bad_B, (2, 2), op=op)
+
+
+@pytest.mark.parametrize("op", ["trans", "conj"])
+def test_spmm_transposed_deferred_matches_synchronous(device, op):
+    """The queued-behind-the-check path (fresh C) and the synchronous one
+    (out= given) give the same bits."""
+    dt = torch.complex64 if op == "conj" else torch.float32
+    d, i, p, sh = S.powerlaw(1 << 15, dt, torch.int32, device, seed=21)
+    B = S.dense(sh[0], 16, dt, device, seed=3)
+    a = fs.flagsparse_spmm_csr(d, i, p, B, sh, op=op)
+    out = torch.empty_like(a)
+    b = fs.flagsparse_spmm_csr(d, i, p, B, sh, op=op, out=out)
+    assert torch.equal(a, b)
+
+
 def test_spmm_op_validation_messages(device):
     d, i, p, sh = S.random_csr(8, 12, 0.3, torch.float32, torch.int32, device, seed=1)
     B_non = torch.randn(12, 4, device=device)

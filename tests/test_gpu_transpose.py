@@ -54,6 +54,33 @@ def test_transpose_multi_pass_keys(device):
     _check(d, i, p, sh, True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["float32", "float64", "complex64"])
+def test_transpose_three_wide_passes(device, dtype):
+    # more than 2^22 columns: three 11-bit passes of the workgroup-tile sort
+    d, i, p, sh = S.random_csr(3000, 9_000_000, 25.0 / 9_000_000, dtype, torch.int64, device, seed=11)
+    _check(d, i, p, sh, dtype == torch.complex64)
+
+
+@pytest.mark.parametrize("rows", [255, 256, 257, 512, 1023])
+def test_transpose_tile_boundaries(device, rows):
+    # 32 entries per row: nnz just below, at and above multiples of the
+    # 8192-entry workgroup tile (and of its 1024-entry wave sub-tiles)
+    d, i, p, sh = S.uniform_rows(rows, 5000, 32, torch.float32, torch.int32, device, seed=rows)
+    _check(d, i, p, sh, False)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.complex64], ids=["float32", "complex64"])
+def test_transpose_workgroup_path_matches_wave_path(device, monkeypatch, dtype):
+    # the workgroup-tile passes and the wave-tile passes give the same bits
+    d, i, p, sh = S.powerlaw(1 << 17, dtype, torch.int32, device, seed=9)
+    monkeypatch.setenv("FLAGSPARSE_TRANSPOSE_WG", "1")
+    a = _csr.transpose_csr(d, i, p, sh, conj=True)
+    monkeypatch.setenv("FLAGSPARSE_TRANSPOSE_WG", "0")
+    b = _csr.transpose_csr(d, i, p, sh, conj=True)
+    for x, y in zip(a[:3], b[:3]):
+        assert torch.equal(x, y)
+
+
 def test_transpose_empty(device):
     d = torch.empty(0, dtype=torch.float32, device=device)
     i = torch.empty(0, dtype=torch.int64, device=device)
