@@ -698,7 +698,7 @@ __global__ __launch_bounds__(256) void colptr_kernel(const K* __restrict__ keys,
   for (int w = 0; w < W; ++w) {
     const int64_t k = k0 + w;
     if (k > nnz) break;
-    const int64_t cur = k < nnz ? (int64_t)kv[w] : n_cols;
+    const int64_t cur = k < nnz ? ((int64_t)kv[w] < n_cols ? (int64_t)kv[w] : n_cols) : n_cols;
     for (int64_t c = prev + 1; c <= cur; ++c) colptr[c] = (OP)k;
     prev = cur;
   }
@@ -731,7 +731,7 @@ __global__ __launch_bounds__(256) void identity_kernel(const void* __restrict__ 
 // minimum of the first position of each column the tile holds, and a
 // suffix minimum over the columns (empty columns take the next one's start).
 #ifndef FS_WG_WAVES
-#define FS_WG_WAVES 16
+#define FS_WG_WAVES 8
 #endif
 #ifndef FS_WG_CHUNKS
 #define FS_WG_CHUNKS 12
@@ -832,20 +832,19 @@ __device__ inline void wg_rows(const P* __restrict__ rowptr, int64_t r0, int64_t
   }
 }
 
-// Row of the first entry of every wave sub-tile (binary search).
+// Row of the first entry of every wave sub-tile: thread r writes r for the
+// sub-tiles whose first entry lies in row r (one coalesced pass over the row
+// pointer instead of a binary search per sub-tile).  A malformed row pointer
+// can leave slots unwritten; the scatter clamps what it reads.
 template <class P>
 __global__ __launch_bounds__(256) void wg_tile_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows,
                                                            int64_t n_sub, int64_t* __restrict__ tile_row) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_sub) return;
-  const int64_t e = t * kWgSub;
-  int64_t lo = 0, hi = n_rows - 1;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if ((int64_t)rowptr[mid + 1] <= e) lo = mid + 1;
-    else hi = mid;
-  }
-  tile_row[t] = lo;
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  const int64_t a = (int64_t)rowptr[r], b = (int64_t)rowptr[r + 1];
+  int64_t sub = a <= 0 ? 0 : (a + kWgSub - 1) / kWgSub;
+  const int64_t end = b <= 0 ? 0 : ((b + kWgSub - 1) / kWgSub < n_sub ? (b + kWgSub - 1) / kWgSub : n_sub);
+  for (; sub < end; ++sub) tile_row[sub] = r;
 }
 
 // Per-tile digit counts, cnt[tile][nd] (nd = mask + 1 digits).
@@ -942,6 +941,12 @@ __global__ __launch_bounds__(256) void wg_scan_down_kernel(uint32_t* __restrict_
   }
 }
 
+__device__ inline int64_t xcd_tile(uint32_t b, uint32_t n) {
+  constexpr uint32_t kXcds = 8;
+  const uint32_t q = n / kXcds, r = n % kXcds, x = b % kXcds, i = b / kXcds;
+  return x < r ? (int64_t)x * (q + 1) + i : (int64_t)r * (q + 1) + (int64_t)(x - r) * q + i;
+}
+
 // Stable scatter of one workgroup-tile pass (see above).  Steps: keys and
 // payload into registers; per wave, ranks within the digit against the
 // wave's LDS counters (16-bit, two digits per word); per digit, the waves'
@@ -966,7 +971,12 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
-  const int64_t tile = blockIdx.x;
+  // Consecutive tiles on one XCD: workgroups are dealt to the 8 XCDs in
+  // turn, so workgroup b takes tile xcd_tile(b) and each XCD walks its own
+  // contiguous range of tiles.  The runs that neighbouring tiles write for
+  // one digit are adjacent in the output, so they then meet in the same L2
+  // and leave it as whole lines.
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
   const int64_t tbase = tile * kWgTile;
   const int tcnt = n - tbase < kWgTile ? (int)(n - tbase) : (int)kWgTile;
   const int64_t base = tbase + (int64_t)w * kWgSub;
@@ -991,8 +1001,9 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
     uint32_t row[kWgChunks];
     if (cnt > 0) {
       const int64_t sub = tile * kWgWaves + w;
-      const int64_t r0 = io.tile_row[sub];
-      const int64_t r1 = sub + 1 < io.n_sub ? io.tile_row[sub + 1] : io.n_rows - 1;
+      auto clamp_row = [&](int64_t r) { return r < 0 ? (int64_t)0 : (r >= io.n_rows ? io.n_rows - 1 : r); };
+      const int64_t r0 = clamp_row(io.tile_row[sub]);
+      const int64_t r1 = sub + 1 < io.n_sub ? clamp_row(io.tile_row[sub + 1]) : io.n_rows - 1;
       unsigned* s_mark = reinterpret_cast<unsigned*>(s_buf) + w * kWgSub;
       if (io.ptr64)
         wg_rows<int64_t>(static_cast<const int64_t*>(io.rowptr), r0, r1, base, cnt, s_mark, lane, row);
@@ -1153,9 +1164,10 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
   }
 }
 
-// colptr[c] = min(colptr[c], colptr[c + 1], ...): block minima, then every
-// block's suffix minimum with the minimum of the blocks after it.
-constexpr int kMinItems = 16;
+// colptr[c] = min(colptr[c], colptr[c + 1], ...): block minima, their
+// suffix minima, then every block's suffix minimum with the minimum of the
+// blocks after it.
+constexpr int kMinItems = 4;
 constexpr int64_t kMinTile = 256 * kMinItems;
 
 template <class OP>
@@ -1177,22 +1189,37 @@ __global__ __launch_bounds__(256) void suffix_min_reduce_kernel(const OP* __rest
   if (threadIdx.x == 0) bmin[blockIdx.x] = s[0];
 }
 
+// Suffix minima of the block minima, in place (one workgroup, 256 blocks
+// at a time from the end, with the running minimum carried).
 template <class OP>
-__global__ __launch_bounds__(256) void suffix_min_down_kernel(OP* __restrict__ p, int64_t n,
-                                                              const OP* __restrict__ bmin, int64_t n_blocks) {
+__global__ __launch_bounds__(256) void suffix_min_blocks_kernel(OP* __restrict__ bmin, int64_t n_blocks) {
   __shared__ OP s[256];
-  // the minimum over the blocks after this one (the last entry, nnz, bounds all)
-  OP carry = p[n - 1];
-  for (int64_t b = (int64_t)blockIdx.x + 1 + threadIdx.x; b < n_blocks; b += 256)
-    if (bmin[b] < carry) carry = bmin[b];
-  s[threadIdx.x] = carry;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off && s[threadIdx.x + off] < s[threadIdx.x]) s[threadIdx.x] = s[threadIdx.x + off];
+  const int t = threadIdx.x;
+  OP carry = bmin[n_blocks - 1];
+  for (int64_t hi = n_blocks; hi > 0; hi -= 256) {
+    const int64_t b = hi - 256 + t;
+    OP v = b >= 0 ? bmin[b] : carry;
+    if (carry < v) v = carry;
+    s[t] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const OP o = t + off < 256 ? s[t + off] : carry;
+      __syncthreads();
+      if (o < s[t]) s[t] = o;
+      __syncthreads();
+    }
+    if (b >= 0) bmin[b] = s[t];
+    carry = s[0];
     __syncthreads();
   }
-  carry = s[0];
-  __syncthreads();
+}
+
+template <class OP>
+__global__ __launch_bounds__(256) void suffix_min_down_kernel(OP* __restrict__ p, int64_t n,
+                                                              const OP* __restrict__ bsuf, int64_t n_blocks) {
+  __shared__ OP s[256];
+  // the minimum over the blocks after this one (the last entry, nnz, bounds all)
+  OP carry = (int64_t)blockIdx.x + 1 < n_blocks ? bsuf[blockIdx.x + 1] : p[n - 1];
   // thread t owns kMinItems consecutive entries: its own suffix minima, then
   // the minimum over the threads after it
   const int64_t i0 = (int64_t)blockIdx.x * kMinTile + (int64_t)threadIdx.x * kMinItems;
@@ -1435,10 +1462,19 @@ inline bool transpose_wg_applies(int val_t, int64_t n_rows, int64_t n_cols, int6
   return val_t != FS_C128 && nnz > 0 && nnz < lim && n_rows <= lim && n_cols <= lim + 1;
 }
 
+// FLAGSPARSE_TRANSPOSE_COLPTR=keys: the last pass writes the sorted keys and
+// colptr_kernel reads the column pointer off them (A/B of the atomic minima).
+inline bool colptr_from_keys() {
+  const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_COLPTR");
+  return e && std::string(e) == "keys";
+}
+
 template <class OP>
 int colptr_suffix_min(OP* colptr, int64_t n, OP* bmin, int64_t n_blocks, hipStream_t s) {
   hipLaunchKernelGGL((suffix_min_reduce_kernel<OP>), dim3((unsigned)n_blocks), dim3(256), 0, s, colptr, n, bmin);
   FS_CHECK_LAUNCH("suffix_min_reduce_kernel");
+  hipLaunchKernelGGL((suffix_min_blocks_kernel<OP>), dim3(1), dim3(256), 0, s, bmin, n_blocks);
+  FS_CHECK_LAUNCH("suffix_min_blocks_kernel");
   hipLaunchKernelGGL((suffix_min_down_kernel<OP>), dim3((unsigned)n_blocks), dim3(256), 0, s, colptr, n, bmin,
                      n_blocks);
   FS_CHECK_LAUNCH("suffix_min_down_kernel");
@@ -1480,15 +1516,14 @@ int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, 
   const int vw = val_t == FS_F32 ? 1 : 2;
   int64_t* tile_row = reinterpret_cast<int64_t*>(ws + L.off_tile_row);
   if (ptr_t == FS_I32)
-    hipLaunchKernelGGL((wg_tile_rows_kernel<int32_t>), dim3((unsigned)ceil_div(L.n_sub, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((wg_tile_rows_kernel<int32_t>), dim3((unsigned)ceil_div(n_rows, 256)), dim3(256), 0, s,
                        static_cast<const int32_t*>(indptr), n_rows, L.n_sub, tile_row);
   else
-    hipLaunchKernelGGL((wg_tile_rows_kernel<int64_t>), dim3((unsigned)ceil_div(L.n_sub, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((wg_tile_rows_kernel<int64_t>), dim3((unsigned)ceil_div(n_rows, 256)), dim3(256), 0, s,
                        static_cast<const int64_t*>(indptr), n_rows, L.n_sub, tile_row);
   FS_CHECK_LAUNCH("wg_tile_rows_kernel");
   const int64_t n_ptr = n_cols + 1;
-  const char* cp = std::getenv("FLAGSPARSE_TRANSPOSE_COLPTR");
-  const bool by_keys = cp && std::string(cp) == "keys";
+  const bool by_keys = colptr_from_keys();
   if (!by_keys) {
     if (op_t == FS_I32)
       hipLaunchKernelGGL((fill_kernel<int32_t>), dim3((unsigned)ceil_div(n_ptr, 256)), dim3(256), 0, s,
@@ -2093,7 +2128,9 @@ extern "C" size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_col
 }
 
 extern "C" int fs_csr_transpose_bounded(int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz) {
-  return transpose_wg_applies(val_t, n_rows, n_cols, nnz) ? 1 : 0;
+  // (the column pointer from atomic minima and a suffix minimum is monotone
+  // and within [0, nnz] whatever the keys; read off sorted keys it is not)
+  return transpose_wg_applies(val_t, n_rows, n_cols, nnz) && !colptr_from_keys() ? 1 : 0;
 }
 
 extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, int out_ptr_t, int64_t n_rows,
