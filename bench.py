@@ -375,8 +375,13 @@ def run_config(name, args):
         if op != "non":
             # Public call including the per-call transpose (reference semantics).
             full = lambda: fs.flagsparse_spmm_csr(data, indices, indptr, B, shape, op=op)  # noqa: E731
-            full()
-            extra["ms_with_transpose"] = round(time_loop(full, max(2, args.steps // 10), stream), 4)
+            for _ in range(3):
+                full()
+            extra["ms_with_transpose"] = round(time_loop(full, max(5, args.steps // 4), stream), 4)
+            # the transpose alone (fs_csr_transpose), as the public call runs it
+            tr = lambda: _csr.transpose_csr(data, indices, indptr, shape, conj=(op == "conj"))  # noqa: E731
+            tr()
+            extra["transpose_ms"] = round(time_loop(tr, max(5, args.steps // 4), stream), 4)
 
     # Untimed clock settle (at least SETTLE_S of back-to-back steps: a step
     # is ~0.15 ms, so a handful of warm-up steps ends before the GPU leaves
@@ -668,6 +673,7 @@ def compact_entry(e):
     x = e.get("extra", {})
     if "ms_with_transpose" in x:
         out["ms_with_transpose"] = x["ms_with_transpose"]
+        out["transpose_ms"] = x.get("transpose_ms")
     if "one_shot" in x:
         out["one_shot_ms"] = x["one_shot"]["ms_per_call"]
     if "cpu_baseline" in e:
