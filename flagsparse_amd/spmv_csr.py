@@ -1103,6 +1103,10 @@ def flagsparse_spmv_csr(
             fast = _spmv_oneshot(data, indices, indptr, x, shape, index_fallback_policy, bool(return_time or return_meta))
             if fast is not None:
                 return _finish_spmv(fast[0], out, return_time, return_meta, 0.0, fast[1], 0, "oneshot")
+        if op_code != SPMV_OP_NON and not use_opt and not (return_time or return_meta):
+            fast = _spmv_transposed_oneshot(data, indices, indptr, x, shape, op_code, index_fallback_policy)
+            if fast is not None:
+                return _finish_spmv(fast, out, False, False, 0.0, None, 0, "oneshot")
         prepared = _prepare_spmv(
             data,
             indices,
@@ -1195,6 +1199,40 @@ def _oneshot_launch(data, indices, indptr, x, y, n_rows, n_cols, flags):
         _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype), n_rows, n_cols,
         data.numel(), _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(x), _lib.ptr(y),
         flags.data_ptr(), _lib.stream_handle(data.device))
+
+
+def _spmv_transposed_oneshot(data, indices, indptr, x, shape, op_code, index_fallback_policy):
+    """The unprepared y = A^T x / A^H x with one synchronisation: the
+    structure check (fs_csr_check_enqueue), the transpose (which stays in
+    bounds on any input, fs_csr_transpose_bounded) and the one-launch SpMV
+    on A^T are queued back to back; the reference's structure error, if any,
+    is raised before y is returned (spmv_csr.py:546-558, then the transpose
+    of :477-515 and :615-618).  None when the general path must run: an
+    invalid x, empty shapes, float16 / bfloat16 / complex128, a forced
+    kernel or a failed launch."""
+    if os.environ.get("FLAGSPARSE_SPMV_ONESHOT", "1") == "0" or os.environ.get("FLAGSPARSE_SPMV_KERNEL"):
+        return None
+    data, indices, indptr, n_rows, n_cols = _validate_spmv_host(data, indices, indptr, shape, index_fallback_policy)
+    nnz = data.numel()
+    if data.dtype not in HIP_VALUE_DTYPES or n_rows == 0 or n_cols == 0 or nnz == 0:
+        return None
+    try:
+        x = _validate_spmv_x_for(x, data.dtype, n_rows, data.device)
+    except (TypeError, ValueError):
+        return None
+    if not _lib.lib().fs_csr_transpose_bounded(_lib.value_code(data.dtype), n_rows, n_cols, nnz):
+        return None
+    pending = _PendingCheck(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
+    td, ti, tp, tsh = transpose_csr(data, indices, indptr, (n_rows, n_cols), conj=(op_code == SPMV_OP_CONJ_TRANS))
+    y = torch.empty(n_cols, dtype=data.dtype, device=data.device)
+    flag_t = _oneshot_flags()
+    rc = _oneshot_launch(td, ti, tp, x, y, n_cols, n_rows, flag_t)
+    pending.finish()  # raises the reference's error for a malformed A
+    if rc != 0:
+        return None
+    if any(flag_t.tolist()):
+        raise RuntimeError("fs_spmv_csr_oneshot: the transpose of a valid matrix failed its structure check")
+    return y
 
 
 def _spmv_oneshot(data, indices, indptr, x, shape, index_fallback_policy, timed):

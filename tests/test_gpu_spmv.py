@@ -642,15 +642,18 @@ def test_spmv_sell_other_stencils(device, monkeypatch, grid, dtype):
     _sampled_rows_check(data, indices, indptr, sh, x, y, rows, REL_TOL[dtype])
 
 
+@pytest.mark.parametrize("op", ["non", "trans"])
 @pytest.mark.parametrize("offset", [0, 1], ids=["aligned", "offset"])
 @pytest.mark.parametrize("ptr_dtype", INDEX_DTYPES, ids=INDEX_IDS)
 @pytest.mark.parametrize("idx_dtype", INDEX_DTYPES, ids=INDEX_IDS)
-def test_spmv_structure_errors(device, ptr_dtype, idx_dtype, offset):
+def test_spmv_structure_errors(device, ptr_dtype, idx_dtype, offset, op):
     """The reference's structure checks (spmv_csr.py:546-558), their messages
     and order, with each fault placed deep in arrays larger than one
     workgroup's share so that the one-pass device check must find it.
     offset=1 passes indices that start one element into their storage (not
-    16-byte aligned), which takes the scalar-load path of the check."""
+    16-byte aligned), which takes the scalar-load path of the check.
+    op="trans" takes the path that queues the transpose and the SpMV behind
+    the check (every column also holds three ones, so y is the same)."""
     n = 300_000
     per = 3
     indptr = torch.arange(0, (n + 1) * per, per, dtype=torch.int64)
@@ -660,7 +663,7 @@ def test_spmv_structure_errors(device, ptr_dtype, idx_dtype, offset):
 
     def call(p, c, shape=(n, n)):
         c_dev = torch.cat([c[:offset], c]).to(idx_dtype).to(device)[offset:]
-        return fs.flagsparse_spmv_csr(data, c_dev, p.to(ptr_dtype).to(device), x, shape)
+        return fs.flagsparse_spmv_csr(data, c_dev, p.to(ptr_dtype).to(device), x, shape, op=op)
 
     y = call(indptr, cols)  # valid: every row sums three ones
     assert torch.equal(y, torch.full((n,), 3.0, device=device))
@@ -911,3 +914,23 @@ def test_last_kernel_names_the_launched_kernel(device, monkeypatch, forced, expe
     prep = fs.prepare_spmv_csr(d2, i2, p2, sh2)
     fs.flagsparse_spmv_csr(x=S.vector(sh2[1], torch.float64, device, seed=8), prepared=prep)
     assert _lib.last_kernel() == "spmv_sell_group_kernel"
+
+
+@pytest.mark.parametrize("op", ["trans", "conj"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64, torch.complex128],
+                         ids=["float32", "float64", "complex64", "complex128"])
+def test_spmv_transposed_one_sync_matches_prepared(device, dtype, op):
+    """The unprepared A^T x / A^H x (check, transpose and one-launch SpMV
+    queued back to back) against the prepared route on the same matrix,
+    within the dtype's tolerance, and its meta kernel name."""
+    d, i, p, sh = S.powerlaw(1 << 15, dtype, torch.int32, device, seed=31)
+    x = S.vector(sh[0], dtype, device, seed=2)
+    y = fs.flagsparse_spmv_csr(d, i, p, x, sh, op=op)
+    prep = fs.prepare_spmv_csr(d, i, p, sh, op=op)
+    ref = fs.flagsparse_spmv_csr(x=x, prepared=prep)
+    tol = REL_TOL[dtype]
+    err = ((y - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+    assert err <= tol, err
+    # a wrong x length still raises the reference's error, after the checks
+    with pytest.raises(ValueError, match="x length"):
+        fs.flagsparse_spmv_csr(d, i, p, S.vector(sh[1] + 1, dtype, device, seed=2), sh, op=op)
