@@ -48,6 +48,17 @@ __device__ inline void wave_sync_t() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Tile of workgroup b out of n so that each of the 8 XCDs (to which
+// workgroups are dealt in turn) walks one contiguous range of tiles: the
+// runs that neighbouring tiles of a scatter write for one digit or panel
+// are adjacent in the output, so they meet in the same L2 and leave it as
+// whole lines.
+__device__ inline int64_t xcd_tile(uint32_t b, uint32_t n) {
+  constexpr uint32_t kXcds = 8;
+  const uint32_t q = n / kXcds, r = n % kXcds, x = b % kXcds, i = b / kXcds;
+  return x < r ? (int64_t)x * (q + 1) + i : (int64_t)r * (q + 1) + (int64_t)(x - r) * q + i;
+}
+
 // Lanes (among `active`) whose digit equals this lane's digit; `mask` has
 // the pass's digit bits (a uniform value: bits above it are skipped).
 __device__ inline uint64_t peer_mask(unsigned digit, uint64_t active, unsigned mask) {
@@ -322,7 +333,7 @@ __global__ __launch_bounds__(64, 2) void radix_scatter_kernel(const void* __rest
   K* s_key = reinterpret_cast<K*>(s_buf);
   Pos* s_pos = reinterpret_cast<Pos*>(s_buf);
   const int lane = threadIdx.x;
-  const int64_t sub = blockIdx.x;
+  const int64_t sub = xcd_tile(blockIdx.x, gridDim.x);
   if (sub >= n_sub) return;
   const int64_t base = sub * kSub;
   const int cnt = n - base < kSub ? (int)(n - base) : (int)kSub;
@@ -790,6 +801,9 @@ struct WgIO {
   int op64;
   int64_t n_cols;
   uint32_t conj_mask;       // xor into the high word of 8-byte values (complex64 conj)
+  const void* other;        // first pass: explicit second index per entry (COO), in place of rows from rowptr
+  int other64;
+  int swap;                 // this pass sorts by the payload's index: it and the key change places
 };
 
 // Keys of a wave sub-tile: `cnt` entries from `base` (kind 1: 8-byte
@@ -797,7 +811,12 @@ struct WgIO {
 // pointer, the chunks at immediate offsets from it.
 __device__ inline void wg_load_keys(const void* keys, int kind, int64_t base, int cnt, int lane,
                                     uint32_t (&key)[kWgChunks]) {
-  if (kind == 1) {
+  if (kind == 5 || kind == 6) {  // one word of each 8- / 12-byte payload (`keys` points at it)
+    const int W = kind == 5 ? 2 : 3;
+    const uint32_t* p = static_cast<const uint32_t*>(keys) + (base + lane) * W;
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) key[ch] = ch * 64 + lane < cnt ? p[ch * 64 * W] : 0u;
+  } else if (kind == 1) {
     const int64_t* p = static_cast<const int64_t*>(keys) + base + lane;
 #pragma unroll
     for (int ch = 0; ch < kWgChunks; ++ch) key[ch] = ch * 64 + lane < cnt ? (uint32_t)p[ch * 64] : 0u;
@@ -941,12 +960,6 @@ __global__ __launch_bounds__(256) void wg_scan_down_kernel(uint32_t* __restrict_
   }
 }
 
-__device__ inline int64_t xcd_tile(uint32_t b, uint32_t n) {
-  constexpr uint32_t kXcds = 8;
-  const uint32_t q = n / kXcds, r = n % kXcds, x = b % kXcds, i = b / kXcds;
-  return x < r ? (int64_t)x * (q + 1) + i : (int64_t)r * (q + 1) + (int64_t)(x - r) * q + i;
-}
-
 // Stable scatter of one workgroup-tile pass (see above).  Steps: keys and
 // payload into registers; per wave, ranks within the digit against the
 // wave's LDS counters (16-bit, two digits per word); per digit, the waves'
@@ -971,12 +984,7 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
-  // Consecutive tiles on one XCD: workgroups are dealt to the 8 XCDs in
-  // turn, so workgroup b takes tile xcd_tile(b) and each XCD walks its own
-  // contiguous range of tiles.  The runs that neighbouring tiles write for
-  // one digit are adjacent in the output, so they then meet in the same L2
-  // and leave it as whole lines.
-  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);  // per-XCD tile ranges
   const int64_t tbase = tile * kWgTile;
   const int tcnt = n - tbase < kWgTile ? (int)(n - tbase) : (int)kWgTile;
   const int64_t base = tbase + (int64_t)w * kWgSub;
@@ -999,7 +1007,9 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
       }
     }
     uint32_t row[kWgChunks];
-    if (cnt > 0) {
+    if (io.other) {
+      wg_load_keys(io.other, io.other64 ? 1 : 0, base, cnt, lane, row);
+    } else if (cnt > 0) {
       const int64_t sub = tile * kWgWaves + w;
       auto clamp_row = [&](int64_t r) { return r < 0 ? (int64_t)0 : (r >= io.n_rows ? io.n_rows - 1 : r); };
       const int64_t r0 = clamp_row(io.tile_row[sub]);
@@ -1025,6 +1035,19 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
     const Pay* pp = pay_in + base + lane;
 #pragma unroll
     for (int ch = 0; ch < kWgChunks; ++ch) pay[ch] = ch * 64 + lane < cnt ? pp[ch * 64] : Pay{};
+    if (io.swap) {
+#pragma unroll
+      for (int ch = 0; ch < kWgChunks; ++ch) {
+        const uint32_t k = key[ch];
+        if constexpr (VW == 1) {
+          key[ch] = (uint32_t)(pay[ch] >> 32);
+          pay[ch] = (pay[ch] & 0xffffffffull) | ((uint64_t)k << 32);
+        } else {
+          key[ch] = pay[ch].r;
+          pay[ch].r = k;
+        }
+      }
+    }
   }
   // ranks within the wave's digits, against wave w's own counters
   uint32_t* wc = reinterpret_cast<uint32_t*>(s_buf);
@@ -1535,7 +1558,7 @@ int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, 
   }
   WgIO io{vals,   indptr, ptr_t == FS_I64 ? 1 : 0, tile_row, n_rows, L.n_sub, t_vals, t_cols,
           oi_t == FS_I64 ? 1 : 0, by_keys ? nullptr : t_indptr, op_t == FS_I64 ? 1 : 0, n_cols,
-          (conj && val_t == FS_C64) ? 0x80000000u : 0u};
+          (conj && val_t == FS_C64) ? 0x80000000u : 0u, nullptr, 0, 0};
   uint32_t* counts = reinterpret_cast<uint32_t*>(ws + L.off_counts);
   uint32_t* partial = reinterpret_cast<uint32_t*>(ws + L.off_partial);
   uint32_t* totals = reinterpret_cast<uint32_t*>(ws + L.off_totals);
@@ -1929,7 +1952,7 @@ __global__ __launch_bounds__(64) void panel_scatter_kernel(const V* __restrict__
   __shared__ unsigned s_cur[kMaxPanels];
   __shared__ int64_t s_bounds[2];
   const int lane = threadIdx.x;
-  const int64_t sub = blockIdx.x;
+  const int64_t sub = xcd_tile(blockIdx.x, gridDim.x);
   if (sub >= n_sub) return;
   const int64_t base = sub * kSub;
   const int cnt = n - base < kSub ? (int)(n - base) : (int)kSub;
@@ -2178,9 +2201,95 @@ static Layout coo_layout(int64_t n_rows, int64_t n_cols, int64_t nnz) {
   return make_layout(n_rows, range, nnz);
 }
 
+// COO -> CSR on the workgroup-tile passes (4- and 8-byte values, sizes below
+// 2^32): an LSD sort by column, then by row (stable both times, so the order
+// is lexicographic by (row, col) and equal pairs keep their input order).
+// The payload carries the value and the row; the first row pass swaps the
+// row into the key and the column into the payload; the last pass writes
+// values, columns and, through atomic minima and a suffix minimum, indptr.
+inline bool coo_wg_applies(int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz, int assume_sorted) {
+  return !assume_sorted && transpose_wg_applies(val_t, n_rows, n_cols, nnz) && n_rows <= (int64_t)0xffffffffLL &&
+         !colptr_from_keys();
+}
+
+int coo_to_csr_wg(char* ws, int val_t, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz, const void* vals,
+                  const void* rows, const void* cols, void* out_vals, void* out_cols, void* out_indptr,
+                  hipStream_t s) {
+  const WgLayout L = make_wg_layout(std::max(n_rows, n_cols), nnz);
+  const int vw = val_t == FS_F32 ? 1 : 2;
+  const int64_t n_ptr = n_rows + 1;
+  hipLaunchKernelGGL((fill_kernel<int64_t>), dim3((unsigned)ceil_div(n_ptr, 256)), dim3(256), 0, s,
+                     static_cast<int64_t*>(out_indptr), n_ptr, (int64_t)nnz);
+  FS_CHECK_LAUNCH("fill_kernel");
+  const int idx_kind = idx_t == FS_I32 ? 0 : 1;
+  const int col_bits = key_bits(n_cols), row_bits = key_bits(n_rows);
+  const int col_passes = col_bits == 0 ? 0 : (col_bits + kWgMaxBits - 1) / kWgMaxBits;
+  const int row_passes = row_bits == 0 ? 1 : (row_bits + kWgMaxBits - 1) / kWgMaxBits;
+  const int passes = col_passes + row_passes;
+  // the first pass reads its keys from the columns (or, with one column,
+  // from the rows) and its second index from the other array
+  WgIO io{vals, nullptr, 0, nullptr, n_rows, 0, out_vals, out_cols, 0, out_indptr, 1, n_rows, 0u,
+          col_passes > 0 ? rows : cols, idx_t == FS_I64 ? 1 : 0, 0};
+  uint32_t* counts = reinterpret_cast<uint32_t*>(ws + L.off_counts);
+  uint32_t* partial = reinterpret_cast<uint32_t*>(ws + L.off_partial);
+  uint32_t* totals = reinterpret_cast<uint32_t*>(ws + L.off_totals);
+  uint32_t* ka = reinterpret_cast<uint32_t*>(ws + L.off_keys_a);
+  uint32_t* kb = reinterpret_cast<uint32_t*>(ws + L.off_keys_b);
+  void* pa = ws + L.off_pay_a;
+  void* pb = ws + L.off_pay_b;
+  const void* kin = col_passes > 0 ? cols : rows;
+  int kind = idx_kind;
+  const void* pin = nullptr;
+  uint32_t* kout = ka;
+  void* pout = pa;
+  const dim3 g((unsigned)L.n_tiles);
+  for (int p = 0; p < passes; ++p) {
+    const bool col_phase = p < col_passes;
+    const int q = col_phase ? p : p - col_passes;              // pass within its phase
+    const int nq = col_phase ? col_passes : row_passes;
+    const int bits = col_phase ? col_bits : row_bits;
+    // the phase's key bits split evenly over its passes
+    int shift = 0;
+    for (int j = 0; j < q; ++j) shift += (bits - shift + (nq - j) - 1) / (nq - j);
+    const int pbits = (bits - shift + (nq - q) - 1) / (nq - q);
+    const unsigned mask = pbits > 0 ? (1u << pbits) - 1u : 0u;
+    const int nd = (int)mask + 1;
+    io.swap = (!col_phase && q == 0 && col_passes > 0) ? 1 : 0;
+    // a swapping pass counts the keys it will sort by: the rows, still in the payload
+    const void* ckin = kin;
+    int ckind = kind;
+    if (io.swap) {
+      ckin = static_cast<const char*>(pin) + 4 * (vw == 1 ? 1 : 2);
+      ckind = vw == 1 ? 5 : 6;  // the row word of the 8- / 12-byte payload
+    }
+    hipLaunchKernelGGL(wg_count_kernel, g, dim3(kWgThreads), 0, s, ckin, ckind, nnz, shift, mask, counts);
+    FS_CHECK_LAUNCH("wg_count_kernel");
+    hipLaunchKernelGGL(wg_scan_reduce_kernel, dim3((unsigned)L.n_blocks), dim3(256), 0, s, counts, L.n_tiles, nd,
+                       partial);
+    FS_CHECK_LAUNCH("wg_scan_reduce_kernel");
+    hipLaunchKernelGGL(wg_scan_column_kernel, dim3((unsigned)nd), dim3(256), 0, s, partial, L.n_blocks, nd, totals);
+    FS_CHECK_LAUNCH("wg_scan_column_kernel");
+    hipLaunchKernelGGL(wg_scan_down_kernel, dim3((unsigned)L.n_blocks), dim3(256), 0, s, counts, L.n_tiles, nd,
+                       partial, totals);
+    FS_CHECK_LAUNCH("wg_scan_down_kernel");
+    const int mode = passes == 1 ? kScatterOnly : p == 0 ? kScatterFirst : p == passes - 1 ? kScatterLast
+                                                                                            : kScatterPlain;
+    const int rc = vw == 1 ? wg_launch_scatter<1>(mode, g, s, kin, kind, pin, nnz, shift, mask, counts, kout, pout, io)
+                           : wg_launch_scatter<2>(mode, g, s, kin, kind, pin, nnz, shift, mask, counts, kout, pout, io);
+    if (rc != FS_OK) return rc;
+    kin = kout;
+    kind = 2;
+    pin = pout;
+    kout = kout == ka ? kb : ka;
+    pout = pout == pa ? pb : pa;
+  }
+  return colptr_suffix_min<uint64_t>(static_cast<uint64_t*>(out_indptr), n_ptr,
+                                     reinterpret_cast<uint64_t*>(ws + L.off_bmin), L.n_min_blocks, s);
+}
+
 extern "C" size_t fs_coo_to_csr_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t nnz) {
   if (nnz <= 0) return 0;
-  return coo_layout(n_rows, n_cols, nnz).total;
+  return std::max(coo_layout(n_rows, n_cols, nnz).total, make_wg_layout(std::max(n_rows, n_cols), nnz).total);
 }
 
 extern "C" int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_cols, int64_t nnz, const void* vals,
@@ -2197,6 +2306,12 @@ extern "C" int fs_coo_to_csr(int val_t, int idx_t, int64_t n_rows, int64_t n_col
     return FS_OK;
   }
   if (!vals || !rows || !cols || !out_vals || !out_cols) return fail(FS_E_INVALID, "fs_coo_to_csr: null pointer");
+  if (coo_wg_applies(val_t, n_rows, n_cols, nnz, assume_sorted)) {
+    if (!ws || ws_bytes < make_wg_layout(std::max(n_rows, n_cols), nnz).total)
+      return fail(FS_E_WORKSPACE, "fs_coo_to_csr: workspace too small");
+    return coo_to_csr_wg(static_cast<char*>(ws), val_t, idx_t, n_rows, n_cols, nnz, vals, rows, cols, out_vals,
+                         out_cols, out_indptr, stream);
+  }
   const Layout L = coo_layout(n_rows, n_cols, nnz);
   if (!ws || ws_bytes < L.total) return fail(FS_E_WORKSPACE, "fs_coo_to_csr: workspace too small");
   char* w = static_cast<char*>(ws);

@@ -29,14 +29,28 @@ def _random_coo(n_rows, n_cols, nnz, dtype, idx_dtype, device, seed, dups=False)
 @pytest.mark.parametrize("dtype", VALUE_DTYPES, ids=VALUE_IDS)
 @pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64], ids=["int32", "int64"])
 @pytest.mark.parametrize("dups", [False, True], ids=["distinct", "dups"])
-@pytest.mark.parametrize("shape_nnz", [((1, 1), 1), ((300, 200), 5000), ((4000, 70000), 200000)])
+@pytest.mark.parametrize("shape_nnz", [((1, 1), 1), ((300, 200), 5000), ((4000, 70000), 200000), ((1, 5000), 3000),
+                                       ((5000, 1), 3000), ((3000, 9_000_000), 40000), ((300_000, 300_000), 600_000)])
 def test_coo_to_csr_bit_exact(device, dtype, idx_dtype, dups, shape_nnz):
+    # (one row / one column: a single sort phase; 9M columns: three column
+    # passes; 300k x 300k: many workgroup tiles on both phases)
     (m, n), nnz = shape_nnz
     data, row, col = _random_coo(m, n, nnz, dtype, idx_dtype, device, seed=m + nnz, dups=dups)
     d, c, p = fs.coo_to_csr_for_spmv(data, row, col, (m, n))
     od, oc, op = O.coo_to_csr(np_(data), np_(row), np_(col), (m, n))
     assert c.dtype == torch.int32 and p.dtype == torch.int64
     assert np.array_equal(np_(p), op) and np.array_equal(np_(c), oc) and np.array_equal(np_(d), od)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.complex64], ids=["float32", "complex64"])
+def test_coo_to_csr_workgroup_path_matches_wave_path(device, monkeypatch, dtype):
+    data, row, col = _random_coo(50_000, 40_000, 400_000, dtype, torch.int32, device, seed=8, dups=True)
+    monkeypatch.setenv("FLAGSPARSE_TRANSPOSE_WG", "1")
+    a = fs.coo_to_csr_for_spmv(data, row, col, (50_000, 40_000))
+    monkeypatch.setenv("FLAGSPARSE_TRANSPOSE_WG", "0")
+    b = fs.coo_to_csr_for_spmv(data, row, col, (50_000, 40_000))
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
 
 
 def test_coo_to_csr_assume_sorted_and_empty(device):
