@@ -103,6 +103,37 @@ struct VT<c64> {
 
 __device__ inline double add(double a, double b) { return a + b; }
 __device__ inline c64 add(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
+__device__ inline float add(float a, float b) { return a + b; }
+__device__ inline c32 add(c32 a, c32 b) { return c32{a.re + b.re, a.im + b.im}; }
+
+// Accumulation in the value type itself (float in float, complex64 in
+// complex64), as the reference's opt / alg1 / alg2 SpMM kernels accumulate
+// float32 data (spmm_csr.py:2792-3109, spmm_csr_opt_alg2.py:438-729); double
+// and complex128 are the same as VT.
+template <class V>
+struct VN : VT<V> {};
+template <>
+struct VN<float> {
+  using acc = float;
+  static constexpr bool complex = false;
+  __device__ static acc zero() { return 0.0f; }
+  __device__ static acc fma(float a, float x, acc s) { return __builtin_fmaf(a, x, s); }
+  __device__ static float out(acc s) { return s; }
+};
+template <>
+struct VN<c32> {
+  using acc = c32;
+  static constexpr bool complex = true;
+  __device__ static acc zero() { return c32{0.0f, 0.0f}; }
+  __device__ static acc fma(c32 a, c32 x, acc s) {
+    s.re = __builtin_fmaf(a.re, x.re, s.re);
+    s.re = __builtin_fmaf(-a.im, x.im, s.re);
+    s.im = __builtin_fmaf(a.re, x.im, s.im);
+    s.im = __builtin_fmaf(a.im, x.re, s.im);
+    return s;
+  }
+  __device__ static c32 out(acc s) { return s; }
+};
 
 // Streaming (non-temporal) load of one element.
 __device__ inline float load_stream(const float* p) { return __builtin_nontemporal_load(p); }
@@ -251,6 +282,15 @@ bool valid_types(int val_t, int idx_t, int ptr_t);
 
 // FS_CHECK_LAUNCH for the main kernel of an entry point: also records its
 // name for fs_last_kernel().
+// Workgroup b of a 1-D grid of n, renumbered so that each of the 8 XCDs (to
+// which the hardware deals workgroups in turn) walks one contiguous range:
+// a bijection on [0, n).
+__device__ inline int64_t xcd_range_block(uint32_t b, uint32_t n) {
+  constexpr uint32_t kX = 8;
+  const uint32_t q = n / kX, r = n % kX, x = b % kX, i = b / kX;
+  return x < r ? (int64_t)x * (q + 1) + i : (int64_t)r * (q + 1) + (int64_t)(x - r) * q + i;
+}
+
 #define FS_CHECK_MAIN_LAUNCH(name)                          \
   do {                                                      \
     int _rc = ::fs::check_hip(hipGetLastError(), name);     \

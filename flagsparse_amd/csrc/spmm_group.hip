@@ -74,14 +74,13 @@ __device__ inline T bcast_lane(const T& v, int src_lane) {
 // 1.447 / 1.400 ms), two gathers per batch instead of four (more waves per
 // SIMD; C4 1.33 ms against 1.26), a residency bound through
 // amdgpu_waves_per_eu (spills registers).
-template <class V, int LPR, int U, bool VEC, class I>
+template <class V, int LPR, int U, bool VEC, class I, class T = VT<V>>
 __global__ __launch_bounds__(256) void spmm_group_kernel(
     const V* __restrict__ vals, const I* __restrict__ cols, const void* __restrict__ rowptr_raw, int ptr64,
     const V* __restrict__ B, int64_t sbk, int64_t sbn, V* __restrict__ C, int64_t scm, int64_t scn,
     int64_t n_dense, const int64_t* __restrict__ part, int sub_items,
-    typename VT<V>::acc* __restrict__ head, typename VT<V>::acc* __restrict__ tail, int64_t n_rows,
-    int64_t nnz, int64_t n_sub, int xcd_cols) {
-  using T = VT<V>;
+    typename T::acc* __restrict__ head, typename T::acc* __restrict__ tail, int64_t n_rows,
+    int64_t nnz, int64_t n_sub, int xcd_cols, int row_ranges) {
   using A = typename T::acc;
   constexpr int G = 64 / LPR;
   constexpr int EPL = group_epl<V>();
@@ -91,7 +90,10 @@ __global__ __launch_bounds__(256) void spmm_group_kernel(
   const int g = lane / LPR;
   const int gl = lane % LPR;
   const int64_t ctile = xcd_cols > 0 ? (int64_t)(blockIdx.x % (unsigned)xcd_cols) : (int64_t)blockIdx.y;
-  const int64_t tblk = xcd_cols > 0 ? (int64_t)(blockIdx.x / (unsigned)xcd_cols) : (int64_t)blockIdx.x;
+  // row_ranges (2-D grid only): each XCD walks one contiguous range of tile
+  // blocks, so the rows in flight on an XCD at any moment are adjacent
+  const int64_t tblk = xcd_cols > 0 ? (int64_t)(blockIdx.x / (unsigned)xcd_cols)
+                                    : (row_ranges ? xcd_range_block(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x);
   const int64_t wid = tblk * 4 + (threadIdx.x >> 6);
   if (wid * G >= n_sub) return;  // wave-uniform; no barriers below
   const int64_t st = wid * G + g;
@@ -274,12 +276,11 @@ __global__ __launch_bounds__(256) void spmm_zero_kernel(V* __restrict__ C, int64
 }
 
 // Rows that cross sub-tiles: C[row] = tail[f] + ... + tail[t-1] + head[t].
-template <class V>
+template <class V, class T = VT<V>>
 __global__ __launch_bounds__(256) void spmm_group_fixup_kernel(
     const void* __restrict__ rowptr_raw, int ptr64, const int64_t* __restrict__ part, int sub_items,
-    const typename VT<V>::acc* __restrict__ head, const typename VT<V>::acc* __restrict__ tail,
+    const typename T::acc* __restrict__ head, const typename T::acc* __restrict__ tail,
     V* __restrict__ C, int64_t scm, int64_t scn, int64_t n_dense, int64_t n_sub) {
-  using T = VT<V>;
   using A = typename T::acc;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= n_sub) return;
@@ -361,12 +362,12 @@ inline int spmm_tile_items_for(int val_t, int64_t n_dense) {
   return group_sub_items(val_t, n_dense);
 }
 
-template <class V, int LPR>
+template <class V, int LPR, class T>
 int launch_spmm_group(const fs_csr_plan* plan, const void* vals, const void* cols, const void* indptr,
                       const void* B, int64_t sbk, int64_t sbn, void* C, int64_t scm, int64_t scn,
                       int64_t n_dense, const int64_t* part, int sub_items, int64_t n_sub, void* ws,
                       hipStream_t stream) {
-  using A = typename VT<V>::acc;
+  using A = typename T::acc;
   constexpr int G = 64 / LPR;
   constexpr int EPL = group_epl<V>();
   A* head = static_cast<A*>(ws);
@@ -378,6 +379,8 @@ int launch_spmm_group(const fs_csr_plan* plan, const void* vals, const void* col
   int xcd_cols = (col_tiles == 2 || col_tiles == 4 || col_tiles == 8) ? (int)col_tiles : 0;
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_XCD")) xcd_cols = std::atoi(e) != 0 ? (int)col_tiles : 0;
   if (xcd_cols > 0 && blocks * col_tiles > 0x7fffffffLL) xcd_cols = 0;
+  int row_ranges = 0;
+  if (const char* e = std::getenv("FLAGSPARSE_SPMM_ROW_RANGES")) row_ranges = std::atoi(e) != 0;
   dim3 grid = xcd_cols > 0 ? dim3((unsigned)(blocks * col_tiles)) : dim3((unsigned)blocks, (unsigned)col_tiles);
   size_t lds = (size_t)4 * G * (size_t)sub_items * sizeof(uint16_t);
   if (const char* e = std::getenv("FLAGSPARSE_SPMM_WG_CAP")) lds = std::max(lds, lds_pad_for_cap(std::atoi(e), 0));
@@ -390,10 +393,10 @@ int launch_spmm_group(const fs_csr_plan* plan, const void* vals, const void* col
   auto go = [&](auto icode) {
     using I = std::conditional_t<decltype(icode)::value, int64_t, int32_t>;
     auto launch = [&](auto vcode) {
-      hipLaunchKernelGGL((spmm_group_kernel<V, LPR, 4, decltype(vcode)::value, I>), grid, dim3(256), lds, stream,
+      hipLaunchKernelGGL((spmm_group_kernel<V, LPR, 4, decltype(vcode)::value, I, T>), grid, dim3(256), lds, stream,
                          static_cast<const V*>(vals), static_cast<const I*>(cols), indptr, ptr64,
                          static_cast<const V*>(B), sbk, sbn, static_cast<V*>(C), scm, scn, n_dense, part, sub_items,
-                         head, tail, plan->n_rows, plan->nnz, n_sub, xcd_cols);
+                         head, tail, plan->n_rows, plan->nnz, n_sub, xcd_cols, row_ranges);
     };
     if (vec) launch(std::true_type{});
     else launch(std::false_type{});
@@ -403,25 +406,41 @@ int launch_spmm_group(const fs_csr_plan* plan, const void* vals, const void* col
   FS_CHECK_MAIN_LAUNCH("spmm_group_kernel");
   const int64_t fix_blocks = ceil_div(n_sub, 4);
   const int64_t fix_cols = ceil_div(n_dense, 64) < 64 ? ceil_div(n_dense, 64) : 64;
-  hipLaunchKernelGGL((spmm_group_fixup_kernel<V>), dim3((unsigned)fix_blocks, (unsigned)fix_cols), dim3(256), 0,
+  hipLaunchKernelGGL((spmm_group_fixup_kernel<V, T>), dim3((unsigned)fix_blocks, (unsigned)fix_cols), dim3(256), 0,
                      stream, indptr, plan->ptr_t == FS_I64 ? 1 : 0, part, sub_items, head, tail,
                      static_cast<V*>(C), scm, scn, n_dense, n_sub);
   FS_CHECK_LAUNCH("spmm_group_fixup_kernel");
   return FS_OK;
 }
 
+template <class V, class T>
+int launch_spmm_group_lpr_t(int lpr, const fs_csr_plan* plan, const void* vals, const void* cols,
+                            const void* indptr, const void* B, int64_t sbk, int64_t sbn, void* C, int64_t scm,
+                            int64_t scn, int64_t n_dense, const int64_t* part, int sub_items, int64_t n_sub,
+                            void* ws, hipStream_t s) {
+  switch (lpr) {
+    case 8: return launch_spmm_group<V, 8, T>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
+    case 16: return launch_spmm_group<V, 16, T>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
+    case 32: return launch_spmm_group<V, 32, T>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
+    case 64: return launch_spmm_group<V, 64, T>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
+  }
+  return fail(FS_E_INVALID, "fs_spmm_csr: unsupported lane-group width");
+}
+
+// native = 1: float32 / complex64 accumulate in their own precision (VN);
+// otherwise, and always for float64 / complex128, in VT's.
 template <class V>
-int launch_spmm_group_lpr(int lpr, const fs_csr_plan* plan, const void* vals, const void* cols,
+int launch_spmm_group_lpr(int lpr, int native, const fs_csr_plan* plan, const void* vals, const void* cols,
                           const void* indptr, const void* B, int64_t sbk, int64_t sbn, void* C, int64_t scm,
                           int64_t scn, int64_t n_dense, const int64_t* part, int sub_items, int64_t n_sub,
                           void* ws, hipStream_t s) {
-  switch (lpr) {
-    case 8: return launch_spmm_group<V, 8>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
-    case 16: return launch_spmm_group<V, 16>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
-    case 32: return launch_spmm_group<V, 32>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
-    case 64: return launch_spmm_group<V, 64>(plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, sub_items, n_sub, ws, s);
+  if constexpr (std::is_same_v<V, float> || std::is_same_v<V, c32>) {
+    if (native)
+      return launch_spmm_group_lpr_t<V, VN<V>>(lpr, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense,
+                                               part, sub_items, n_sub, ws, s);
   }
-  return fail(FS_E_INVALID, "fs_spmm_csr: unsupported lane-group width");
+  return launch_spmm_group_lpr_t<V, VT<V>>(lpr, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part,
+                                           sub_items, n_sub, ws, s);
 }
 
 }  // namespace fs
@@ -476,11 +495,13 @@ extern "C" int fs_spmm_csr_strided(const fs_csr_plan* plan, const void* vals, co
   }
   if (group) {
     const int lpr = group_lpr(plan->val_t, n_dense);
+    int native = 0;
+    if (const char* e = std::getenv("FLAGSPARSE_SPMM_ACC")) native = std::string(e) == "native";
     switch (plan->val_t) {
-      case FS_F32: return launch_spmm_group_lpr<float>(lpr, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
-      case FS_F64: return launch_spmm_group_lpr<double>(lpr, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
-      case FS_C64: return launch_spmm_group_lpr<c32>(lpr, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
-      default: return launch_spmm_group_lpr<c64>(lpr, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
+      case FS_F32: return launch_spmm_group_lpr<float>(lpr, native, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
+      case FS_F64: return launch_spmm_group_lpr<double>(lpr, native, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
+      case FS_C64: return launch_spmm_group_lpr<c32>(lpr, native, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
+      default: return launch_spmm_group_lpr<c64>(lpr, native, plan, vals, cols, indptr, B, sbk, sbn, C, scm, scn, n_dense, part, tile_items, n_tiles, ws, stream);
     }
   }
   // Merge-path kernel (FLAGSPARSE_SPMM_KERNEL=merge): row-major B / C only.
