@@ -360,13 +360,9 @@ def run_config(name, args):
         step()  # the first launch builds the route's copies (the SELL-64 copy of a stencil)
         sell = plan._sell
         if sell is not None and sell.spmm_fits(B, C):
-            sell_abi = (
-                _lib.value_code(sell.vals.dtype), sell.col_code, _lib.index_code(sell.indptr.dtype), sell.layout,
-                sell.n_rows, _lib.ptr(sell.vals), _lib.ptr(sell.cols),
-                _lib.ptr(sell.table) if sell.table is not None else None, _lib.ptr(sell.slice_ptr),
-                _lib.ptr(sell.indptr), _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.stream_handle(device),
-            )
-            kernel_call = lambda: lib.fs_spmm_sell(*sell_abi)  # noqa: E731
+            sell_fn, sell_name, sell_args = sell.spmm_call(B, C)
+            kernel_call = lambda: sell_fn(*sell_args)  # noqa: E731
+            extra["sell_entry_point"] = sell_name
             extra["sell_column_storage"] = {0: "int32", 1: "int64", 2: "int16 offset from the row",
                                             3: "uint8 code of the offset from the row"}[sell.col_code]
         bytes_alg = S.bytes_spmm(nnz, m, k, n_dense, vb, ib, pb)

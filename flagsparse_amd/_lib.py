@@ -77,6 +77,8 @@ EXPORTED_SYMBOLS = (
     "fs_csr_to_sell",
     "fs_spmv_sell",
     "fs_spmm_sell",
+    "fs_spmm_sell_staged_fits",
+    "fs_spmm_sell_staged",
 )
 
 
@@ -125,6 +127,11 @@ def _declare(lib):
     lib.fs_csr_check_bytes.argtypes = []
     lib.fs_csr_check.restype = _i32
     lib.fs_csr_check.argtypes = [_vp, _i32, _vp, _i32, _i64, _i64, _vp, ctypes.POINTER(_i64), _vp]
+    lib.fs_spmm_sell_staged_fits.restype = _i32
+    lib.fs_spmm_sell_staged_fits.argtypes = [_i32, _vp, _i32, _i64]
+    lib.fs_spmm_sell_staged.restype = _i32
+    lib.fs_spmm_sell_staged.argtypes = [_i32, _i32, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64,
+                                        _vp, _i64, _i64, _vp]
     lib.fs_csr_transpose_bounded.restype = _i32
     lib.fs_csr_transpose_bounded.argtypes = [_i32, _i64, _i64, _i64]
     lib.fs_csr_check_enqueue.restype = _i32

@@ -23,7 +23,9 @@
 // reference's prepare caches (spmv_csr.py:124-130).
 #include "fs_common.hpp"
 
+#include <algorithm>
 #include <cstdlib>
+#include <vector>
 #include <type_traits>
 
 namespace fs {
@@ -640,6 +642,246 @@ int spmm_sell_t(int layout, int64_t n_rows, const void* sv, const void* sc, cons
   return FS_OK;
 }
 
+// ---------------------------------------------------------------------------
+// SpMM on the SELL-64 copy with offset codes, B staged through LDS.
+// A slice's 64 rows read B rows row + offset[code]: for every code a window
+// of 64 consecutive B rows, and codes whose windows overlap or touch (a
+// stencil's x-neighbours: offsets -1, 0, +1) share one band.  A workgroup
+// per (slice, column tile) first copies its bands' B-row tiles into LDS with
+// coalesced 16-byte loads (each B row of a band once), then every row walks
+// its slots and reads its B slices from LDS: the B rows a 27-point stencil
+// slice needs are 9 bands of 66 rows, read once instead of once per use.
+// Slots are summed in the same order as spmm_sell_kernel (bit-identical).
+// ---------------------------------------------------------------------------
+constexpr int kSellMaxBands = 32;
+struct SellBands {
+  int n;                      // bands
+  int lo[kSellMaxBands];      // smallest offset of the band's codes
+  int hi[kSellMaxBands];      // largest offset
+  int lds[kSellMaxBands];     // first LDS row of the band (hi - lo + 64 rows each)
+  int rows;                   // LDS rows of all bands
+};
+constexpr int kSellStageSlots = 32;  // slots of values and codes staged at a time
+constexpr int kSellStageU = 8;       // slots read from LDS together
+constexpr int kSellStageBatch = 8;   // B loads in flight per thread while staging
+
+template <class V, class P, int TL, int G>
+__global__ __launch_bounds__(256) void spmm_sell_staged_kernel(
+    const V* __restrict__ sell_vals, const uint8_t* __restrict__ codes, const int* __restrict__ table,
+    const int64_t* __restrict__ slice_ptr, const P* __restrict__ rowptr, const V* __restrict__ B, int64_t ldb,
+    int64_t n_b_rows, V* __restrict__ C, int64_t ldc, int64_t n_dense, int64_t n_rows, int col_tiles,
+    SellBands bands) {
+  using T = VT<V>;
+  using A = typename T::acc;
+  using L4 = __attribute__((ext_vector_type(4))) unsigned int;
+  constexpr int EPL = (int)(16 / sizeof(V));
+  constexpr int RW = 64 / TL;  // rows per wave instruction
+  constexpr int KR = 16 / RW;  // a wave's 16 rows take KR instruction rows
+  static_assert(TL == 4 || TL == 8, "4 or 8 lanes per row tile (a wave's 16 rows in whole instructions)");
+  extern __shared__ L4 s_b[];  // the bands' B tiles, then a chunk of the slice's values and codes
+  __shared__ int s_base[kSellCodes];
+  const int t = threadIdx.x;
+  // consecutive slices on one XCD: neighbouring slices' bands overlap in its L2
+  const int64_t blk = xcd_range_block(blockIdx.x, gridDim.x);
+  const int64_t slice = blk / col_tiles;
+  const int ctile = (int)(blk - slice * col_tiles);
+  const int64_t row0 = slice * kSellRows;
+  const int64_t col0 = (int64_t)ctile * TL * EPL;
+  {  // LDS row of code t's window for local row 0 (-1: the code is not in use)
+    const int off = table[t];
+    int base = -1;
+    for (int b = 0; b < bands.n; ++b)
+      if (off >= bands.lo[b] && off <= bands.hi[b]) base = bands.lds[b] + (off - bands.lo[b]);
+    s_base[t] = base;
+  }
+  __syncthreads();
+  // the bands' B tiles: LDS rows are the bands' rows back to back; each
+  // thread issues kSellStageBatch loads before it stores any (one latency
+  // per batch, not per band)
+  {
+    const int total = bands.rows * TL;
+    for (int i0 = t; i0 < total; i0 += 256 * kSellStageBatch) {
+      L4 v[kSellStageBatch];
+      int at[kSellStageBatch];
+#pragma unroll
+      for (int u = 0; u < kSellStageBatch; ++u) {
+        const int i = i0 + u * 256;
+        at[u] = -1;
+        v[u] = L4{0u, 0u, 0u, 0u};
+        if (i < total) {
+          const int q = i / TL, pc = i - q * TL;
+          int b = 0;
+          while (b + 1 < bands.n && bands.lds[b + 1] <= q) ++b;
+          const int64_t g = row0 + bands.lo[b] + (q - bands.lds[b]);
+          const int64_t c = col0 + (int64_t)pc * EPL;
+          at[u] = i;
+          if (g >= 0 && g < n_b_rows && c < n_dense) v[u] = *reinterpret_cast<const L4*>(B + g * ldb + c);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kSellStageBatch; ++u)
+        if (at[u] >= 0) s_b[at[u]] = v[u];
+    }
+  }
+  V* s_v = reinterpret_cast<V*>(s_b + (size_t)bands.rows * TL);
+  int16_t* s_o = reinterpret_cast<int16_t*>(s_v + kSellStageSlots * kSellRows);  // LDS row of the entry's window
+  const int lane = t & 63;
+  const int sub = lane / TL, gl = lane - sub * TL;
+  const int64_t base = slice_ptr[slice];
+  const int slots = (int)((slice_ptr[slice + 1] - base) / kSellRows);
+  int lr[KR], len[KR];
+#pragma unroll
+  for (int k = 0; k < KR; ++k) {
+    lr[k] = (t >> 6) * 16 + sub + RW * k;
+    const int64_t r = row0 + lr[k];
+    len[k] = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
+  }
+  A acc[KR][EPL];
+#pragma unroll
+  for (int k = 0; k < KR; ++k)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[k][e] = T::zero();
+  // the slice's values and codes pass through LDS kSellStageSlots slots at a
+  // time (their storage is contiguous per slot range: chunks start on pair
+  // boundaries)
+  for (int j0 = 0; j0 < slots; j0 += kSellStageSlots) {
+    const int nj = slots - j0 < kSellStageSlots ? slots - j0 : kSellStageSlots;
+    const int64_t cbase = base + (int64_t)j0 * kSellRows;
+    for (int i = t; i < nj * kSellRows; i += 256) {
+      s_v[i] = load_stream(sell_vals + cbase + i);
+      s_o[i] = (int16_t)s_base[__builtin_nontemporal_load(codes + cbase + i)];
+    }
+    __syncthreads();  // (the first time also the bands)
+    // kSellStageU slots at a time: their LDS loads are independent
+    for (int jj0 = 0; jj0 < nj; jj0 += kSellStageU) {
+#pragma unroll
+      for (int k = 0; k < KR; ++k) {
+        V a[kSellStageU];
+        int o[kSellStageU];
+#pragma unroll
+        for (int u = 0; u < kSellStageU; ++u) {
+          const int jj = jj0 + u < nj ? jj0 + u : nj - 1;
+          const int li = (jj / G) * (G * kSellRows) + G * lr[k] + (jj % G);
+          a[u] = s_v[li];
+          o[u] = s_o[li] < 0 ? 0 : s_o[li];  // (an unused code: a read inside the bands, discarded)
+        }
+        L4 q[kSellStageU];
+#pragma unroll
+        for (int u = 0; u < kSellStageU; ++u) q[u] = s_b[(o[u] + lr[k]) * TL + gl];
+#pragma unroll
+        for (int u = 0; u < kSellStageU; ++u) {
+          if (jj0 + u < nj && j0 + jj0 + u < len[k]) {
+            V bv[EPL];
+            __builtin_memcpy(bv, &q[u], 16);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[k][e] = T::fma(a[u], bv[e], acc[k][e]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int64_t col = col0 + (int64_t)gl * EPL;
+  if (col >= n_dense) return;
+#pragma unroll
+  for (int k = 0; k < KR; ++k) {
+    const int64_t r = row0 + lr[k];
+    if (r < n_rows) {
+      V o[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = T::out(acc[k][e]);
+      L4 w;
+      __builtin_memcpy(&w, o, 16);
+      *reinterpret_cast<L4*>(C + r * ldc + col) = w;
+    }
+  }
+}
+
+// Bands from the codes' offsets (host): sorted, merged while windows of 64
+// rows overlap or touch.  Returns the LDS rows they take, or -1 when there
+// are more than kSellMaxBands.
+inline int sell_bands(const int* offsets, int n_codes, SellBands& bands) {
+  std::vector<int> o(offsets, offsets + n_codes);
+  std::sort(o.begin(), o.end());
+  o.erase(std::unique(o.begin(), o.end()), o.end());
+  bands.n = 0;
+  int rows = 0;
+  for (size_t i = 0; i < o.size();) {
+    int lo = o[i], hi = o[i];
+    ++i;
+    while (i < o.size() && (int64_t)o[i] <= (int64_t)hi + kSellRows) hi = o[i++];
+    if (bands.n == kSellMaxBands) return -1;
+    bands.lo[bands.n] = lo;
+    bands.hi[bands.n] = hi;
+    bands.lds[bands.n] = rows;
+    rows += hi - lo + kSellRows;
+    ++bands.n;
+  }
+  bands.rows = rows;
+  return rows;
+}
+
+// dynamic LDS per workgroup (at least 2 per CU); FLAGSPARSE_SPMM_SELL_STAGE_LDS_KB overrides
+inline size_t sell_stage_lds_limit() {
+  const int kb = env_int("FLAGSPARSE_SPMM_SELL_STAGE_LDS_KB", 64);
+  return (size_t)(kb >= 16 && kb <= 80 ? kb : 64) * 1024;
+}
+
+// Dynamic LDS of the staged kernel for these offsets and B width, 0 when it
+// does not apply (more than kSellMaxBands bands, or over sell_stage_lds_limit()).
+inline size_t sell_staged_lds(int val_size, const int* offsets, int n_codes, int64_t n_dense, int* tl_out,
+                              SellBands* bands_out) {
+  SellBands bands{};
+  const int rows = sell_bands(offsets, n_codes, bands);
+  if (rows < 0) return 0;
+  const int epl = 16 / val_size;
+  const int64_t pieces = (n_dense + epl - 1) / epl;
+  int tl = pieces <= 4 ? 4 : 8;
+  if (const int e = env_int("FLAGSPARSE_SPMM_SELL_STAGE_TL", 0); e == 4 || e == 8) tl = e;
+  const size_t chunk = (size_t)kSellStageSlots * kSellRows * ((size_t)val_size + 2);
+  if (tl == 8 && (size_t)rows * tl * 16 + chunk > sell_stage_lds_limit()) tl = 4;
+  const size_t lds = (size_t)rows * tl * 16 + chunk;
+  if (lds > sell_stage_lds_limit()) return 0;
+  if (tl_out) *tl_out = tl;
+  if (bands_out) *bands_out = bands;
+  return lds;
+}
+
+template <class V, class P>
+int spmm_sell_staged_t(int layout, int64_t n_rows, int64_t n_b_rows, const void* sv, const uint8_t* codes,
+                       const int* table, const int* offsets, int n_codes, const int64_t* slice_ptr,
+                       const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t n_dense,
+                       hipStream_t s) {
+  constexpr int EPL = (int)(16 / sizeof(V));
+  if (n_dense % EPL || ldb % EPL || ldc % EPL || ((uintptr_t)B % 16) || ((uintptr_t)C % 16))
+    return fail(FS_E_INVALID, "fs_spmm_sell_staged: B / C rows must be whole 16-byte slices");
+  if (layout == FS_SELL_PAIR && VT<V>::complex)
+    return fail(FS_E_INVALID, "fs_spmm_sell_staged: the pair layout is for real values");
+  SellBands bands{};
+  int tl = 8;
+  const size_t lds = sell_staged_lds((int)sizeof(V), offsets, n_codes, n_dense, &tl, &bands);
+  if (lds == 0) return fail(FS_E_INVALID, "fs_spmm_sell_staged: the offsets' bands do not fit LDS");
+  const int64_t pieces = n_dense / EPL;  // 16-byte slices per B row
+  const int col_tiles = (int)ceil_div(pieces, tl);
+  const int64_t n_slices = ceil_div(n_rows, kSellRows);
+  const int64_t blocks = n_slices * col_tiles;
+  if (blocks > 0x7fffffffLL) return fail(FS_E_INVALID, "fs_spmm_sell_staged: grid too large");
+  auto go = [&](auto tc, auto gc) {
+    hipLaunchKernelGGL((spmm_sell_staged_kernel<V, P, decltype(tc)::value, decltype(gc)::value>),
+                       dim3((unsigned)blocks), dim3(256), lds, s, static_cast<const V*>(sv), codes, table, slice_ptr,
+                       static_cast<const P*>(indptr), static_cast<const V*>(B), ldb, n_b_rows, static_cast<V*>(C),
+                       ldc, n_dense, n_rows, col_tiles, bands);
+  };
+  auto by_g = [&](auto tc) {
+    if (layout == FS_SELL_PAIR) go(tc, std::integral_constant<int, 2>{});
+    else go(tc, std::integral_constant<int, 1>{});
+  };
+  if (tl == 4) by_g(std::integral_constant<int, 4>{});
+  else by_g(std::integral_constant<int, 8>{});
+  FS_CHECK_MAIN_LAUNCH("spmm_sell_staged_kernel");
+  return FS_OK;
+}
+
 template <class V, class I, class P>
 struct SpmmF {
   int operator()(int layout, int64_t n_rows, const void* sv, const void* sc, const int* table,
@@ -733,4 +975,41 @@ extern "C" int fs_spmm_sell(int val_t, int sell_idx_t, int ptr_t, int layout, in
   if (!indptr || !slice_ptr || !C || !B) return fail(FS_E_INVALID, "fs_spmm_sell: null pointer");
   return dispatch_vip<SpmmF>(val_t, sell_idx_t, ptr_t, layout, n_rows, sell_vals, sell_cols, code_table, slice_ptr,
                              indptr, B, ldb, C, ldc, n_dense, stream);
+}
+
+extern "C" int fs_spmm_sell_staged_fits(int val_t, const int32_t* offsets_host, int n_codes, int64_t n_dense) {
+  if (val_t < FS_F32 || val_t > FS_C128 || !offsets_host || n_codes <= 0 || n_codes > kSellCodes || n_dense <= 0)
+    return 0;
+  const int esz[] = {4, 8, 8, 16};
+  return sell_staged_lds(esz[val_t], offsets_host, n_codes, n_dense, nullptr, nullptr) > 0 ? 1 : 0;
+}
+
+extern "C" int fs_spmm_sell_staged(int val_t, int ptr_t, int layout, int64_t n_rows, int64_t n_b_rows,
+                                   const void* sell_vals, const void* sell_codes, const int32_t* code_table,
+                                   const int32_t* offsets_host, int n_codes, const int64_t* slice_ptr,
+                                   const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc,
+                                   int64_t n_dense, hipStream_t stream) {
+  if (!valid_types(val_t, FS_I32, ptr_t)) return fail(FS_E_INVALID, "fs_spmm_sell_staged: bad type code");
+  if (!(layout == FS_SELL_SLOT || layout == FS_SELL_PAIR)) return fail(FS_E_INVALID, "fs_spmm_sell_staged: bad layout");
+  if (n_rows < 0 || n_b_rows < 0 || n_dense < 0 || n_codes < 0 || n_codes > kSellCodes)
+    return fail(FS_E_INVALID, "fs_spmm_sell_staged: bad size");
+  if (n_rows == 0 || n_dense == 0) return FS_OK;
+  if (ldc < n_dense || ldb < n_dense) return fail(FS_E_INVALID, "fs_spmm_sell_staged: leading dimension smaller than n_dense");
+  if (!sell_vals || !sell_codes || !code_table || !offsets_host || !slice_ptr || !indptr || !B || !C)
+    return fail(FS_E_INVALID, "fs_spmm_sell_staged: null pointer");
+  const uint8_t* codes = static_cast<const uint8_t*>(sell_codes);
+  auto by_p = [&](auto vtag) {
+    using V = typename decltype(vtag)::type;
+    if (ptr_t == FS_I32)
+      return spmm_sell_staged_t<V, int32_t>(layout, n_rows, n_b_rows, sell_vals, codes, code_table, offsets_host,
+                                            n_codes, slice_ptr, indptr, B, ldb, C, ldc, n_dense, stream);
+    return spmm_sell_staged_t<V, int64_t>(layout, n_rows, n_b_rows, sell_vals, codes, code_table, offsets_host,
+                                          n_codes, slice_ptr, indptr, B, ldb, C, ldc, n_dense, stream);
+  };
+  switch (val_t) {
+    case FS_F32: return by_p(type_tag<float>{});
+    case FS_F64: return by_p(type_tag<double>{});
+    case FS_C64: return by_p(type_tag<c32>{});
+    default: return by_p(type_tag<c64>{});
+  }
 }

@@ -544,7 +544,8 @@ class SellCsr:
     offsets the codes stand for.  The CSR row pointer of the prepared matrix supplies the
     row lengths."""
 
-    __slots__ = ("vals", "cols", "col_code", "layout", "slice_ptr", "indptr", "n_rows", "padded", "table", "n_codes")
+    __slots__ = ("vals", "cols", "col_code", "layout", "slice_ptr", "indptr", "n_rows", "padded", "table", "n_codes",
+                 "offsets_host")
 
     def __init__(self, data, indices, indptr, slice_ptr, col_code, layout, offsets=None):
         device = data.device
@@ -563,6 +564,7 @@ class SellCsr:
         self.cols = torch.zeros(self.padded, dtype=col_dtype, device=device)
         self.table = None
         self.n_codes = 0
+        self.offsets_host = None
         lut = None
         if col_code == _SELL_C8:
             self.n_codes = len(offsets)
@@ -572,6 +574,7 @@ class SellCsr:
             lut_host = np.zeros(65536, dtype=np.uint8)
             lut_host[np.asarray(offsets, dtype=np.int64) + 32768] = np.arange(len(offsets), dtype=np.uint8)
             self.table = torch.from_numpy(table).to(device)
+            self.offsets_host = np.ascontiguousarray(np.asarray(offsets, dtype=np.int32))
             lut = torch.from_numpy(lut_host).to(device)
         _lib.check(
             lib.fs_csr_to_sell(
@@ -593,17 +596,32 @@ class SellCsr:
                 and n % epl == 0 and B.stride(0) % epl == 0 and C.stride(0) % epl == 0
                 and B.data_ptr() % 16 == 0 and C.data_ptr() % 16 == 0 and B.stride(0) >= n and C.stride(0) >= n)
 
+    def spmm_call(self, B, C):
+        """(entry point, name, arguments) of C = A B on this copy:
+        fs_spmm_sell, or with FLAGSPARSE_SPMM_SELL_STAGE=1 and offset codes
+        whose bands fit, the B-through-LDS kernel (fs_spmm_sell_staged; the
+        same bits, measured slower on the 27-point stencil: 1.37 against
+        0.59 ms at N = 32 f32, so it is not the default)."""
+        lib = _lib.lib()
+        stream = _lib.stream_handle(self.vals.device)
+        if (self.col_code == _SELL_C8 and os.environ.get("FLAGSPARSE_SPMM_SELL_STAGE", "0") == "1"
+                and lib.fs_spmm_sell_staged_fits(_lib.value_code(self.vals.dtype), self.offsets_host.ctypes.data,
+                                                 self.n_codes, int(B.shape[1]))):
+            return lib.fs_spmm_sell_staged, "fs_spmm_sell_staged", (
+                _lib.value_code(self.vals.dtype), _lib.index_code(self.indptr.dtype), self.layout, self.n_rows,
+                int(B.shape[0]), _lib.ptr(self.vals), _lib.ptr(self.cols), _lib.ptr(self.table),
+                self.offsets_host.ctypes.data, self.n_codes, _lib.ptr(self.slice_ptr), _lib.ptr(self.indptr),
+                _lib.ptr(B), int(B.stride(0)), _lib.ptr(C), int(C.stride(0)), int(B.shape[1]), stream)
+        return lib.fs_spmm_sell, "fs_spmm_sell", (
+            _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype), self.layout,
+            self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols),
+            _lib.ptr(self.table) if self.table is not None else None, _lib.ptr(self.slice_ptr),
+            _lib.ptr(self.indptr), _lib.ptr(B), int(B.stride(0)), _lib.ptr(C), int(C.stride(0)), int(B.shape[1]),
+            stream)
+
     def spmm(self, B, C):
-        _lib.check(
-            _lib.lib().fs_spmm_sell(
-                _lib.value_code(self.vals.dtype), self.col_code, _lib.index_code(self.indptr.dtype), self.layout,
-                self.n_rows, _lib.ptr(self.vals), _lib.ptr(self.cols),
-                _lib.ptr(self.table) if self.table is not None else None, _lib.ptr(self.slice_ptr),
-                _lib.ptr(self.indptr), _lib.ptr(B), int(B.stride(0)), _lib.ptr(C), int(C.stride(0)), int(B.shape[1]),
-                _lib.stream_handle(self.vals.device),
-            ),
-            "fs_spmm_sell",
-        )
+        fn, name, args = self.spmm_call(B, C)
+        _lib.check(fn(*args), name)
 
     def spmv(self, x, y):
         _lib.check(

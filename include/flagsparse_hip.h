@@ -437,6 +437,24 @@ int fs_spmm_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_row
                  const int32_t* code_table, const int64_t* slice_ptr,
                  const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc,
                  int64_t n_dense, hipStream_t stream);
+/*
+ * fs_spmm_sell for a copy with offset codes (FS_SELL_C8), B staged through
+ * LDS: per (slice, column tile) a workgroup copies the B-row tiles its
+ * codes' windows cover (`offsets_host`: the n_codes offsets the codes stand
+ * for, host memory; `code_table`: the same 256-entry table on the device)
+ * with coalesced 16-byte loads, then sums every row from LDS in the same
+ * order as fs_spmm_sell (the same bits).  `n_b_rows` is B's row count.
+ * fs_spmm_sell_staged_fits says whether the offsets' bands (merged windows
+ * of 64 rows) fit: at most 32 bands within 64 KB of LDS.  The row-block SpMM
+ * that streams dense-B tiles through LDS, for banded and stencil matrices on
+ * the reference's prepared route (spmm_csr.py:134-237, 2040-2174).
+ */
+int fs_spmm_sell_staged_fits(int val_t, const int32_t* offsets_host, int n_codes, int64_t n_dense);
+int fs_spmm_sell_staged(int val_t, int ptr_t, int layout, int64_t n_rows, int64_t n_b_rows,
+                        const void* sell_vals, const void* sell_codes, const int32_t* code_table,
+                        const int32_t* offsets_host, int n_codes, const int64_t* slice_ptr,
+                        const void* indptr, const void* B, int64_t ldb, void* C, int64_t ldc,
+                        int64_t n_dense, hipStream_t stream);
 int fs_spmv_sell(int val_t, int sell_idx_t, int ptr_t, int layout, int64_t n_rows,
                  const void* sell_vals, const void* sell_cols,
                  const int32_t* code_table, const int64_t* slice_ptr,
