@@ -7,16 +7,21 @@
 // row ids, and build the new indptr with bincount + cumsum; conj is applied
 // to the data first (spmv_csr.py:615-618, spmm_csr.py:341-349).
 //
-// Here: an LSD radix sort over the column index, 8 bits per pass, over wave
-// sub-tiles of kSub entries held in registers.  Lanes holding equal digits
-// find each other with eight ballots ("peer masks"), so per-digit counts and
-// the stable rank of every entry come from popcounts: no atomics, and equal
-// keys keep their input order, which is what makes the result identical to
-// the reference's stable argsort.  Per pass: count -> exclusive scan over
-// [digit][sub-tile] -> scatter, which sorts each sub-tile by digit in LDS
-// first so that every digit's entries leave as one contiguous run.  The new
-// indptr is read off the sorted keys (colptr[c] = first position whose
-// key >= c).
+// Here: an LSD radix sort over the column index.  Within a tile, lanes
+// holding equal digits find each other with ballots ("peer masks") and take
+// their ranks from one returning LDS atomic per group, in input order, so
+// equal keys keep their input order: the result is the reference's stable
+// argsort, bit for bit.  Per pass: per-tile digit counts -> exclusive scan
+// over (digit, tile) -> a scatter that sorts the tile by digit in LDS first,
+// so that every digit's entries leave as one contiguous run.
+//  - 4- and 8-byte values (positions below 2^32): workgroup tiles of
+//    kWgTile entries, up to 11 key bits per pass, the (value, row) payload
+//    built by the first pass and written out by the last, the column pointer
+//    from integer atomic minima and a suffix minimum (wg_* kernels);
+//    COO -> CSR runs on the same passes (column, then row).
+//  - otherwise: wave tiles of kSub entries, up to 8 bits per pass, positions
+//    through the sort and a gather at the end, the column pointer read off
+//    the sorted keys (radix_* kernels).
 #include "fs_common.hpp"
 
 #include <algorithm>
