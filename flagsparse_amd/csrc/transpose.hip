@@ -860,10 +860,14 @@ __device__ inline void wg_rows(const P* __restrict__ rowptr, int64_t r0, int64_t
 // sub-tiles whose first entry lies in row r (one coalesced pass over the row
 // pointer instead of a binary search per sub-tile).  A malformed row pointer
 // can leave slots unwritten; the scatter clamps what it reads.
-template <class P>
+// (The same launch fills the column pointer with nnz, its start value for
+// the last pass's atomic minima: thread k < n_fill writes fill[k].)
+template <class P, class OP>
 __global__ __launch_bounds__(256) void wg_tile_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows,
-                                                           int64_t n_sub, int64_t* __restrict__ tile_row) {
+                                                           int64_t n_sub, int64_t* __restrict__ tile_row,
+                                                           OP* __restrict__ fill, int64_t n_fill, OP fill_value) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < n_fill) fill[r] = fill_value;
   if (r >= n_rows) return;
   const int64_t a = (int64_t)rowptr[r], b = (int64_t)rowptr[r + 1];
   int64_t sub = a <= 0 ? 0 : (a + kWgSub - 1) / kWgSub;
@@ -1242,12 +1246,28 @@ __global__ __launch_bounds__(256) void suffix_min_blocks_kernel(OP* __restrict__
   }
 }
 
+// scanned = 1: bsuf holds the suffix minima of the block minima; 0: the
+// block minima themselves, and each block takes the minimum of those after
+// it (a few thousand L2-resident reads per block, one launch less).
 template <class OP>
 __global__ __launch_bounds__(256) void suffix_min_down_kernel(OP* __restrict__ p, int64_t n,
-                                                              const OP* __restrict__ bsuf, int64_t n_blocks) {
+                                                              const OP* __restrict__ bsuf, int64_t n_blocks,
+                                                              int scanned) {
   __shared__ OP s[256];
   // the minimum over the blocks after this one (the last entry, nnz, bounds all)
   OP carry = (int64_t)blockIdx.x + 1 < n_blocks ? bsuf[blockIdx.x + 1] : p[n - 1];
+  if (!scanned) {
+    for (int64_t b = (int64_t)blockIdx.x + 2 + threadIdx.x; b < n_blocks; b += 256)
+      if (bsuf[b] < carry) carry = bsuf[b];
+    s[threadIdx.x] = carry;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+      if ((int)threadIdx.x < off && s[threadIdx.x + off] < s[threadIdx.x]) s[threadIdx.x] = s[threadIdx.x + off];
+      __syncthreads();
+    }
+    carry = s[0];
+    __syncthreads();
+  }
   // thread t owns kMinItems consecutive entries: its own suffix minima, then
   // the minimum over the threads after it
   const int64_t i0 = (int64_t)blockIdx.x * kMinTile + (int64_t)threadIdx.x * kMinItems;
@@ -1501,13 +1521,36 @@ template <class OP>
 int colptr_suffix_min(OP* colptr, int64_t n, OP* bmin, int64_t n_blocks, hipStream_t s) {
   hipLaunchKernelGGL((suffix_min_reduce_kernel<OP>), dim3((unsigned)n_blocks), dim3(256), 0, s, colptr, n, bmin);
   FS_CHECK_LAUNCH("suffix_min_reduce_kernel");
-  hipLaunchKernelGGL((suffix_min_blocks_kernel<OP>), dim3(1), dim3(256), 0, s, bmin, n_blocks);
-  FS_CHECK_LAUNCH("suffix_min_blocks_kernel");
+  const int scanned = n_blocks > 8192 ? 1 : 0;  // (few blocks: each reads the later minima itself)
+  if (scanned) {
+    hipLaunchKernelGGL((suffix_min_blocks_kernel<OP>), dim3(1), dim3(256), 0, s, bmin, n_blocks);
+    FS_CHECK_LAUNCH("suffix_min_blocks_kernel");
+  }
   hipLaunchKernelGGL((suffix_min_down_kernel<OP>), dim3((unsigned)n_blocks), dim3(256), 0, s, colptr, n, bmin,
-                     n_blocks);
+                     n_blocks, scanned);
   FS_CHECK_LAUNCH("suffix_min_down_kernel");
   return FS_OK;
 }
+
+// Passes for `bits` key bits (at least one): two passes up to 2 x 11 - 1
+// bits, beyond that at most 10 bits per pass.  Measured (ms): 22-bit C3
+// columns 1.92 in two 11-bit passes against 1.44 in three (8 + 7 + 7: runs
+// of 2048 digits are 3 entries long and the count table grows to 90 MB);
+// 21-bit R-MAT / stencil columns 1.03 / 1.23 in two against 1.12 / 1.53 in
+// three.  FLAGSPARSE_TRANSPOSE_PASS_BITS=8..11 caps the bits per pass (A/B).
+inline int wg_passes(int bits) {
+  int cap = bits <= 2 * kWgMaxBits - 1 ? kWgMaxBits : 10;
+  if (const char* e = std::getenv("FLAGSPARSE_TRANSPOSE_PASS_BITS")) {
+    const int v = std::atoi(e);
+    if (v >= 8 && v <= kWgMaxBits) cap = v;
+  }
+  return bits == 0 ? 1 : (bits + cap - 1) / cap;
+}
+
+template <class T>
+struct type_id {
+  using type = T;
+};
 
 template <int VW>
 int wg_launch_scatter(int mode, dim3 g, hipStream_t s, const void* kin, int kind, const void* pin, int64_t nnz,
@@ -1543,23 +1586,23 @@ int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, 
   const WgLayout L = make_wg_layout(n_cols, nnz);
   const int vw = val_t == FS_F32 ? 1 : 2;
   int64_t* tile_row = reinterpret_cast<int64_t*>(ws + L.off_tile_row);
-  if (ptr_t == FS_I32)
-    hipLaunchKernelGGL((wg_tile_rows_kernel<int32_t>), dim3((unsigned)ceil_div(n_rows, 256)), dim3(256), 0, s,
-                       static_cast<const int32_t*>(indptr), n_rows, L.n_sub, tile_row);
-  else
-    hipLaunchKernelGGL((wg_tile_rows_kernel<int64_t>), dim3((unsigned)ceil_div(n_rows, 256)), dim3(256), 0, s,
-                       static_cast<const int64_t*>(indptr), n_rows, L.n_sub, tile_row);
-  FS_CHECK_LAUNCH("wg_tile_rows_kernel");
   const int64_t n_ptr = n_cols + 1;
   const bool by_keys = colptr_from_keys();
-  if (!by_keys) {
-    if (op_t == FS_I32)
-      hipLaunchKernelGGL((fill_kernel<int32_t>), dim3((unsigned)ceil_div(n_ptr, 256)), dim3(256), 0, s,
-                         static_cast<int32_t*>(t_indptr), n_ptr, (int32_t)nnz);
-    else
-      hipLaunchKernelGGL((fill_kernel<int64_t>), dim3((unsigned)ceil_div(n_ptr, 256)), dim3(256), 0, s,
-                         static_cast<int64_t*>(t_indptr), n_ptr, (int64_t)nnz);
-    FS_CHECK_LAUNCH("fill_kernel");
+  {
+    // sub-tile rows, and (unless the keys give it) the column pointer filled with nnz
+    const int64_t n_fill = by_keys ? 0 : n_ptr;
+    const unsigned blocks = (unsigned)ceil_div(std::max(n_rows, n_fill), 256);
+    auto go = [&](auto ptag, auto otag) {
+      using P = typename decltype(ptag)::type;
+      using OP = typename decltype(otag)::type;
+      hipLaunchKernelGGL((wg_tile_rows_kernel<P, OP>), dim3(blocks), dim3(256), 0, s, static_cast<const P*>(indptr),
+                         n_rows, L.n_sub, tile_row, static_cast<OP*>(t_indptr), n_fill, (OP)nnz);
+    };
+    if (ptr_t == FS_I32 && op_t == FS_I32) go(type_id<int32_t>{}, type_id<int32_t>{});
+    else if (ptr_t == FS_I32) go(type_id<int32_t>{}, type_id<int64_t>{});
+    else if (op_t == FS_I32) go(type_id<int64_t>{}, type_id<int32_t>{});
+    else go(type_id<int64_t>{}, type_id<int64_t>{});
+    FS_CHECK_LAUNCH("wg_tile_rows_kernel");
   }
   WgIO io{vals,   indptr, ptr_t == FS_I64 ? 1 : 0, tile_row, n_rows, L.n_sub, t_vals, t_cols,
           oi_t == FS_I64 ? 1 : 0, by_keys ? nullptr : t_indptr, op_t == FS_I64 ? 1 : 0, n_cols,
@@ -1572,7 +1615,7 @@ int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, 
   void* pa = ws + L.off_pay_a;
   void* pb = ws + L.off_pay_b;
   const int bits = key_bits(n_cols);
-  const int passes = bits == 0 ? 1 : (bits + kWgMaxBits - 1) / kWgMaxBits;
+  const int passes = wg_passes(bits);
   const void* kin = cols;  // the CSR columns, then the keys of the previous pass
   int kind = idx_t == FS_I32 ? 0 : 1;
   const void* pin = nullptr;
@@ -2228,8 +2271,8 @@ int coo_to_csr_wg(char* ws, int val_t, int idx_t, int64_t n_rows, int64_t n_cols
   FS_CHECK_LAUNCH("fill_kernel");
   const int idx_kind = idx_t == FS_I32 ? 0 : 1;
   const int col_bits = key_bits(n_cols), row_bits = key_bits(n_rows);
-  const int col_passes = col_bits == 0 ? 0 : (col_bits + kWgMaxBits - 1) / kWgMaxBits;
-  const int row_passes = row_bits == 0 ? 1 : (row_bits + kWgMaxBits - 1) / kWgMaxBits;
+  const int col_passes = col_bits == 0 ? 0 : wg_passes(col_bits);
+  const int row_passes = wg_passes(row_bits);
   const int passes = col_passes + row_passes;
   // the first pass reads its keys from the columns (or, with one column,
   // from the rows) and its second index from the other array
