@@ -105,19 +105,25 @@ def transpose_out_dtypes(indices_dtype, indptr_dtype, n_rows, nnz):
     return out_index_dtype, out_indptr_dtype
 
 
-def transpose_csr(data, indices, indptr, shape, conj=False):
+def transpose_csr(data, indices, indptr, shape, conj=False, compact=False):
     """CSR of A^T (A^H when conj and complex): stable by column, on device.
 
-    Returns (t_data, t_indices, t_indptr, (n_cols, n_rows)).
+    Returns (t_data, t_indices, t_indptr, (n_cols, n_rows)).  The index
+    dtypes follow the reference's rules; compact=True (for a transpose that
+    stays inside an operator call) takes int32 wherever the values fit, which
+    the kernels then read at half the bytes.
     """
     n_rows, n_cols = int(shape[0]), int(shape[1])
     nnz = data.numel()
     device = data.device
     if data.dtype in (torch.float16, torch.bfloat16):
         # the permutation is exact through float32 (16-bit values round-trip)
-        td, ti, tp, tsh = transpose_csr(data.to(torch.float32), indices, indptr, shape, conj=False)
+        td, ti, tp, tsh = transpose_csr(data.to(torch.float32), indices, indptr, shape, conj=False, compact=compact)
         return td.to(data.dtype), ti, tp, tsh
     out_index_dtype, out_indptr_dtype = transpose_out_dtypes(indices.dtype, indptr.dtype, n_rows, nnz)
+    if compact:
+        out_index_dtype = torch.int32 if n_rows <= _INDEX_LIMIT_INT32 else torch.int64
+        out_indptr_dtype = torch.int32 if nnz <= _INDEX_LIMIT_INT32 else torch.int64
     t_indptr = torch.empty(n_cols + 1, dtype=out_indptr_dtype, device=device)
     if nnz == 0:
         t_indptr.zero_()

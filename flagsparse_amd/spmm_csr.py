@@ -188,7 +188,7 @@ def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False, defer=
 def _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending):
     """op(A) @ B for A^T / A^H queued behind a pending structure check; the
     check is finished (and raises) before C is returned."""
-    data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code)
+    data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=True)
     n_rows, n_cols = int(shape[0]), int(shape[1])
     plan = None
     if n_rows > 0:
@@ -199,11 +199,16 @@ def _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending)
     return C
 
 
-def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code):
-    """A (non), A^T (trans) or A^H (conj) as CSR (spmm_csr.py:341-349)."""
+def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=False):
+    """A (non), A^T (trans) or A^H (conj) as CSR (spmm_csr.py:341-349);
+    compact=True for a transpose that only this call's SpMM reads (int32
+    indices and row pointer wherever they fit)."""
     if op_code == SPMM_OP_NON:
         return data, indices, indptr, shape
-    return transpose_csr(data, indices, indptr, shape, conj=(op_code == SPMM_OP_CONJ_TRANS))
+    # (complex64 keeps int64 indices: its SpMM runs the int64-index kernel
+    # anyway, see _SpmmPlan.launch_indices)
+    compact = compact and data.dtype != torch.complex64
+    return transpose_csr(data, indices, indptr, shape, conj=(op_code == SPMM_OP_CONJ_TRANS), compact=compact)
 
 
 def _check_segment_override(max_row_nnz, block_nnz, max_segments):
@@ -469,7 +474,7 @@ def flagsparse_spmm_csr(
         torch.cuda.synchronize()
         t0 = time.perf_counter()
     if _spmm_op_transposes(op_code):
-        data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code)
+        data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=True)
         n_rows, n_cols = int(shape[0]), int(shape[1])
     if do_timing:
         torch.cuda.synchronize()

@@ -1241,7 +1241,8 @@ def _spmv_transposed_oneshot(data, indices, indptr, x, shape, op_code, index_fal
     if not _lib.lib().fs_csr_transpose_bounded(_lib.value_code(data.dtype), n_rows, n_cols, nnz):
         return None
     pending = _PendingCheck(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
-    td, ti, tp, tsh = transpose_csr(data, indices, indptr, (n_rows, n_cols), conj=(op_code == SPMV_OP_CONJ_TRANS))
+    td, ti, tp, tsh = transpose_csr(data, indices, indptr, (n_rows, n_cols), conj=(op_code == SPMV_OP_CONJ_TRANS),
+                                    compact=True)
     y = torch.empty(n_cols, dtype=data.dtype, device=data.device)
     flag_t = _oneshot_flags()
     rc = _oneshot_launch(td, ti, tp, x, y, n_cols, n_rows, flag_t)
