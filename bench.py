@@ -350,7 +350,7 @@ def run_config(name, args):
         lib = _lib.lib()
         tile_items, n_tiles, part = plan.tiling(data.dtype, n_dense)
         ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(data.dtype), n_tiles, n_dense), device)
-        launch_indices, launch_plan = plan.launch_indices(route.kernel_indices, route.data.dtype)
+        launch_indices, launch_plan = plan.launch_indices(route.kernel_indices, route.data.dtype, n_dense)
         args_abi = (
             launch_plan, _lib.ptr(route.data), _lib.ptr(launch_indices), _lib.ptr(route.kernel_indptr),
             _lib.ptr(B), n_dense, _lib.ptr(C), n_dense, n_dense, _lib.ptr(part), tile_items, n_tiles,

@@ -205,8 +205,8 @@ def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=Fals
     indices and row pointer wherever they fit)."""
     if op_code == SPMM_OP_NON:
         return data, indices, indptr, shape
-    # (complex64 keeps int64 indices: its SpMM runs the int64-index kernel
-    # anyway, see _SpmmPlan.launch_indices)
+    # (complex64 keeps int64 indices: its wide-B SpMM would widen them again,
+    # see _SpmmPlan.launch_indices)
     compact = compact and data.dtype != torch.complex64
     return transpose_csr(data, indices, indptr, shape, conj=(op_code == SPMM_OP_CONJ_TRANS), compact=compact)
 
@@ -301,17 +301,22 @@ class _SpmmPlan:
         tile_items = int(_lib.lib().fs_spmm_tile_items(_lib.value_code(_compute_dtype(value_dtype)), int(n_dense)))
         return tile_items, self.csr.n_tiles(tile_items), self.csr.partition(self.indptr, tile_items)
 
-    def launch_indices(self, indices, value_dtype):
+    def launch_indices(self, indices, value_dtype, n_dense=None):
         """(column indices, plan struct) a launch passes to fs_spmm_csr.
 
-        complex64 with int32 column indices runs the int64-index kernel on a
-        widened copy of the indices (built once per plan).  On gfx950 the
-        int32 instantiation of that kernel serialises its B-row gathers
-        behind waits for every outstanding load, which measured 10-34% slower
-        (R-MAT 2^20, N = 32 / 64 / 128: 1.29 / 1.69 / 2.93 ms, against 1.05 /
-        1.26 / 2.67 ms with int64 indices); for f32 / f64 int32 indices are as
-        fast or faster.  The widening costs one pass over the indices."""
-        if value_dtype != torch.complex64 or indices.dtype != torch.int32:
+        complex64 with int32 column indices and B rows of at least 512 bytes
+        (the merge-path kernel's launches) runs the int64-index kernel on a
+        widened copy of the indices (built once per plan): the int32
+        instantiation of that kernel serialises its B-row gathers behind
+        waits for outstanding loads (R-MAT 2^20, N = 64 / 128: 1.69 / 2.95
+        ms against 1.28 / 2.68 ms with int64 indices).  The lane-group
+        kernel (narrower B) runs as fast on int32 indices (N = 32: 0.73 /
+        0.74 ms), so those launches skip the widening pass (0.1 ms on 32 M
+        entries, which a per-call plan would pay every call).
+        FLAGSPARSE_SPMM_WIDEN_C64=0 never widens (A/B)."""
+        narrow_b = n_dense is not None and n_dense * 8 < 512
+        if (value_dtype != torch.complex64 or indices.dtype != torch.int32 or narrow_b
+                or os.environ.get("FLAGSPARSE_SPMM_WIDEN_C64", "1") == "0"):
             return indices, self.csr.plan
         if self._wide is None:
             wide_plan = _lib.FsCsrPlan()
@@ -365,7 +370,7 @@ def _hip_spmm(data, indices, indptr, B, n_rows, plan, out_dtype, C=None):
         C_k.zero_()
     else:
         plan.set_residency(indices, int(plan.csr.plan.n_cols), n_dense, cdt)
-        launch_indices, launch_plan = plan.launch_indices(indices, cdt)
+        launch_indices, launch_plan = plan.launch_indices(indices, cdt, n_dense)
         tile_items, n_tiles, part = plan.tiling(cdt, n_dense)
         lib = _lib.lib()
         ws = _lib.workspace(lib.fs_spmm_workspace_bytes(_lib.value_code(cdt), n_tiles, n_dense), device)

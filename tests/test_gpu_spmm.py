@@ -364,17 +364,21 @@ def test_spmm_skewed_columns_cap_residency_bit_identical(device, monkeypatch):
 
 @pytest.mark.parametrize("n_dense", [32, 64, 128])
 def test_spmm_complex64_int32_indices_run_widened(device, monkeypatch, n_dense):
-    """complex64 with int32 column indices launches the int64-index kernel on
-    a widened copy of the indices; the result is bit-identical to the int64
-    input's and matches the oracle."""
+    """complex64 with int32 column indices and B rows of at least 512 bytes
+    launches the int64-index kernel on a widened copy of the indices (narrower
+    B runs the int32 indices as they are); the result is bit-identical to the
+    int64 input's and matches the oracle."""
     for k in ("FLAGSPARSE_SPMM_WG_CAP", "FLAGSPARSE_SPMM_VEC", "FLAGSPARSE_SPMM_G", "FLAGSPARSE_SPMM_XCD"):
         monkeypatch.delenv(k, raising=False)
     d, i64, p, sh = S.rmat(14, dtype=torch.complex64, index_dtype=torch.int64, device=device, seed=9)
     B = S.dense(sh[1], n_dense, torch.complex64, device, seed=10, dist="normal")
     r32 = fs.prepare_spmm_csr_route(d, i64.to(torch.int32), p, sh)
     C32 = fs.flagsparse_spmm_csr_run(r32, B)
-    wide_indices, wide_plan = r32.hip_plan()._wide
-    assert wide_indices.dtype == torch.int64 and wide_plan.idx_t == 1
+    if n_dense * 8 >= 512:
+        wide_indices, wide_plan = r32.hip_plan()._wide
+        assert wide_indices.dtype == torch.int64 and wide_plan.idx_t == 1
+    else:
+        assert r32.hip_plan()._wide is None
     C64 = fs.flagsparse_spmm_csr_run(fs.prepare_spmm_csr_route(d, i64, p, sh), B)
     assert torch.equal(C32, C64)
     _check(d, i64.to(torch.int32), p, sh, B, "non")
