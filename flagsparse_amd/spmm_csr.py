@@ -188,7 +188,8 @@ def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False, defer=
 def _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending):
     """op(A) @ B for A^T / A^H queued behind a pending structure check; the
     check is finished (and raises) before C is returned."""
-    data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=True)
+    data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code,
+                                                            compact=_compact_ok(data, B))
     n_rows, n_cols = int(shape[0]), int(shape[1])
     plan = None
     if n_rows > 0:
@@ -199,15 +200,19 @@ def _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending)
     return C
 
 
+def _compact_ok(data, B):
+    """Whether this call's SpMM takes int32 indices as they are: all but
+    complex64 launches with B rows of at least 512 bytes, which would widen
+    them again (_SpmmPlan.launch_indices)."""
+    return not (data.dtype == torch.complex64 and int(B.shape[1]) * 8 >= 512)
+
+
 def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=False):
     """A (non), A^T (trans) or A^H (conj) as CSR (spmm_csr.py:341-349);
     compact=True for a transpose that only this call's SpMM reads (int32
     indices and row pointer wherever they fit)."""
     if op_code == SPMM_OP_NON:
         return data, indices, indptr, shape
-    # (complex64 keeps int64 indices: its wide-B SpMM would widen them again,
-    # see _SpmmPlan.launch_indices)
-    compact = compact and data.dtype != torch.complex64
     return transpose_csr(data, indices, indptr, shape, conj=(op_code == SPMM_OP_CONJ_TRANS), compact=compact)
 
 
@@ -479,7 +484,8 @@ def flagsparse_spmm_csr(
         torch.cuda.synchronize()
         t0 = time.perf_counter()
     if _spmm_op_transposes(op_code):
-        data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=True)
+        data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code,
+                                                                compact=_compact_ok(data, B))
         n_rows, n_cols = int(shape[0]), int(shape[1])
     if do_timing:
         torch.cuda.synchronize()
