@@ -567,11 +567,34 @@ __global__ __launch_bounds__(256) void spmv_stream_t_kernel(
 //     else row by row with the whole workgroup per row (long rows).
 // flags[0..3]: start, end, decrease, column (set to 1; zeroed by the host).
 // ---------------------------------------------------------------------------
-template <int SUBS, class V, class I, bool DL>
+// The DL stage copy (global -> LDS, asynchronous) of `cnt` entries from S;
+// returns the value / index offsets of S inside the staged 16-byte rows.
+template <class V, class I, class A>
+__device__ inline void oneshot_stage_dl(const V* __restrict__ vals, const I* __restrict__ cols, int64_t S, int cnt,
+                                        unsigned char* t_lds, int C, int& ov, int& oi) {
+  constexpr int NT = 256;
+  constexpr int CMAX = stream_items<A>();
+  constexpr int EV = 16 / (int)sizeof(V);
+  constexpr int EI = 16 / (int)sizeof(I);
+  const StreamTLayout L = stream_t_layout(C, sizeof(V), sizeof(I), true);
+  const int64_t Sv = S & ~(int64_t)(EV - 1);
+  const int64_t Si = S & ~(int64_t)(EI - 1);
+  ov = (int)(S - Sv);
+  oi = (int)(S - Si);
+  constexpr int KV = (CMAX + 2 * EV + NT * EV - 1) / (NT * EV);
+  constexpr int KI = (CMAX + 2 * EI + NT * EI - 1) / (NT * EI);
+  lds_copy16<NT / 64, KV>(reinterpret_cast<const unsigned char*>(vals + Sv), t_lds, (ov + cnt + EV - 1) / EV);
+  lds_copy16<NT / 64, KI>(reinterpret_cast<const unsigned char*>(cols + Si), t_lds + L.col_off,
+                          (oi + cnt + EI - 1) / EI);
+}
+
+// PRESTAGED (with DL): the caller issued oneshot_stage_dl already (offsets
+// ov0 / oi0), before its row-pointer phase, so the copy's latency overlaps it.
+template <int SUBS, class V, class I, bool DL, bool PRESTAGED = false>
 __device__ inline void oneshot_rows(const V* __restrict__ vals, const I* __restrict__ cols,
                                     const V* __restrict__ x, V* __restrict__ y, int64_t row0, int rows,
                                     int64_t S, int cnt, const int* s_off, unsigned char* t_lds, int C,
-                                    uint64_t n_cols, bool& bad) {
+                                    uint64_t n_cols, bool& bad, int ov0 = 0, int oi0 = 0) {
   using T = VT<V>;
   using A = typename T::acc;
   constexpr int NT = 256;
@@ -582,20 +605,9 @@ __device__ inline void oneshot_rows(const V* __restrict__ vals, const I* __restr
   V* s_val = reinterpret_cast<V*>(t_lds);
   I* s_col = reinterpret_cast<I*>(t_lds + L.col_off);
   const int t = threadIdx.x;
-  int ov = 0, oi = 0;
+  int ov = ov0, oi = oi0;
   if constexpr (DL) {
-    constexpr int EV = 16 / (int)sizeof(V);
-    constexpr int EI = 16 / (int)sizeof(I);
-    const int64_t Sv = S & ~(int64_t)(EV - 1);
-    const int64_t Si = S & ~(int64_t)(EI - 1);
-    ov = (int)(S - Sv);
-    oi = (int)(S - Si);
-    constexpr int KV = (CMAX + 2 * EV + NT * EV - 1) / (NT * EV);
-    constexpr int KI = (CMAX + 2 * EI + NT * EI - 1) / (NT * EI);
-    lds_copy16<NT / 64, KV>(reinterpret_cast<const unsigned char*>(vals + Sv), reinterpret_cast<unsigned char*>(s_val),
-                            (ov + cnt + EV - 1) / EV);
-    lds_copy16<NT / 64, KI>(reinterpret_cast<const unsigned char*>(cols + Si), reinterpret_cast<unsigned char*>(s_col),
-                            (oi + cnt + EI - 1) / EI);
+    if constexpr (!PRESTAGED) oneshot_stage_dl<V, I, A>(vals, cols, S, cnt, t_lds, C, ov, oi);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS copies have landed
   } else {
     V v[K];
@@ -665,31 +677,41 @@ __global__ __launch_bounds__(256) void spmv_oneshot_kernel(
   // flags live in pinned host memory: system-scope stores reach it directly
   auto raise = [&](int k) { __hip_atomic_store(flags + k, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
   int* s_off = reinterpret_cast<int*>(t_lds + L.off_off);
-  __shared__ int64_t s_p[R + 1];
   __shared__ A s_red[4];
   const int t = threadIdx.x;
   const int64_t blk = logical_block(remap, n_blocks);
   if (blk < 0) return;  // whole workgroup
   const int64_t rb0 = blk * R;
   const int rows = n_rows - rb0 < R ? (int)(n_rows - rb0) : R;
-  if (t <= rows) s_p[t] = (int64_t)rowptr[rb0 + t];
-  __syncthreads();
-  if (t < rows && s_p[t + 1] < s_p[t]) raise(2);
-  if (t == 0 && blk == 0 && s_p[0] != 0) raise(0);
-  if (t == 0 && rb0 + rows == n_rows && s_p[rows] != nnz) raise(1);
-  // clamped into [S, E] within [0, nnz]: only the arrays' own entries are read
-  const int64_t S = s_p[0] < 0 ? 0 : (s_p[0] > nnz ? nnz : s_p[0]);
-  const int64_t E = s_p[rows] < S ? S : (s_p[rows] > nnz ? nnz : s_p[rows]);
+  // Row pointers: each of threads 0..rows loads its own and (below rows) the
+  // next one into registers first.  The block's entry range [S, E] comes
+  // from its first and last (uniform loads), clamped within [0, nnz], so
+  // only the arrays' own entries are read.  With DL and a range that fits
+  // the stage, the stage copy is issued next, before anything waits on the
+  // row-pointer loads, so its latency overlaps theirs and the checks.
+  int64_t my_p = 0, my_q = 0;
+  if (t <= rows) my_p = (int64_t)rowptr[rb0 + t];
+  if (t < rows) my_q = (int64_t)rowptr[rb0 + t + 1];
+  const int64_t p_lo = (int64_t)rowptr[rb0], p_hi = (int64_t)rowptr[rb0 + rows];
+  const int64_t S = p_lo < 0 ? 0 : (p_lo > nnz ? nnz : p_lo);
+  const int64_t E = p_hi < S ? S : (p_hi > nnz ? nnz : p_hi);
+  const int cnt = (int)(E - S);
+  int ov = 0, oi = 0;
+  if constexpr (DL) {
+    if (cnt <= C) oneshot_stage_dl<V, I, A>(vals, cols, S, cnt, t_lds, C, ov, oi);
+  }
+  if (t < rows && my_q < my_p) raise(2);
+  if (t == 0 && blk == 0 && p_lo != 0) raise(0);
+  if (t == 0 && rb0 + rows == n_rows && p_hi != nnz) raise(1);
   if (t <= rows) {
-    const int64_t v = s_p[t] < S ? S : (s_p[t] > E ? E : s_p[t]);
+    const int64_t v = my_p < S ? S : (my_p > E ? E : my_p);
     s_off[t] = (int)(v - S);
   }
   __syncthreads();
-  const int cnt = (int)(E - S);
   const uint64_t nc = (uint64_t)n_cols;
   bool bad = false;
   if (cnt <= C) {
-    oneshot_rows<4, V, I, DL>(vals, cols, x, y, rb0, rows, S, cnt, s_off, t_lds, C, nc, bad);
+    oneshot_rows<4, V, I, DL, DL>(vals, cols, x, y, rb0, rows, S, cnt, s_off, t_lds, C, nc, bad, ov, oi);
   } else {
     const int half = rows < 32 ? rows : 32;
     const int c0 = s_off[half] - s_off[0], c1 = s_off[rows] - s_off[half];
