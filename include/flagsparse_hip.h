@@ -296,8 +296,11 @@ int fs_spmm_csr_strided(const fs_csr_plan* plan, const void* vals, const void* c
  * (spmv_csr.py:477-515, spmm_csr.py:300-349) and the conj step
  * (spmv_csr.py:615-618, spmm_csr.py:341-349).  The result is identical to a
  * stable sort of the entries by column: within each output row the entries
- * keep ascending source-row order.  Built atomic-free by an LSD radix sort
- * on the column index (per-tile digit counts, scan, stable scatter).
+ * keep ascending source-row order.  Built by an LSD radix sort on the column
+ * index (per-tile digit counts, scan, stable scatter; no global atomics in
+ * the partition); for 4- and 8-byte values with positions below 2^32 the
+ * column pointer comes from integer atomic minima of each column's first
+ * position and a suffix minimum (order-independent, so deterministic).
  * Output types: out_idx_t / out_ptr_t (the reference's rules: indices keep
  * their type unless n_rows > 2^31-1, indptr keeps its type unless
  * nnz > 2^31-1).
