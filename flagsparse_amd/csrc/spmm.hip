@@ -307,7 +307,16 @@ __global__ __launch_bounds__(256) void spmm_fixup_kernel(
   for (int64_t col = (int64_t)blockIdx.y * 64 + (threadIdx.x & 63); col < n_dense;
        col += (int64_t)gridDim.y * 64) {
     A sum = tail[f * n_dense + col];
-    for (int64_t k = f + 1; k < t; ++k) sum = add(sum, tail[k * n_dense + col]);
+    // the tail fragments in sub-tile order, 8 loads in flight before they are added
+    int64_t k = f + 1;
+    for (; k + 8 <= t; k += 8) {
+      A v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = tail[(k + u) * n_dense + col];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum = add(sum, v[u]);
+    }
+    for (; k < t; ++k) sum = add(sum, tail[k * n_dense + col]);
     sum = add(sum, head[t * n_dense + col]);
     C[r0 * ldc + col] = T::out(sum);
   }
