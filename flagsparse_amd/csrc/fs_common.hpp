@@ -106,6 +106,36 @@ __device__ inline c64 add(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; 
 __device__ inline float add(float a, float b) { return a + b; }
 __device__ inline c32 add(c32 a, c32 b) { return c32{a.re + b.re, a.im + b.im}; }
 
+// Fix-up of a row that ends in tile t but starts before it: the tile where
+// it starts is the last f < t whose first row precedes r0 (part is
+// non-decreasing and part[t] == r0), or 0.  A binary search: a hub row
+// spanning many tiles is found in log steps, not one dependent load per tile.
+__device__ inline int64_t fixup_start_tile(const int64_t* __restrict__ part, int64_t t, int64_t r0) {
+  int64_t lo = 0, hi = t - 1;
+  if (part[hi] < r0) return hi;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (part[mid] < r0) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Sum of acc-typed fragments v[f..t) in order, 8 loads in flight at a time.
+template <class A>
+__device__ inline A sum_fragments(const A* __restrict__ v, int64_t stride, int64_t f, int64_t t, A sum) {
+  int64_t k = f;
+  for (; k + 8 <= t; k += 8) {
+    A w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = v[(k + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum = add(sum, w[u]);
+  }
+  for (; k < t; ++k) sum = add(sum, v[k * stride]);
+  return sum;
+}
+
 // Accumulation in the value type itself (float in float, complex64 in
 // complex64), as the reference's opt / alg1 / alg2 SpMM kernels accumulate
 // float32 data (spmm_csr.py:2792-3109, spmm_csr_opt_alg2.py:438-729); double
@@ -280,8 +310,6 @@ bool valid_types(int val_t, int idx_t, int ptr_t);
     if (_rc != FS_OK) return _rc;                           \
   } while (0)
 
-// FS_CHECK_LAUNCH for the main kernel of an entry point: also records its
-// name for fs_last_kernel().
 // Workgroup b of a 1-D grid of n, renumbered so that each of the 8 XCDs (to
 // which the hardware deals workgroups in turn) walks one contiguous range:
 // a bijection on [0, n).
@@ -291,6 +319,8 @@ __device__ inline int64_t xcd_range_block(uint32_t b, uint32_t n) {
   return x < r ? (int64_t)x * (q + 1) + i : (int64_t)r * (q + 1) + (int64_t)(x - r) * q + i;
 }
 
+// FS_CHECK_LAUNCH for the main kernel of an entry point: also records its
+// name for fs_last_kernel().
 #define FS_CHECK_MAIN_LAUNCH(name)                          \
   do {                                                      \
     int _rc = ::fs::check_hip(hipGetLastError(), name);     \

@@ -290,21 +290,11 @@ __global__ __launch_bounds__(256) void spmm_group_fixup_kernel(
   const int64_t start = ptr64 ? static_cast<const int64_t*>(rowptr_raw)[r0]
                               : (int64_t) static_cast<const int32_t*>(rowptr_raw)[r0];
   if (start >= n0) return;
-  int64_t f = t - 1;
-  while (f > 0 && part[f] == r0) --f;
+  const int64_t f = fixup_start_tile(part, t, r0);
   for (int64_t col = (int64_t)blockIdx.y * 64 + (threadIdx.x & 63); col < n_dense;
        col += (int64_t)gridDim.y * 64) {
     A sum = tail[f * n_dense + col];
-    // the tail fragments in sub-tile order, 8 loads in flight before they are added
-    int64_t k = f + 1;
-    for (; k + 8 <= t; k += 8) {
-      A v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = tail[(k + u) * n_dense + col];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) sum = add(sum, v[u]);
-    }
-    for (; k < t; ++k) sum = add(sum, tail[k * n_dense + col]);
+    sum = sum_fragments(tail + col, n_dense, f + 1, t, sum);  // in sub-tile order
     sum = add(sum, head[t * n_dense + col]);
     C[r0 * scm + col * scn] = T::out(sum);
   }

@@ -864,10 +864,8 @@ __global__ __launch_bounds__(256) void nnz_fixup_kernel(const P* __restrict__ ro
   const int64_t ra = part[b];
   if (part[b + 1] == ra) return;                // owns no row
   if ((int64_t)rowptr[ra] >= b * C) return;     // first row begins inside
-  int64_t f = b - 1;
-  while (f > 0 && part[f] == ra) --f;           // blocks f..b-1 have tails for row ra
-  A sum = tail[f];
-  for (int64_t k = f + 1; k < b; ++k) sum = add(sum, tail[k]);
+  const int64_t f = fixup_start_tile(part, b, ra);  // blocks f..b-1 have tails for row ra
+  const A sum = sum_fragments(tail, 1, f + 1, b, tail[f]);
   y[ra] = T::out(add(sum, head[b]));
 }
 
@@ -1389,10 +1387,8 @@ __global__ __launch_bounds__(256) void merge_fixup_kernel(
   if (part[t + 1] == r0) return;  // tile holds no row end
   const int64_t n0 = t * tile_items - r0;
   if ((int64_t)rowptr[r0] >= n0) return;  // row r0 starts inside tile t
-  int64_t f = t - 1;
-  while (f > 0 && part[f] == r0) --f;
-  A sum = tail[f];
-  for (int64_t k = f + 1; k < t; ++k) sum = add(sum, tail[k]);
+  const int64_t f = fixup_start_tile(part, t, r0);
+  A sum = sum_fragments(tail, 1, f + 1, t, tail[f]);
   sum = add(sum, head[t]);
   store_row<V>(y, r0, sum);
 }
