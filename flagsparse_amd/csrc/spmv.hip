@@ -459,6 +459,31 @@ __device__ inline void lds_copy16(const unsigned char* g, unsigned char* dst, in
   }
 }
 
+// One lane's walk over its slots of a staged row [a, b): entries sub,
+// sub + SUBS, ... into four partial sums, four slots per step.  A step past
+// the row's end reads its last entry again (an index clamped to b - 1), so
+// every LDS read and gather is issued unconditionally and all four gathers
+// are in flight together; the sums of such slots are computed and dropped,
+// so each partial sum adds exactly the row's own slots, in order.  `guard`
+// maps each column before its gather.
+template <int SUBS, class T, class V, class I, class A, class G>
+__device__ inline void slot_walk(const I* sc, const V* sv, const V* __restrict__ x, int a, int b, int sub, A& acc0,
+                                 A& acc1, A& acc2, A& acc3, G guard) {
+  const int e = b - 1;
+  for (int q = a + sub; q < b; q += 4 * SUBS) {
+    const int q1 = q + SUBS < e ? q + SUBS : e, q2 = q + 2 * SUBS < e ? q + 2 * SUBS : e,
+              q3 = q + 3 * SUBS < e ? q + 3 * SUBS : e;
+    const I c0 = guard(sc[q]), c1 = guard(sc[q1]), c2 = guard(sc[q2]), c3 = guard(sc[q3]);
+    const V x0 = x[c0], x1 = x[c1], x2 = x[c2], x3 = x[c3];
+    const V v0 = sv[q], v1 = sv[q1], v2 = sv[q2], v3 = sv[q3];
+    acc0 = T::fma(v0, x0, acc0);
+    const A n1 = T::fma(v1, x1, acc1), n2 = T::fma(v2, x2, acc2), n3 = T::fma(v3, x3, acc3);
+    if (q + SUBS < b) acc1 = n1;
+    if (q + 2 * SUBS < b) acc2 = n2;
+    if (q + 3 * SUBS < b) acc3 = n3;
+  }
+}
+
 // SUBS lanes per row (4, 8, 16, 32 or 64): a 256-thread workgroup owns
 // 256 / SUBS rows, so rows of up to stream_items / (256 / SUBS) entries fit
 // the stage (f64: 32 entries at 4 lanes per row, 512 at 64).
@@ -533,16 +558,7 @@ __global__ __launch_bounds__(256) void spmv_stream_t_kernel(
     const int a = s_off[r], b = s_off[r + 1];
     const I* sc = s_col + oi;
     const V* sv = s_val + ov;
-    for (int q = a + sub; q < b; q += 4 * SUBS) {  // up to four gathers in flight per lane
-      const bool h1 = q + SUBS < b, h2 = q + 2 * SUBS < b, h3 = q + 3 * SUBS < b;
-      const I c0 = sc[q], c1 = h1 ? sc[q + SUBS] : c0, c2 = h2 ? sc[q + 2 * SUBS] : c0,
-              c3 = h3 ? sc[q + 3 * SUBS] : c0;
-      const V x0 = x[c0], x1 = x[c1], x2 = x[c2], x3 = x[c3];
-      acc0 = T::fma(sv[q], x0, acc0);
-      if (h1) acc1 = T::fma(sv[q + SUBS], x1, acc1);
-      if (h2) acc2 = T::fma(sv[q + 2 * SUBS], x2, acc2);
-      if (h3) acc3 = T::fma(sv[q + 3 * SUBS], x3, acc3);
-    }
+    slot_walk<SUBS, T>(sc, sv, x, a, b, sub, acc0, acc1, acc2, acc3, [](I c) { return c; });
   }
   A acc = add(add(acc0, acc1), add(acc2, acc3));
 #pragma unroll
@@ -558,7 +574,8 @@ __global__ __launch_bounds__(256) void spmv_stream_t_kernel(
 //   - every workgroup reads its 65 row pointers (it needs them anyway) and
 //     flags a start other than 0 (first block), an end other than nnz (last
 //     block) and any decrease; every gathered column outside [0, n_cols)
-//     is flagged and read as column 0, so no access leaves the arrays;
+//     is flagged and read as the last column, so no access leaves the
+//     arrays;
 //   - row pointers are clamped into [0, nnz] before use, so a malformed
 //     matrix is computed on garbage but never read out of bounds; the host
 //     raises the reference's error for any flag and discards y;
@@ -569,6 +586,23 @@ __global__ __launch_bounds__(256) void spmv_stream_t_kernel(
 // ---------------------------------------------------------------------------
 // The DL stage copy (global -> LDS, asynchronous) of `cnt` entries from S;
 // returns the value / index offsets of S inside the staged 16-byte rows.
+// Column range check of the one-shot kernel: column c is in [0, n_cols)
+// iff (U)c <= last (for int32 columns `last` is capped at INT32_MAX, so a
+// negative column, at or above 2^31 as unsigned, is out of range for any
+// n_cols).
+template <class I>
+struct ColGuard;
+template <>
+struct ColGuard<int32_t> {
+  using U = uint32_t;
+  __device__ static U last(uint64_t n_cols) { return n_cols - 1 > 0x7fffffffull ? 0x7fffffffu : (U)(n_cols - 1); }
+};
+template <>
+struct ColGuard<int64_t> {
+  using U = uint64_t;
+  __device__ static U last(uint64_t n_cols) { return n_cols - 1; }
+};
+
 template <class V, class I, class A>
 __device__ inline void oneshot_stage_dl(const V* __restrict__ vals, const I* __restrict__ cols, int64_t S, int cnt,
                                         unsigned char* t_lds, int C, int& ov, int& oi) {
@@ -634,33 +668,35 @@ __device__ inline void oneshot_rows(const V* __restrict__ vals, const I* __restr
   const int r = (t >> 6) * RPW + lane % RPW;
   const int sub = lane / RPW;
   A acc0 = T::zero(), acc1 = T::zero(), acc2 = T::zero(), acc3 = T::zero();
+  // Columns as unsigned: a negative one is above `last`, like one past the
+  // end.  Each is clamped to `last` for its gather and folded into a running
+  // maximum that is tested once, after the walk.
+  using U = typename ColGuard<I>::U;
+  const U last = ColGuard<I>::last(n_cols);
+  U cmax = 0;
   auto guard = [&](I c) -> I {
-    if ((uint64_t)(int64_t)c >= n_cols) {
-      bad = true;
-      return (I)0;
-    }
-    return c;
+    const U u = (U)c;
+    cmax = u > cmax ? u : cmax;
+    return (I)(u < last ? u : last);
   };
   if (r < rows) {
     const int a = s_off[r], b = s_off[r + 1];
     const I* sc = s_col + oi;
     const V* sv = s_val + ov;
-    for (int q = a + sub; q < b; q += 4 * SUBS) {
-      const bool h1 = q + SUBS < b, h2 = q + 2 * SUBS < b, h3 = q + 3 * SUBS < b;
-      const I c0 = guard(sc[q]), c1 = h1 ? guard(sc[q + SUBS]) : c0, c2 = h2 ? guard(sc[q + 2 * SUBS]) : c0,
-              c3 = h3 ? guard(sc[q + 3 * SUBS]) : c0;
-      const V x0 = x[c0], x1 = x[c1], x2 = x[c2], x3 = x[c3];
-      acc0 = T::fma(sv[q], x0, acc0);
-      if (h1) acc1 = T::fma(sv[q + SUBS], x1, acc1);
-      if (h2) acc2 = T::fma(sv[q + 2 * SUBS], x2, acc2);
-      if (h3) acc3 = T::fma(sv[q + 3 * SUBS], x3, acc3);
-    }
+    slot_walk<SUBS, T>(sc, sv, x, a, b, sub, acc0, acc1, acc2, acc3, guard);
   }
   A acc = add(add(acc0, acc1), add(acc2, acc3));
 #pragma unroll
   for (int off = RPW; off < 64; off <<= 1) acc = add(acc, shfl(acc, lane ^ off));  // fixed order
   if (sub == 0 && r < rows) store_stream(y + row0 + r, T::out(acc));
+  if (cmax > last) bad = true;
   __syncthreads();  // the stage is reused by the caller
+}
+
+__device__ inline int64_t readlane_i64(int64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 template <class V, class I, class P, bool DL>
@@ -689,10 +725,16 @@ __global__ __launch_bounds__(256) void spmv_oneshot_kernel(
   // only the arrays' own entries are read.  With DL and a range that fits
   // the stage, the stage copy is issued next, before anything waits on the
   // row-pointer loads, so its latency overlaps theirs and the checks.
-  int64_t my_p = 0, my_q = 0;
-  if (t <= rows) my_p = (int64_t)rowptr[rb0 + t];
-  if (t < rows) my_q = (int64_t)rowptr[rb0 + t + 1];
-  const int64_t p_lo = (int64_t)rowptr[rb0], p_hi = (int64_t)rowptr[rb0 + rows];
+  // The loads are unconditional (threads past the block read its last row
+  // pointer) and converted only after all are issued: a load in a divergent
+  // branch, or one whose address waits on another, puts one memory latency
+  // after another before the stage copy can start.  Lane 63's raw_q is the
+  // block's last row pointer in every wave (rows <= 64).
+  const P raw_p = rowptr[rb0 + (t <= rows ? t : rows)];
+  const P raw_q = rowptr[rb0 + (t < rows ? t + 1 : rows)];
+  const P raw_lo = rowptr[rb0];
+  const int64_t my_p = (int64_t)raw_p, my_q = (int64_t)raw_q;
+  const int64_t p_lo = (int64_t)raw_lo, p_hi = readlane_i64(my_q, 63);
   const int64_t S = p_lo < 0 ? 0 : (p_lo > nnz ? nnz : p_lo);
   const int64_t E = p_hi < S ? S : (p_hi > nnz ? nnz : p_hi);
   const int cnt = (int)(E - S);
@@ -735,12 +777,10 @@ __global__ __launch_bounds__(256) void spmv_oneshot_kernel(
         const int a = s_off[r], b = s_off[r + 1];
         A acc = T::zero();
         for (int q = a + t; q < b; q += 256) {
-          I c = cols[S + q];
-          if ((uint64_t)(int64_t)c >= nc) {
-            bad = true;
-            c = (I)0;
-          }
-          acc = T::fma(vals[S + q], x[c], acc);
+          const auto u = (typename ColGuard<I>::U)cols[S + q];
+          const auto last = ColGuard<I>::last(nc);
+          if (u > last) bad = true;
+          acc = T::fma(vals[S + q], x[u < last ? u : last], acc);
         }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) acc = add(acc, shfl(acc, lane ^ off));  // fixed order

@@ -89,6 +89,32 @@ def test_oneshot_errors_leave_out_untouched(device):
     assert y is out and torch.all(out == 3.0)
 
 
+@pytest.mark.parametrize("kind", ["short", "halves", "long"])
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+def test_oneshot_column_check_on_every_block_path(device, monkeypatch, kind, index_dtype):
+    """A column below 0, at n_cols or far past it is flagged on each of the
+    three ways through a block (the kernel compares columns as unsigned and
+    clamps them for the gather); the last column itself is valid."""
+    monkeypatch.delenv("FLAGSPARSE_SPMV_ONESHOT", raising=False)
+    monkeypatch.delenv("FLAGSPARSE_SPMV_KERNEL", raising=False)
+    data, indices, indptr, sh = _matrix(kind, torch.float64, index_dtype, device)
+    x = S.vector(sh[1], torch.float64, device, seed=8)
+    row = 400 if kind == "long" else (indptr.numel() - 1) // 2  # row 400 has 5000 entries
+    k = int(indptr[row].item()) + 3
+    far = (1 << 31) - 1 if index_dtype == torch.int32 else 1 << 40
+    for bad in (-1, sh[1], far, -far):
+        c = indices.clone()
+        c[k] = bad
+        with pytest.raises(IndexError, match="indices out of range for n_cols"):
+            fs.flagsparse_spmv_csr(data, c, indptr, x, sh)
+        assert _lib.last_kernel() == "spmv_oneshot_kernel"
+    c = indices.clone()
+    c[k] = sh[1] - 1
+    y = fs.flagsparse_spmv_csr(data, c, indptr, x, sh)
+    ref = O.spmv_csr_wide(np_(data), np_(c), np_(indptr), np_(x), sh)
+    assert rel_err(np_(y), ref) <= REL_TOL[torch.float64]
+
+
 def test_oneshot_switch_off_runs_general_path(device, monkeypatch):
     data, indices, indptr, sh = S.uniform_rows(3000, 3000, 8, torch.float32, torch.int32, device, seed=5)
     x = S.vector(sh[1], torch.float32, device, seed=6)
