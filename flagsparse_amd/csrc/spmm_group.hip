@@ -106,12 +106,17 @@ __global__ __launch_bounds__(256) void spmm_group_kernel(
   // past a group's last nnz read B row 0.
   const int64_t col0_ld = valid > 0 ? col0 : 0;
 
-  // sub-tile coordinates (merge path)
+  // sub-tile coordinates (merge path).  The prologue's loads are
+  // unconditional, and each waits only on what its address needs: the
+  // partition entries, then at once the row pointers and the first entry
+  // chunks (a load in a branch is waited for at the branch's end).
+  const int64_t st_ld = live ? st : n_sub - 1;
+  const int64_t p0 = part[st_ld], p1 = part[st_ld + 1];
   int64_t r0 = 0, r1 = 0, n0 = 0;
   int nz = 0, R = 0;
   if (live) {
-    r0 = part[st];
-    r1 = part[st + 1];
+    r0 = p0;
+    r1 = p1;
     const int64_t d0 = st * (int64_t)sub_items;
     const int64_t total = n_rows + nnz;
     const int64_t dend = d0 + sub_items < total ? d0 + sub_items : total;
@@ -119,26 +124,18 @@ __global__ __launch_bounds__(256) void spmm_group_kernel(
     nz = (int)(dend - r1 - n0);
     R = (int)(r1 - r0);
   }
-  // row pointer entries (int32 or int64; the width only matters here, in the prologue)
+  // Row pointer entries, int32 or int64, by one 8-byte load either way: an
+  // int32 entry is read from the aligned 8-byte word that holds it (which
+  // never crosses a page).
   auto rp = [&](int64_t i) -> int64_t {
-    return ptr64 ? static_cast<const int64_t*>(rowptr_raw)[i] : (int64_t) static_cast<const int32_t*>(rowptr_raw)[i];
+    const unsigned char* a = static_cast<const unsigned char*>(rowptr_raw) + (i << (ptr64 ? 3 : 2));
+    const uintptr_t mis = (uintptr_t)a & 7;
+    const uint64_t w = *reinterpret_cast<const uint64_t*>(a - mis);
+    return ptr64 ? (int64_t)w : (int64_t)(int32_t)(uint32_t)(mis ? w >> 32 : w);
   };
-  const bool head_partial = R > 0 && rp(r0) < n0;
-  // row ends of the sub-tile -> LDS, as offsets from n0 (<= nz <= sub_items)
-  uint16_t* re_tab = lds_re + (size_t)((threadIdx.x >> 6) * G + g) * (size_t)sub_items;
-  for (int k = gl; k < R; k += LPR) re_tab[k] = (uint16_t)(rp(r0 + 1 + k) - n0);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int maxnz = nz;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) maxnz = max(maxnz, __shfl_xor(maxnz, off));
-  maxnz = __builtin_amdgcn_readfirstlane(maxnz);
 
   const I* colp = cols + n0;
   const V* valp = vals + n0;
-  const V* Bl = B + col0_ld * sbn;
-  const uint32_t row_bytes = (uint32_t)(sbk * (int64_t)sizeof(V));
   // Entry chunks: LPR entries per group, one per lane; chunk c + 1 is loaded
   // while chunk c is walked.  Every global load below is unconditional, so
   // the compiler counts the ones in flight exactly and waits for a gather
@@ -155,6 +152,39 @@ __global__ __launch_bounds__(256) void spmm_group_kernel(
   V valC, valN;
   load_chunk(0, colC, valC);
   load_chunk(1, colN, valN);
+
+  const int64_t row_start = rp(r0);
+  // row ends of the sub-tile -> LDS, as offsets from n0 (<= nz <= sub_items),
+  // four loads in flight per lane; the first four go out with the loads
+  // above (an index clamped to R - 1 reads a real entry, r0 itself when R
+  // is 0)
+  uint16_t* re_tab = lds_re + (size_t)((threadIdx.x >> 6) * G + g) * (size_t)sub_items;
+  auto row_ends = [&](int k0) {
+    int64_t e[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = k0 + u * LPR + gl;
+      e[u] = rp(r0 + 1 + (k < R ? k : R - 1));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = k0 + u * LPR + gl;
+      if (k < R) re_tab[k] = (uint16_t)(e[u] - n0);
+    }
+  };
+  row_ends(0);
+  for (int k0 = 4 * LPR; k0 < R; k0 += 4 * LPR) row_ends(k0);
+  const bool head_partial = R > 0 && row_start < n0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int maxnz = nz;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) maxnz = max(maxnz, __shfl_xor(maxnz, off));
+  maxnz = __builtin_amdgcn_readfirstlane(maxnz);
+
+  const V* Bl = B + col0_ld * sbn;
+  const uint32_t row_bytes = (uint32_t)(sbk * (int64_t)sizeof(V));
   int row = 0;
   int re = R > 0 ? (int)re_tab[0] : 0x7fffffff;
 

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import flagsparse_amd as fs
+from flagsparse_amd import _lib
 from flagsparse_amd import synthetic as S
 from oracle import csr_oracle as O
 from tests._helpers import ELEM_TOL, INDEX_DTYPES, INDEX_IDS, OPS, REL_TOL, VALUE_DTYPES, VALUE_IDS, np_, rel_err
@@ -64,6 +65,31 @@ def test_spmm_matches_oracle(lane_layout, device, dtype, index_dtype, op, n_dens
                                long_rows=((300, 330),))
     B = S.dense(m if op != "non" else k, n_dense, dtype, device, seed=5)
     _check(d, i, p, sh, B, op)
+
+
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+@pytest.mark.parametrize("lpr", ["16", "32"])
+def test_spmm_group_row_pointer_view_at_odd_word(device, monkeypatch, index_dtype, lpr):
+    """The lane-group kernel reads row pointers by aligned 8-byte words: an
+    int32 row-pointer view that starts 4 bytes into its storage (entries in
+    the upper half of their words) gives the same result as a fresh copy,
+    with rows that cross sub-tiles (256 items per wave)."""
+    for k in _LAYOUT_ENV:
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("FLAGSPARSE_SPMM_KERNEL", "group")
+    monkeypatch.setenv("FLAGSPARSE_SPMM_LPR", lpr)
+    monkeypatch.setenv("FLAGSPARSE_SPMM_WAVE_ITEMS", "256")
+    d, i, p, sh = S.random_csr(1003, 517, 0.04, torch.float32, index_dtype, device, seed=11, empty_row_every=7,
+                               long_rows=((500, 510),))
+    store = torch.zeros(p.numel() + 1, dtype=p.dtype, device=device)
+    store[1:] = p
+    view = store[1:]
+    if p.dtype == torch.int32:
+        assert view.data_ptr() % 8 == 4
+    B = S.dense(517, 24, torch.float32, device, seed=2)
+    C = _check(d, i, view, sh, B, "non")
+    assert _lib.last_kernel() == "spmm_group_kernel"
+    assert torch.equal(C, fs.flagsparse_spmm_csr(d, i, p.clone(), B, sh))
 
 
 @pytest.mark.parametrize("M,N,K", [(8, 4, 16), (64, 16, 96)])
