@@ -987,7 +987,6 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
   constexpr int kWords = kWgMaxDigits / 2;  // counter words per wave
   __shared__ __attribute__((aligned(16))) uint8_t s_buf[kWgBufBytes];
   __shared__ uint32_t s_off[kWgMaxDigits];
-  __shared__ uint16_t s_dig[kWgTile];
   __shared__ int64_t s_wave[kWgWaves];
   const int nd = (int)mask + 1;
   const int t = threadIdx.x;
@@ -1134,37 +1133,41 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
     local[ch] += (my[digit >> 1] >> ((digit & 1u) * 16u)) & 0xffffu;
   }
   __syncthreads();
-  // keys (and digits) into the digit-sorted copy
+  // keys into the digit-sorted copy; then thread t takes sorted positions
+  // t, t + kWgThreads, ... and keeps their destinations in registers (the
+  // payload windows below overwrite the keys)
   uint32_t* s_key = reinterpret_cast<uint32_t*>(s_buf);
 #pragma unroll
-  for (int ch = 0; ch < kWgChunks; ++ch) {
-    if (ch * 64 + lane < cnt) {
-      s_key[local[ch]] = key[ch];
-      s_dig[local[ch]] = (uint16_t)((key[ch] >> shift) & mask);
-    }
-  }
+  for (int ch = 0; ch < kWgChunks; ++ch)
+    if (ch * 64 + lane < cnt) s_key[local[ch]] = key[ch];
   __syncthreads();
-  if (!kLast || io.colptr == nullptr) {
-    for (int i = t; i < tcnt; i += kWgThreads) keys_out[s_off[s_dig[i]] + (uint32_t)i] = s_key[i];
-  } else {
-    // the first entry of each column in the tile: its position is a
-    // candidate for the column's start (the smallest over tiles wins)
-    for (int i = t; i < tcnt; i += kWgThreads) {
-      const uint32_t k = s_key[i];
-      if ((i == 0 || s_key[i - 1] != k) && (int64_t)k < io.n_cols) {
-        const uint32_t dst = s_off[s_dig[i]] + (uint32_t)i;
+  static_assert(kWgTile == (int64_t)kWgChunks * kWgThreads, "one sorted position per thread and chunk");
+  uint32_t dst[kWgChunks];
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch) {
+    const int i = t + ch * kWgThreads;
+    const uint32_t k = i < tcnt ? s_key[i] : 0u;
+    dst[ch] = s_off[(k >> shift) & mask] + (uint32_t)i;
+    if (i < tcnt) {
+      if (!kLast || io.colptr == nullptr) {
+        keys_out[dst[ch]] = k;
+      } else if ((i == 0 || s_key[i - 1] != k) && (int64_t)k < io.n_cols) {
+        // the first entry of each column in the tile: its position is a
+        // candidate for the column's start (the smallest over tiles wins)
         if (io.op64)
-          __hip_atomic_fetch_min(static_cast<uint64_t*>(io.colptr) + k, (uint64_t)dst, __ATOMIC_RELAXED,
+          __hip_atomic_fetch_min(static_cast<uint64_t*>(io.colptr) + k, (uint64_t)dst[ch], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
         else
-          __hip_atomic_fetch_min(static_cast<uint32_t*>(io.colptr) + k, dst, __ATOMIC_RELAXED,
+          __hip_atomic_fetch_min(static_cast<uint32_t*>(io.colptr) + k, dst[ch], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
   __syncthreads();
-  // the payload, in windows of the buffer
+  // the payload, in windows of the buffer (each window holds whole rounds
+  // of sorted positions, so a thread's positions stay its own)
   constexpr int kWin = kWgBufBytes / (int)sizeof(Pay);
+  static_assert(kWin % kWgThreads == 0, "windows hold whole rounds of sorted positions");
   Pay* s_pay = reinterpret_cast<Pay*>(s_buf);
   for (int w0 = 0; w0 < tcnt; w0 += kWin) {
 #pragma unroll
@@ -1174,22 +1177,24 @@ __global__ __launch_bounds__(kWgThreads, FS_WG_MIN_WAVES) void wg_scatter_kernel
     }
     __syncthreads();
     const int w1 = w0 + kWin < tcnt ? w0 + kWin : tcnt;
-    for (int i = w0 + t; i < w1; i += kWgThreads) {
-      const uint32_t dst = s_off[s_dig[i]] + (uint32_t)i;
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) {
+      const int i = t + ch * kWgThreads;
+      if (i < w0 || i >= w1) continue;
       const Pay v = s_pay[i - w0];
       if constexpr (kLast) {
         uint32_t r;
         if constexpr (VW == 1) {
-          static_cast<uint32_t*>(io.t_vals)[dst] = (uint32_t)v;
+          static_cast<uint32_t*>(io.t_vals)[dst[ch]] = (uint32_t)v;
           r = (uint32_t)(v >> 32);
         } else {
-          static_cast<uint2*>(io.t_vals)[dst] = make_uint2(v.v0, v.v1 ^ io.conj_mask);
+          static_cast<uint2*>(io.t_vals)[dst[ch]] = make_uint2(v.v0, v.v1 ^ io.conj_mask);
           r = v.r;
         }
-        if (io.oi64) static_cast<int64_t*>(io.t_cols)[dst] = (int64_t)r;
-        else static_cast<int32_t*>(io.t_cols)[dst] = (int32_t)r;
+        if (io.oi64) static_cast<int64_t*>(io.t_cols)[dst[ch]] = (int64_t)r;
+        else static_cast<int32_t*>(io.t_cols)[dst[ch]] = (int32_t)r;
       } else {
-        pay_out[dst] = v;
+        pay_out[dst[ch]] = v;
       }
     }
     __syncthreads();
