@@ -408,3 +408,21 @@ def test_spmm_complex64_int32_indices_run_widened(device, monkeypatch, n_dense):
     C64 = fs.flagsparse_spmm_csr_run(fs.prepare_spmm_csr_route(d, i64, p, sh), B)
     assert torch.equal(C32, C64)
     _check(d, i64.to(torch.int32), p, sh, B, "non")
+
+
+@pytest.mark.parametrize("layout", ["group", "merge"])
+def test_spmm_hub_rows_spanning_hundreds_of_tiles(device, monkeypatch, layout):
+    """Rows of 150,000 and 120,000 entries cross hundreds of sub-tiles (256
+    items per wave for the lane-group kernel): the fix-up finds where each
+    starts by a binary search over the partition and adds its fragments in
+    order."""
+    for k in _LAYOUT_ENV:
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("FLAGSPARSE_SPMM_KERNEL", layout)
+    if layout == "group":
+        monkeypatch.setenv("FLAGSPARSE_SPMM_WAVE_ITEMS", "256")
+    d, i, p, sh = S.random_csr(400, 200_000, 0.0005, torch.float32, torch.int32, device, seed=9,
+                               empty_row_every=11, long_rows=((7, 150_000), (200, 120_000)))
+    B = S.dense(200_000, 40, torch.float32, device, seed=4)
+    _check(d, i, p, sh, B, "non")
+    assert _lib.last_kernel() == ("spmm_group_kernel" if layout == "group" else "spmm_merge_kernel")

@@ -934,3 +934,18 @@ def test_spmv_transposed_one_sync_matches_prepared(device, dtype, op):
     # a wrong x length still raises the reference's error, after the checks
     with pytest.raises(ValueError, match="x length"):
         fs.flagsparse_spmv_csr(d, i, p, S.vector(sh[1] + 1, dtype, device, seed=2), sh, op=op)
+
+
+@pytest.mark.parametrize("kernel", ["merge", "nnzblock"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.complex64], ids=["f32", "c64"])
+def test_spmv_hub_rows_spanning_hundreds_of_tiles(device, monkeypatch, kernel, dtype):
+    """Rows of 150,000 and 120,000 entries cross hundreds of tiles: the
+    fix-up finds where each starts (a binary search over the partition) and
+    adds its fragments in tile order."""
+    monkeypatch.setenv("FLAGSPARSE_SPMV_KERNEL", kernel)
+    data, indices, indptr, sh = S.random_csr(400, 200_000, 0.0005, dtype, torch.int32, device, seed=9,
+                                             empty_row_every=11, long_rows=((7, 150_000), (200, 120_000)))
+    x = S.vector(sh[1], dtype, device, seed=3)
+    y = fs.flagsparse_spmv_csr(data, indices, indptr, x, sh)
+    ref = O.spmv_csr_wide(np_(data), np_(indices), np_(indptr), np_(x), sh)
+    assert rel_err(np_(y), ref) <= REL_TOL[dtype]
