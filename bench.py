@@ -461,8 +461,11 @@ def _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for, ste
     import torch
 
     call = lambda: fs.flagsparse_spmv_csr(data, indices, indptr, x, shape)  # noqa: E731
-    for _ in range(10):
-        call()
+    # the same untimed clock settle as the other legs (SETTLE_S of calls)
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(10):
+            call()
     kernel = _lib.last_kernel()
     n = max(20, steps)
     torch.cuda.synchronize()
