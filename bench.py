@@ -371,12 +371,11 @@ def run_config(name, args):
         if op != "non":
             # Public call including the per-call transpose (reference semantics).
             full = lambda: fs.flagsparse_spmm_csr(data, indices, indptr, B, shape, op=op)  # noqa: E731
-            for _ in range(3):
-                full()
+            settle(full)
             extra["ms_with_transpose"] = round(time_loop(full, max(5, args.steps // 4), stream), 4)
             # the transpose alone (fs_csr_transpose), as the public call runs it
             tr = lambda: _csr.transpose_csr(data, indices, indptr, shape, conj=(op == "conj"))  # noqa: E731
-            tr()
+            settle(tr)
             extra["transpose_ms"] = round(time_loop(tr, max(5, args.steps // 4), stream), 4)
 
     # Untimed clock settle (at least SETTLE_S of back-to-back steps: a step
@@ -451,6 +450,17 @@ def run_config(name, args):
     return line
 
 
+def settle(fn):
+    """Untimed calls of fn for at least SETTLE_S (the GPU clock ramp)."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+
+
 def _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for, steps, stream, device):
     """What an unprepared flagsparse_spmv_csr(data, indices, indptr, x, shape)
     costs per call, wall clock: the structure checks, the launch of the
@@ -461,11 +471,7 @@ def _one_shot_spmv(fs, _lib, data, indices, indptr, shape, x, bytes_alg_for, ste
     import torch
 
     call = lambda: fs.flagsparse_spmv_csr(data, indices, indptr, x, shape)  # noqa: E731
-    # the same untimed clock settle as the other legs (SETTLE_S of calls)
-    t_settle = time.perf_counter()
-    while time.perf_counter() - t_settle < SETTLE_S:
-        for _ in range(10):
-            call()
+    settle(call)  # the same untimed clock settle as the other legs
     kernel = _lib.last_kernel()
     n = max(20, steps)
     torch.cuda.synchronize()
