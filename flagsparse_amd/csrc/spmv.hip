@@ -584,8 +584,6 @@ __global__ __launch_bounds__(256) void spmv_stream_t_kernel(
 //     else row by row with the whole workgroup per row (long rows).
 // flags[0..3]: start, end, decrease, column (set to 1; zeroed by the host).
 // ---------------------------------------------------------------------------
-// The DL stage copy (global -> LDS, asynchronous) of `cnt` entries from S;
-// returns the value / index offsets of S inside the staged 16-byte rows.
 // Column range check of the one-shot kernel: column c is in [0, n_cols)
 // iff (U)c <= last (for int32 columns `last` is capped at INT32_MAX, so a
 // negative column, at or above 2^31 as unsigned, is out of range for any
@@ -603,6 +601,8 @@ struct ColGuard<int64_t> {
   __device__ static U last(uint64_t n_cols) { return n_cols - 1; }
 };
 
+// The DL stage copy (global -> LDS, asynchronous) of `cnt` entries from S;
+// returns the value / index offsets of S inside the staged 16-byte rows.
 template <class V, class I, class A>
 __device__ inline void oneshot_stage_dl(const V* __restrict__ vals, const I* __restrict__ cols, int64_t S, int cnt,
                                         unsigned char* t_lds, int C, int& ov, int& oi) {
