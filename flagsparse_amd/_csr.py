@@ -105,26 +105,37 @@ def transpose_out_dtypes(indices_dtype, indptr_dtype, n_rows, nnz):
     return out_index_dtype, out_indptr_dtype
 
 
-def transpose_csr(data, indices, indptr, shape, conj=False, compact=False):
+def transpose_csr(data, indices, indptr, shape, conj=False, compact=False, check=None):
     """CSR of A^T (A^H when conj and complex): stable by column, on device.
 
     Returns (t_data, t_indices, t_indptr, (n_cols, n_rows)).  The index
     dtypes follow the reference's rules; compact=True (for a transpose that
     stays inside an operator call) takes int32 wherever the values fit, which
-    the kernels then read at half the bytes.
+    the kernels then read at half the bytes.  check: a pending structure
+    check of this matrix (spmv_csr._PendingCheck) that the transpose runs in
+    its own passes where it can (fs_csr_transpose_checked), else queues first.
     """
     n_rows, n_cols = int(shape[0]), int(shape[1])
     nnz = data.numel()
     device = data.device
     if data.dtype in (torch.float16, torch.bfloat16):
         # the permutation is exact through float32 (16-bit values round-trip)
-        td, ti, tp, tsh = transpose_csr(data.to(torch.float32), indices, indptr, shape, conj=False, compact=compact)
+        td, ti, tp, tsh = transpose_csr(data.to(torch.float32), indices, indptr, shape, conj=False, compact=compact,
+                                        check=check)
         return td.to(data.dtype), ti, tp, tsh
     out_index_dtype, out_indptr_dtype = transpose_out_dtypes(indices.dtype, indptr.dtype, n_rows, nnz)
     if compact:
         out_index_dtype = torch.int32 if n_rows <= _INDEX_LIMIT_INT32 else torch.int64
         out_indptr_dtype = torch.int32 if nnz <= _INDEX_LIMIT_INT32 else torch.int64
     t_indptr = torch.empty(n_cols + 1, dtype=out_indptr_dtype, device=device)
+    lib = _lib.lib()
+    fused = None
+    if check is not None:
+        if nnz > 0 and n_rows > 0 and n_cols > 0 and lib.fs_csr_transpose_bounded(
+                _lib.value_code(data.dtype), n_rows, n_cols, nnz):
+            fused = check.fuse()
+        else:
+            check.queue()
     if nnz == 0:
         t_indptr.zero_()
         return (
@@ -135,9 +146,19 @@ def transpose_csr(data, indices, indptr, shape, conj=False, compact=False):
         )
     t_data = torch.empty_like(data)
     t_indices = torch.empty(nnz, dtype=out_index_dtype, device=device)
-    lib = _lib.lib()
     ws = _lib.workspace(lib.fs_csr_transpose_workspace_bytes(n_rows, n_cols, nnz), device)
     do_conj = 1 if (conj and _is_complex_dtype(data.dtype)) else 0
+    if fused is not None:
+        _lib.check(
+            lib.fs_csr_transpose_checked(
+                _lib.value_code(data.dtype), _lib.index_code(indices.dtype), _lib.index_code(indptr.dtype),
+                _lib.index_code(out_index_dtype), _lib.index_code(out_indptr_dtype), n_rows, n_cols, nnz,
+                _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr), do_conj, _lib.ptr(t_data), _lib.ptr(t_indices),
+                _lib.ptr(t_indptr), _lib.ptr(ws), ws.numel(), fused[0], fused[1], _lib.stream_handle(device),
+            ),
+            "fs_csr_transpose_checked",
+        )
+        return t_data, t_indices, t_indptr, (n_cols, n_rows)
     _lib.check(
         lib.fs_csr_transpose(
             _lib.value_code(data.dtype),

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "fs_csr_check",
     "fs_csr_check_enqueue",
     "fs_csr_transpose_bounded",
+    "fs_csr_transpose_checked",
     "fs_csr_check_decode",
     "fs_csr_check_analyze_bytes",
     "fs_csr_check_analyze",
@@ -182,6 +183,9 @@ def _declare(lib):
     lib.fs_csr_transpose.restype = _i32
     lib.fs_csr_transpose.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32,
                                      _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.fs_csr_transpose_checked.restype = _i32
+    lib.fs_csr_transpose_checked.argtypes = [_i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32,
+                                             _vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp]
     lib.fs_coo_to_csr_workspace_bytes.restype = _sz
     lib.fs_coo_to_csr_workspace_bytes.argtypes = [_i64, _i64, _i64]
     lib.fs_coo_to_csr.restype = _i32

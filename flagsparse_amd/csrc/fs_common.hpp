@@ -293,6 +293,12 @@ inline size_t lds_pad_for_cap(int wg_per_cu, size_t static_lds) {
   return share > static_lds ? std::min<size_t>(share - static_lds, 65536 - static_lds) : 0;
 }
 
+// Structure-check words (fs_csr_check_bytes): [0] indptr[0], [1]
+// indptr[n_rows], [2] rows whose pointer decreases, [3] / [4] the column
+// minimum / maximum, stored with the sign bit flipped so that unsigned
+// atomics order signed values.
+constexpr unsigned long long kSignFlip = 1ull << 63;
+
 // Type-code validation shared by every entry point.
 bool valid_types(int val_t, int idx_t, int ptr_t);
 

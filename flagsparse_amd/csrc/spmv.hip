@@ -133,7 +133,6 @@ __global__ __launch_bounds__(256) void stats_kernel(const P* __restrict__ rowptr
 // pointer decreases, [3] min column, [4] max column; the columns are stored
 // with the sign bit flipped so that the unsigned atomics order signed values.
 // ---------------------------------------------------------------------------
-constexpr unsigned long long kSignFlip = 1ull << 63;
 
 template <class P>
 __global__ void check_init_kernel(const P* __restrict__ rowptr, int64_t n_rows, unsigned long long* check) {

@@ -862,23 +862,74 @@ __device__ inline void wg_rows(const P* __restrict__ rowptr, int64_t r0, int64_t
 // can leave slots unwritten; the scatter clamps what it reads.
 // (The same launch fills the column pointer with nnz, its start value for
 // the last pass's atomic minima: thread k < n_fill writes fill[k].)
+// (With `check`, the fused structure check: each row whose pointer
+// decreases adds one to check[2].)
 template <class P, class OP>
 __global__ __launch_bounds__(256) void wg_tile_rows_kernel(const P* __restrict__ rowptr, int64_t n_rows,
                                                            int64_t n_sub, int64_t* __restrict__ tile_row,
-                                                           OP* __restrict__ fill, int64_t n_fill, OP fill_value) {
+                                                           OP* __restrict__ fill, int64_t n_fill, OP fill_value,
+                                                           unsigned long long* __restrict__ check) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r < n_fill) fill[r] = fill_value;
   if (r >= n_rows) return;
   const int64_t a = (int64_t)rowptr[r], b = (int64_t)rowptr[r + 1];
+  if (check != nullptr && b < a) atomicAdd(&check[2], 1ull);  // malformed input only
   int64_t sub = a <= 0 ? 0 : (a + kWgSub - 1) / kWgSub;
   const int64_t end = b <= 0 ? 0 : ((b + kWgSub - 1) / kWgSub < n_sub ? (b + kWgSub - 1) / kWgSub : n_sub);
   for (; sub < end; ++sub) tile_row[sub] = r;
 }
 
-// Per-tile digit counts, cnt[tile][nd] (nd = mask + 1 digits).
+// The fused structure check's column test over one lane's column values
+// (slots past a sub-tile hold 0): columns outside [0, n_cols) fold into the
+// sign-flipped minimum / maximum in check[3] / check[4], one pair of atomics
+// per wave that holds any, so a valid matrix issues none.  All lanes call it.
+__device__ inline void check_columns(const int64_t (&col)[kWgChunks], uint64_t n_cols, int lane,
+                                     unsigned long long* __restrict__ check) {
+  unsigned long long lo = ~0ull, hi = 0ull;
+#pragma unroll
+  for (int ch = 0; ch < kWgChunks; ++ch) {
+    if ((uint64_t)col[ch] >= n_cols) {
+      const unsigned long long f = (unsigned long long)col[ch] ^ kSignFlip;
+      lo = f < lo ? f : lo;
+      hi = f > hi ? f : hi;
+    }
+  }
+  if (__ballot(lo != ~0ull) != 0ull) {  // wave-uniform
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const unsigned long long olo = __shfl_xor(lo, off), ohi = __shfl_xor(hi, off);
+      lo = olo < lo ? olo : lo;
+      hi = ohi > hi ? ohi : hi;
+    }
+    if (lane == 0) {
+      atomicMin(&check[3], lo);
+      atomicMax(&check[4], hi);
+    }
+  }
+}
+
+// Fused structure check, first words: indptr[0], indptr[n_rows], no
+// decreasing row yet, and a column range of [0, 0] that only an entry
+// outside [0, n_cols) widens.
+template <class P>
+__global__ void fused_check_init_kernel(const P* __restrict__ rowptr, int64_t n_rows,
+                                        unsigned long long* __restrict__ check) {
+  const int k = threadIdx.x;
+  if (k == 0) check[0] = (unsigned long long)(int64_t)rowptr[0];
+  if (k == 1) check[1] = (unsigned long long)(int64_t)rowptr[n_rows];
+  if (k == 2) check[2] = 0ull;
+  if (k == 3 || k == 4) check[k] = kSignFlip;
+}
+
+// Per-tile digit counts, cnt[tile][nd] (nd = mask + 1 digits).  With
+// `check` (the first pass over CSR columns), also the fused structure
+// check's column test.  (16-byte key loads: C4's first count, the first read of
+// the columns, 51 -> 30 us.)
 __global__ __launch_bounds__(kWgThreads) void wg_count_kernel(const void* __restrict__ keys, int kind, int64_t n,
                                                               int shift, unsigned mask,
-                                                              uint32_t* __restrict__ counts) {
+                                                              uint32_t* __restrict__ counts,
+                                                              unsigned long long* __restrict__ check,
+                                                              int64_t n_cols) {
   __shared__ unsigned s_hist[kWgMaxDigits];
   const int nd = (int)mask + 1;
   const int lane = threadIdx.x & 63;
@@ -888,11 +939,51 @@ __global__ __launch_bounds__(kWgThreads) void wg_count_kernel(const void* __rest
   __syncthreads();
   const int64_t base = tile * kWgTile + (int64_t)w * kWgSub;
   const int cnt = n - base >= kWgSub ? (int)kWgSub : (n - base > 0 ? (int)(n - base) : 0);
+  // A full sub-tile of CSR columns (kinds 0 / 1) or keys (kind 2) is read
+  // with 16-byte loads in any order (a count needs no order); otherwise as
+  // the scatter reads it.
   uint32_t key[kWgChunks];
-  wg_load_keys(keys, kind, base, cnt, lane, key);
+  int64_t col[kWgChunks];  // column values, for the fused check
+  const bool checked = check != nullptr && kind <= 1;
+  static_assert(kWgChunks % 4 == 0, "a sub-tile is whole 16-byte loads per lane");
+  const bool full = cnt == (int)kWgSub && kind <= 2 && ((uintptr_t)keys % 16) == 0;
+  if (full && kind == 1) {
+    typedef int64_t L2 __attribute__((ext_vector_type(2)));
+    const L2* p = reinterpret_cast<const L2*>(static_cast<const int64_t*>(keys) + base) + lane;
+#pragma unroll
+    for (int k = 0; k < kWgChunks / 2; ++k) {
+      const L2 q = p[k * 64];
+      col[2 * k] = q[0];
+      col[2 * k + 1] = q[1];
+    }
+  } else if (full) {
+    typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+    const U4* p = reinterpret_cast<const U4*>(static_cast<const uint32_t*>(keys) + base) + lane;
+#pragma unroll
+    for (int k = 0; k < kWgChunks / 4; ++k) {
+      const U4 q = p[k * 64];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) col[4 * k + j] = kind == 0 ? (int64_t)(int32_t)q[j] : (int64_t)q[j];
+    }
+  } else if (checked) {
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) {
+      const int64_t q = base + ch * 64 + lane;
+      col[ch] = ch * 64 + lane >= cnt ? 0
+                : kind == 1            ? static_cast<const int64_t*>(keys)[q]
+                                       : (int64_t) static_cast<const int32_t*>(keys)[q];
+    }
+  }
+  if (full || checked) {
+#pragma unroll
+    for (int ch = 0; ch < kWgChunks; ++ch) key[ch] = (uint32_t)col[ch];
+  } else {
+    wg_load_keys(keys, kind, base, cnt, lane, key);
+  }
+  if (checked) check_columns(col, (uint64_t)n_cols, lane, check);
 #pragma unroll
   for (int ch = 0; ch < kWgChunks; ++ch)
-    if (ch * 64 + lane < cnt) atomicAdd(&s_hist[(key[ch] >> shift) & mask], 1u);
+    if (full || ch * 64 + lane < cnt) atomicAdd(&s_hist[(key[ch] >> shift) & mask], 1u);
   __syncthreads();
   for (int d = threadIdx.x; d < nd; d += kWgThreads) counts[tile * nd + d] = s_hist[d];
 }
@@ -1585,9 +1676,12 @@ int wg_launch_scatter(int mode, dim3 g, hipStream_t s, const void* kin, int kind
   return FS_OK;
 }
 
+// check (may be null): the fused structure check's five words, written by
+// the row-tile and first count kernels (bounded on any input, so the check
+// need not run first).
 int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, int64_t n_rows, int64_t n_cols,
                  int64_t nnz, const void* vals, const void* cols, const void* indptr, int conj, void* t_vals,
-                 void* t_cols, void* t_indptr, hipStream_t s) {
+                 void* t_cols, void* t_indptr, hipStream_t s, unsigned long long* check = nullptr) {
   const WgLayout L = make_wg_layout(n_cols, nnz);
   const int vw = val_t == FS_F32 ? 1 : 2;
   int64_t* tile_row = reinterpret_cast<int64_t*>(ws + L.off_tile_row);
@@ -1600,8 +1694,11 @@ int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, 
     auto go = [&](auto ptag, auto otag) {
       using P = typename decltype(ptag)::type;
       using OP = typename decltype(otag)::type;
+      if (check != nullptr)
+        hipLaunchKernelGGL((fused_check_init_kernel<P>), dim3(1), dim3(64), 0, s, static_cast<const P*>(indptr),
+                           n_rows, check);
       hipLaunchKernelGGL((wg_tile_rows_kernel<P, OP>), dim3(blocks), dim3(256), 0, s, static_cast<const P*>(indptr),
-                         n_rows, L.n_sub, tile_row, static_cast<OP*>(t_indptr), n_fill, (OP)nnz);
+                         n_rows, L.n_sub, tile_row, static_cast<OP*>(t_indptr), n_fill, (OP)nnz, check);
     };
     if (ptr_t == FS_I32 && op_t == FS_I32) go(type_id<int32_t>{}, type_id<int32_t>{});
     else if (ptr_t == FS_I32) go(type_id<int32_t>{}, type_id<int64_t>{});
@@ -1633,7 +1730,8 @@ int transpose_wg(char* ws, int val_t, int idx_t, int ptr_t, int oi_t, int op_t, 
     const int pbits = (bits - shift + (passes - p) - 1) / (passes - p);
     const unsigned mask = (1u << pbits) - 1u;
     const int nd = (int)mask + 1;
-    hipLaunchKernelGGL(wg_count_kernel, g, dim3(kWgThreads), 0, s, kin, kind, nnz, shift, mask, counts);
+    hipLaunchKernelGGL(wg_count_kernel, g, dim3(kWgThreads), 0, s, kin, kind, nnz, shift, mask, counts,
+                       p == 0 ? check : nullptr, n_cols);
     FS_CHECK_LAUNCH("wg_count_kernel");
     hipLaunchKernelGGL(wg_scan_reduce_kernel, dim3((unsigned)L.n_blocks), dim3(256), 0, s, counts, L.n_tiles, nd,
                        partial);
@@ -2248,6 +2346,38 @@ extern "C" int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t, 
   }
 }
 
+// fs_csr_transpose with the CSR structure check fused into its passes (the
+// row-tile kernel tests the row pointers, the first count pass the
+// columns): the five check words (fs_csr_check_bytes) are written to
+// check_dev and copied to host_words, on the stream, for
+// fs_csr_check_decode once it has drained.  For a valid matrix the decoded
+// column range is [0, 0]; outside [0, n_cols) it holds the offending
+// extremes.  Only where fs_csr_transpose_bounded holds (the transpose stays
+// in bounds on any input, so the check need not run first), with nnz > 0.
+extern "C" int fs_csr_transpose_checked(int val_t, int idx_t, int ptr_t, int out_idx_t, int out_ptr_t,
+                                        int64_t n_rows, int64_t n_cols, int64_t nnz, const void* vals,
+                                        const void* cols, const void* indptr, int conj, void* t_vals, void* t_cols,
+                                        void* t_indptr, void* ws, size_t ws_bytes, void* check_dev,
+                                        void* host_words, hipStream_t stream) {
+  if (!valid_types(val_t, idx_t, ptr_t) || !(out_idx_t == FS_I32 || out_idx_t == FS_I64) ||
+      !(out_ptr_t == FS_I32 || out_ptr_t == FS_I64))
+    return fail(FS_E_INVALID, "fs_csr_transpose_checked: bad type code");
+  if (n_rows <= 0 || n_cols <= 0 || nnz <= 0)
+    return fail(FS_E_INVALID, "fs_csr_transpose_checked: needs rows, columns and entries");
+  if (!fs_csr_transpose_bounded(val_t, n_rows, n_cols, nnz))
+    return fail(FS_E_INVALID, "fs_csr_transpose_checked: not a bounded transpose (check with fs_csr_check_enqueue)");
+  if (!vals || !cols || !indptr || !t_vals || !t_cols || !t_indptr || !check_dev || !host_words)
+    return fail(FS_E_INVALID, "fs_csr_transpose_checked: null pointer");
+  if (!ws || ws_bytes < make_wg_layout(n_cols, nnz).total)
+    return fail(FS_E_WORKSPACE, "fs_csr_transpose_checked: workspace too small");
+  unsigned long long* ck = static_cast<unsigned long long*>(check_dev);
+  const int rc = transpose_wg(static_cast<char*>(ws), val_t, idx_t, ptr_t, out_idx_t, out_ptr_t, n_rows, n_cols, nnz,
+                              vals, cols, indptr, conj, t_vals, t_cols, t_indptr, stream, ck);
+  if (rc != FS_OK) return rc;
+  FS_CHECK_HIP(hipMemcpyAsync(host_words, ck, 5 * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream));
+  return FS_OK;
+}
+
 // Key range of a COO matrix: n_rows * n_cols lexicographic keys.
 static Layout coo_layout(int64_t n_rows, int64_t n_cols, int64_t nnz) {
   const int64_t range = (n_cols > 0 && n_rows > INT64_MAX / n_cols) ? INT64_MAX : n_rows * n_cols;
@@ -2315,7 +2445,8 @@ int coo_to_csr_wg(char* ws, int val_t, int idx_t, int64_t n_rows, int64_t n_cols
       ckin = static_cast<const char*>(pin) + 4 * (vw == 1 ? 1 : 2);
       ckind = vw == 1 ? 5 : 6;  // the row word of the 8- / 12-byte payload
     }
-    hipLaunchKernelGGL(wg_count_kernel, g, dim3(kWgThreads), 0, s, ckin, ckind, nnz, shift, mask, counts);
+    hipLaunchKernelGGL(wg_count_kernel, g, dim3(kWgThreads), 0, s, ckin, ckind, nnz, shift, mask, counts,
+                       (unsigned long long*)nullptr, (int64_t)0);
     FS_CHECK_LAUNCH("wg_count_kernel");
     hipLaunchKernelGGL(wg_scan_reduce_kernel, dim3((unsigned)L.n_blocks), dim3(256), 0, s, counts, L.n_tiles, nd,
                        partial);

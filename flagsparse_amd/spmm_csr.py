@@ -176,7 +176,7 @@ def _prepare_spmm_csr_matrix(data, indices, indptr, shape, analyze=False, defer=
     indptr = indptr.contiguous()
     if defer and nnz > 0 and _lib.lib().fs_csr_transpose_bounded(
             _lib.value_code(_compute_dtype(data.dtype)), n_rows, n_cols, nnz):
-        return data, indices, indptr, n_rows, n_cols, _PendingCheck(data, indices, indptr, n_cols, messages)
+        return data, indices, indptr, n_rows, n_cols, _PendingCheck(data, indices, indptr, n_cols, messages, lazy=True)
     if analyze:
         # the row statistics ride on the structure check's round trip
         _, csr = _check_structure(data, indices, indptr, n_cols, messages, analyze=True)
@@ -189,7 +189,7 @@ def _spmm_transposed_deferred(data, indices, indptr, B, shape, op_code, pending)
     """op(A) @ B for A^T / A^H queued behind a pending structure check; the
     check is finished (and raises) before C is returned."""
     data, indices, indptr, shape = _materialize_spmm_csr_op(data, indices, indptr, shape, op_code,
-                                                            compact=_compact_ok(data, B))
+                                                            compact=_compact_ok(data, B), check=pending)
     n_rows, n_cols = int(shape[0]), int(shape[1])
     plan = None
     if n_rows > 0:
@@ -207,13 +207,17 @@ def _compact_ok(data, B):
     return not (data.dtype == torch.complex64 and int(B.shape[1]) * 8 >= 512)
 
 
-def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=False):
+def _materialize_spmm_csr_op(data, indices, indptr, shape, op_code, compact=False, check=None):
     """A (non), A^T (trans) or A^H (conj) as CSR (spmm_csr.py:341-349);
     compact=True for a transpose that only this call's SpMM reads (int32
-    indices and row pointer wherever they fit)."""
+    indices and row pointer wherever they fit); check: a pending structure
+    check that the transpose takes over (transpose_csr)."""
     if op_code == SPMM_OP_NON:
+        if check is not None:
+            check.queue()
         return data, indices, indptr, shape
-    return transpose_csr(data, indices, indptr, shape, conj=(op_code == SPMM_OP_CONJ_TRANS), compact=compact)
+    return transpose_csr(data, indices, indptr, shape, conj=(op_code == SPMM_OP_CONJ_TRANS), compact=compact,
+                         check=check)
 
 
 def _check_segment_override(max_row_nnz, block_nnz, max_segments):

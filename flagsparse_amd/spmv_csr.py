@@ -732,14 +732,15 @@ _check_local = threading.local()
 
 
 class _PendingCheck:
-    """A structure check whose answer is read later (fs_csr_check_enqueue):
-    the check pass and the copy of its five words into this thread's pinned
-    buffer are queued on the stream; finish() synchronises the stream and
-    raises the reference's error, if any."""
+    """A structure check whose answer is read later.  Queued at once
+    (fs_csr_check_enqueue), or, with lazy=True, handed to the transpose that
+    runs next (fuse(): fs_csr_transpose_checked tests the structure in its
+    own passes), or queued by finish() if neither happened.  finish()
+    synchronises the stream and raises the reference's error, if any."""
 
-    __slots__ = ("words", "nnz", "n_cols", "messages", "stream", "_ws")
+    __slots__ = ("words", "nnz", "n_cols", "messages", "stream", "_ws", "_indices", "_indptr", "_queued")
 
-    def __init__(self, data, indices, indptr, n_cols, messages):
+    def __init__(self, data, indices, indptr, n_cols, messages, lazy=False):
         words = getattr(_check_local, "words", None)
         if words is None:
             words = torch.zeros(5, dtype=torch.int64, pin_memory=True)
@@ -749,18 +750,38 @@ class _PendingCheck:
         self.n_cols = int(n_cols)
         self.messages = messages
         self.stream = torch.cuda.current_stream(indptr.device)
+        self._ws = _lib.workspace(_lib.lib().fs_csr_check_bytes(), indptr.device)
+        self._indices, self._indptr = indices, indptr
+        self._queued = False
+        if not lazy:
+            self.queue()
+
+    def queue(self):
+        """Queue the standalone check pass (once)."""
+        if self._queued:
+            return
         lib = _lib.lib()
-        self._ws = _lib.workspace(lib.fs_csr_check_bytes(), indptr.device)
+        indptr, indices = self._indptr, self._indices
         _lib.check(
             lib.fs_csr_check_enqueue(
                 _lib.ptr(indptr), _lib.index_code(indptr.dtype), _lib.ptr(indices) if self.nnz > 0 else None,
                 _lib.index_code(indices.dtype), indptr.numel() - 1, self.nnz, _lib.ptr(self._ws),
-                words.data_ptr(), _lib.stream_handle(indptr.device),
+                self.words.data_ptr(), _lib.stream_handle(indptr.device),
             ),
             "fs_csr_check_enqueue",
         )
+        self._queued = True
+
+    def fuse(self):
+        """(check_dev, host_words) for fs_csr_transpose_checked, which then
+        stands for the check pass; None when the check is already queued."""
+        if self._queued:
+            return None
+        self._queued = True
+        return _lib.ptr(self._ws), self.words.data_ptr()
 
     def finish(self):
+        self.queue()
         self.stream.synchronize()
         vals = (ctypes.c_int64 * 5)()
         _lib.check(_lib.lib().fs_csr_check_decode(self.words.data_ptr(), self.nnz, vals), "fs_csr_check_decode")
@@ -1240,9 +1261,9 @@ def _spmv_transposed_oneshot(data, indices, indptr, x, shape, op_code, index_fal
         return None
     if not _lib.lib().fs_csr_transpose_bounded(_lib.value_code(data.dtype), n_rows, n_cols, nnz):
         return None
-    pending = _PendingCheck(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES)
+    pending = _PendingCheck(data, indices, indptr, n_cols, _SPMV_STRUCT_MESSAGES, lazy=True)
     td, ti, tp, tsh = transpose_csr(data, indices, indptr, (n_rows, n_cols), conj=(op_code == SPMV_OP_CONJ_TRANS),
-                                    compact=True)
+                                    compact=True, check=pending)
     y = torch.empty(n_cols, dtype=data.dtype, device=data.device)
     flag_t = _oneshot_flags()
     rc = _oneshot_launch(td, ti, tp, x, y, n_cols, n_rows, flag_t)

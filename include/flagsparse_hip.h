@@ -317,6 +317,23 @@ size_t fs_csr_transpose_workspace_bytes(int64_t n_rows, int64_t n_cols,
  * transpose, spmm_csr.py:239-297).
  */
 int fs_csr_transpose_bounded(int val_t, int64_t n_rows, int64_t n_cols, int64_t nnz);
+/*
+ * fs_csr_transpose with fs_csr_check_enqueue fused into its passes: the
+ * reference's structure check (spmv_csr.py:546-558, spmm_csr.py:239-297)
+ * followed by its transpose (spmv_csr.py:477-515, spmm_csr.py:300-349), in
+ * one queue of kernels that reads the row pointer and the columns once for
+ * both.  The five check words go to `check_dev` (fs_csr_check_bytes) and,
+ * by an asynchronous copy, to the pinned `host_words`; after the caller has
+ * synchronised `stream`, fs_csr_check_decode gives fs_csr_check's values,
+ * except that a valid matrix reports its column range as [0, 0] (outside
+ * [0, n_cols) the range holds the offending extremes).  Only where
+ * fs_csr_transpose_bounded holds, with nnz > 0 (else FS_E_INVALID).
+ */
+int fs_csr_transpose_checked(int val_t, int idx_t, int ptr_t, int out_idx_t, int out_ptr_t,
+                             int64_t n_rows, int64_t n_cols, int64_t nnz, const void* vals,
+                             const void* cols, const void* indptr, int conj, void* t_vals,
+                             void* t_cols, void* t_indptr, void* ws, size_t ws_bytes,
+                             void* check_dev, void* host_words, hipStream_t stream);
 int fs_csr_transpose(int val_t, int idx_t, int ptr_t, int out_idx_t,
                      int out_ptr_t, int64_t n_rows, int64_t n_cols,
                      int64_t nnz, const void* vals, const void* cols,

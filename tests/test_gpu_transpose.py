@@ -135,3 +135,40 @@ def test_transpose_full_size_matches_stable_argsort(device, case):
     assert torch.equal(tp.to(torch.int64), rp)
     del tv, tc, tp, rv, rc, rp
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.complex64], ids=["f32", "f64", "c64"])
+@pytest.mark.parametrize("index_dtype", INDEX_DTYPES, ids=INDEX_IDS)
+def test_transpose_with_fused_check(device, dtype, index_dtype):
+    """fs_csr_transpose_checked: the transpose is bit-identical to
+    fs_csr_transpose, a valid matrix decodes as valid (column range [0, 0]),
+    and each fault is reported with the reference's error, whether the check
+    runs inside the transpose or is queued on its own (a check that no
+    transpose took over is queued by finish())."""
+    from flagsparse_amd.spmv_csr import _PendingCheck, _SPMV_STRUCT_MESSAGES
+
+    d, i, p, sh = S.random_csr(3000, 5000, 0.01, dtype, index_dtype, device, seed=5, empty_row_every=7,
+                               long_rows=((11, 4000),))
+    ref = _csr.transpose_csr(d, i, p, sh, conj=True)
+    pc = _PendingCheck(d, i, p, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)
+    got = _csr.transpose_csr(d, i, p, sh, conj=True, check=pc)
+    assert pc.finish() == (0, 0)
+    for a, b in zip(got[:3], ref[:3]):
+        assert torch.equal(a, b)
+    big = (1 << 40) if index_dtype == torch.int64 else (1 << 31) - 1
+    for col in (sh[1], -1, big, -big):
+        c = i.clone()
+        c[int(p[1500].item()) + 1] = col
+        pc = _PendingCheck(d, c, p, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)
+        _csr.transpose_csr(d, c, p, sh, check=pc)  # stays in bounds whatever the columns hold
+        with pytest.raises(IndexError, match="indices out of range"):
+            pc.finish()
+    bad = p.clone()
+    bad[2000] = bad[2001] + 5
+    pc = _PendingCheck(d, i, bad, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)
+    _csr.transpose_csr(d, i, bad, sh, check=pc)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        pc.finish()
+    pc = _PendingCheck(d, i, bad, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)  # never fused: finish() queues it
+    with pytest.raises(ValueError, match="non-decreasing"):
+        pc.finish()
