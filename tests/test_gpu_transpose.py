@@ -172,3 +172,49 @@ def test_transpose_with_fused_check(device, dtype, index_dtype):
     pc = _PendingCheck(d, i, bad, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)  # never fused: finish() queues it
     with pytest.raises(ValueError, match="non-decreasing"):
         pc.finish()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_fused_check_half_precision_and_mixed_widths(device, dtype):
+    """Half-precision values transpose through float32 and keep the fused
+    check; an int64 row pointer with int32 columns (and the reverse) reads
+    each width correctly in the row-tile and count passes."""
+    from flagsparse_amd.spmv_csr import _PendingCheck, _SPMV_STRUCT_MESSAGES
+
+    d, i, p, sh = S.random_csr(2000, 3000, 0.01, torch.float32, torch.int32, device, seed=8)
+    d = d.to(dtype)
+    for ii, pp in ((i, p.to(torch.int64)), (i.to(torch.int64), p)):
+        ref = _csr.transpose_csr(d, ii, pp, sh)
+        pc = _PendingCheck(d, ii, pp, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)
+        got = _csr.transpose_csr(d, ii, pp, sh, check=pc)
+        pc.finish()
+        for a, b in zip(got[:3], ref[:3]):
+            assert torch.equal(a, b)
+        c = ii.clone()
+        c[17] = sh[1] + 3
+        pc = _PendingCheck(d, c, pp, sh[1], _SPMV_STRUCT_MESSAGES, lazy=True)
+        _csr.transpose_csr(d, c, pp, sh, check=pc)
+        with pytest.raises(IndexError, match="indices out of range"):
+            pc.finish()
+
+
+def test_transpose_checked_abi_refusals(device):
+    """fs_csr_transpose_checked refuses what it cannot fuse: no entries, or a
+    value type without a bounded transpose (complex128)."""
+    from flagsparse_amd import _lib
+
+    lib = _lib.lib()
+    d, i, p, sh = S.random_csr(64, 64, 0.1, torch.complex128, torch.int32, device, seed=1)
+    nnz = d.numel()
+    td, ti, tp = torch.empty_like(d), torch.empty_like(i), torch.empty(sh[1] + 1, dtype=torch.int32, device=device)
+    ws = _lib.workspace(lib.fs_csr_transpose_workspace_bytes(sh[0], sh[1], nnz), device)
+    ck = _lib.workspace(lib.fs_csr_check_bytes(), device)
+    words = torch.zeros(5, dtype=torch.int64, pin_memory=True)
+    args = lambda vcode, n: (vcode, _lib.index_code(i.dtype), _lib.index_code(p.dtype), _lib.index_code(torch.int32),  # noqa: E731
+                             _lib.index_code(torch.int32), sh[0], sh[1], n, _lib.ptr(d), _lib.ptr(i), _lib.ptr(p), 0,
+                             _lib.ptr(td), _lib.ptr(ti), _lib.ptr(tp), _lib.ptr(ws), ws.numel(), _lib.ptr(ck),
+                             words.data_ptr(), _lib.stream_handle(device))
+    assert lib.fs_csr_transpose_bounded(_lib.value_code(d.dtype), sh[0], sh[1], nnz) == 0
+    assert lib.fs_csr_transpose_checked(*args(_lib.value_code(d.dtype), nnz)) != 0
+    assert "not a bounded transpose" in lib.fs_last_error().decode()
+    assert lib.fs_csr_transpose_checked(*args(_lib.value_code(torch.float64), 0)) != 0
