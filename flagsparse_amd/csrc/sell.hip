@@ -521,18 +521,23 @@ __global__ __launch_bounds__(256) void spmm_sell_kernel(const V* __restrict__ se
   const bool cvalid = col < n_dense;
   const int64_t col_ld = cvalid ? col : 0;
   const int64_t row0 = slice * kSellRows;
+  // Row lengths by unconditional loads (row indices clamped to n_rows, so a
+  // row past the matrix reads rowptr[n_rows] twice and gets length 0): all
+  // of them in flight at once, where loads under a row test had been waited
+  // for one by one.
+  auto row_len = [&](int64_t r) -> int {
+    const int64_t ra = r < n_rows ? r : n_rows, rb = r + 1 < n_rows ? r + 1 : n_rows;
+    return (int)((int64_t)rowptr[rb] - (int64_t)rowptr[ra]);
+  };
   int len[LPR];
 #pragma unroll
-  for (int k = 0; k < LPR; ++k) {
-    const int64_t r = row0 + sub + RW * k;
-    len[k] = r < n_rows ? (int)((int64_t)rowptr[r + 1] - (int64_t)rowptr[r]) : 0;
-  }
+  for (int k = 0; k < LPR; ++k) len[k] = row_len(row0 + sub + RW * k);
   const int64_t base = slice_ptr[slice];
   const int slots = (int)((slice_ptr[slice + 1] - base) / kSellRows);
   // lane = row for the slot's value and column (one coalesced load each);
   // the lanes that gather a row's B slice take them by ds_bpermute
   const int64_t my_r = row0 + lane;
-  const int my_len = my_r < n_rows ? (int)((int64_t)rowptr[my_r + 1] - (int64_t)rowptr[my_r]) : 0;
+  const int my_len = row_len(my_r);
   A acc[LPR][EPL];
 #pragma unroll
   for (int k = 0; k < LPR; ++k)
